@@ -1,0 +1,311 @@
+# SPDX-License-Identifier: Apache-2.0
+"""KDA path benchmark on one MI355X.
+
+Workloads (synthetic inputs resident in HBM before the timed region):
+  prefill  hidden 4096, H=32, D=128, chunk 64, T=8192, batch 1: one step = K1 (conv +
+           SiLU + L2 + decay + beta, bf16 activations in) -> K2 (chunked delta-rule
+           prefill, fp32 state) -> K4 (head RMSNorm + sigmoid gate, bf16 out). The
+           projections are not part of the step (they are plain GEMMs).
+  decode   H=32, D=128, B=64 sequences, one token each: one step = K3 over all 2048
+           (sequence, head) states. The state sets rotate over 4 independent buffers
+           (512 MiB) so that the 256 MB last-level cache cannot hold the working set.
+
+Prints ONE JSON line. `value` is prefill tokens/s; the decode result (state-update GB/s)
+is the `decode` object of the same line. `roofline` is for the dominant prefill kernel;
+`decode.roofline` for K3. Kernel durations come from HIP events recorded on the launch
+stream around every launch inside the timed region. `cpu_baseline` is the CPU oracle
+timed on this host on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "kimi-k3-in-c_amd"))
+
+HBM_PEAK = 8.0e12          # bytes/s, MI355X HBM3E
+BF16_PEAK = 2.5e15         # flop/s, dense bf16 MFMA
+FP32_PEAK = 157.3e12       # flop/s, dense fp32 MFMA
+
+# c2 / c1 shapes
+PRE = dict(hidden=4096, H=32, D=128, T=8192, chunk=64, K=4, gate_lb=-5.0, rms_eps=1e-5)
+DEC = dict(B=64, H=32, D=128)
+
+
+def decode_bytes_per_token(H: int, D: int) -> int:
+    """Algorithmic HBM bytes of one decode token (all heads of one sequence): state read
+    and write 2*H*D*D*4, q k v alpha 4*H*D*4, beta 4*H, o H*D*4."""
+    return 2 * H * D * D * 4 + 4 * H * D * 4 + 4 * H + H * D * 4
+
+
+def prefill_core_flops_per_token(H: int, D: int, C: int) -> float:
+    """Algorithmic flops of the chunked core per token: 2*H*(5*C*D + 3*D*D + C*C/6)."""
+    return 2.0 * H * (5 * C * D + 3 * D * D + C * C / 6.0)
+
+
+def chunk_bytes_per_token(H: int, D: int) -> int:
+    """Algorithmic HBM bytes of K2 per token: q k v g in (fp32) 16*P, beta 4*H, o out 4*P."""
+    P = H * D
+    return 16 * P + 4 * H + 4 * P
+
+
+def cpu_info() -> dict:
+    model, cores = "unknown", os.cpu_count() or 1
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        pass
+    return {"model": model, "threads_available": cores}
+
+
+def ev_pair(torch):
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+# -------------------------------------------------------------------- decode ----
+def bench_decode(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
+    B, H, D = DEC["B"], DEC["H"], DEC["D"]
+    nsets = 4
+    g = torch.Generator(device="cuda").manual_seed(0x4B334441 + 1)
+    sets = []
+    for _ in range(nsets):
+        S = torch.randn((B, H, D, D), device="cuda", generator=g) * 0.1
+        q = torch.nn.functional.normalize(torch.randn((B, H, D), device="cuda", generator=g), dim=-1)
+        k = torch.nn.functional.normalize(torch.randn((B, H, D), device="cuda", generator=g), dim=-1)
+        v = torch.randn((B, H, D), device="cuda", generator=g)
+        alpha = torch.exp(torch.rand((B, H, D), device="cuda", generator=g) * -5.0)
+        beta = torch.rand((B, H), device="cuda", generator=g)
+        o = torch.empty((B, H, D), device="cuda")
+        sets.append((S, o, q.contiguous(), k.contiguous(), v, alpha, beta))
+    qs = 1.0 / math.sqrt(D)
+    for i in range(warmup):
+        k3.kda_decode(*sets[i % nsets], qs)
+    torch.cuda.synchronize()
+    evs = [ev_pair(torch) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        evs[i][0].record()
+        k3.kda_decode(*sets[i % nsets], qs)
+        evs[i][1].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ks = sorted(a.elapsed_time(b) * 1e-3 for a, b in evs)
+    kavg = sum(ks) / len(ks)
+    step_s = wall / steps
+    bytes_step = decode_bytes_per_token(H, D) * B
+    out = {
+        "value": bytes_step / step_s / 1e9, "unit": "GB/s", "tokens_per_s": B / step_s,
+        "ms_per_step": step_s * 1e3, "kernel_ms_avg": kavg * 1e3, "kernel_ms_median": ks[len(ks) // 2] * 1e3,
+        "kernel_ms_min": ks[0] * 1e3, "kernel_ms_max": ks[-1] * 1e3,
+        "config": {"workload": "kda_decode", "batch": B, "heads": H, "head_dim": D,
+                   "state_sets_rotated": nsets, "bytes_per_step": bytes_step},
+        "roofline": {"kernel": "kda_decode_kernel<128,256>", "bound": "hbm",
+                     "achieved": bytes_step / kavg / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                     "frac": bytes_step / kavg / HBM_PEAK, "traffic": None},
+        "tolerance": "rtol 1e-4, atol 1e-4*rms (tests/test_gpu_kernels.py)",
+    }
+    if cpu:
+        out["cpu_baseline"] = cpu_decode(torch, sets[0])
+    return out
+
+
+def cpu_decode(torch, dset) -> dict:
+    import numpy as np
+    sys.path.insert(0, str(REPO / "oracle"))
+    import k3_oracle as ko
+    S, o, q, k, v, alpha, beta = (t.cpu().numpy() for t in dset)
+    B, H, D = q.shape
+    nt = cpu_info()["threads_available"]
+    nt = max(1, min(nt, 16))
+    S = np.ascontiguousarray(S)
+    ko.decode_batch(S, q, k, v, alpha, beta, 1.0 / math.sqrt(D), nt)   # warm
+    n, t0 = 0, time.perf_counter()
+    while True:
+        ko.decode_batch(S, q, k, v, alpha, beta, 1.0 / math.sqrt(D), nt)
+        n += 1
+        el = time.perf_counter() - t0
+        if el > 10.0 or n >= 200:
+            break
+    step = el / n
+    bytes_step = decode_bytes_per_token(H, D) * B
+    return {"value": bytes_step / step / 1e9, "unit": "GB/s", "tokens_per_s": B / step,
+            "cores": nt, "kind": "port", "cpu": cpu_info()["model"],
+            "sample": f"{n} full decode steps (B={B}, H={H}, D={D}) of the C oracle, OpenMP over "
+                      f"(sequence, head) pairs, {el:.1f} s"}
+
+
+# ------------------------------------------------------------------- prefill ----
+def bench_prefill(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
+    c = PRE
+    H, D, T, K = c["H"], c["D"], c["T"], c["K"]
+    P = H * D
+    g = torch.Generator(device="cuda").manual_seed(0x4B334441 + 2)
+    bf = torch.bfloat16
+    q_in = torch.randn((T, P), device="cuda", generator=g).to(bf)
+    k_in = torch.randn((T, P), device="cuda", generator=g).to(bf)
+    v_in = torch.randn((T, P), device="cuda", generator=g).to(bf)
+    z = torch.randn((T, P), device="cuda", generator=g) * 0.02
+    b_logit = torch.randn((T, H), device="cuda", generator=g)
+    gate = torch.randn((T, P), device="cuda", generator=g).to(bf)
+    conv = [torch.randn((P, K), device="cuda", generator=g) * 0.5 for _ in range(3)]
+    A_log = torch.rand((H,), device="cuda", generator=g) * 1.5
+    dt_bias = torch.randn((P,), device="cuda", generator=g)
+    o_norm = 1 + 0.1 * torch.randn((D,), device="cuda", generator=g)
+    f32 = dict(device="cuda", dtype=torch.float32)
+    q, k, v, gg = (torch.empty((T, P), **f32) for _ in range(4))
+    beta = torch.empty((T, H), **f32)
+    o = torch.empty((T, P), **f32)
+    y = torch.empty((T, P), device="cuda", dtype=bf)
+    S = torch.zeros((H, D, D), **f32)
+    conv_state = torch.zeros(3 * P * (K - 1), **f32)
+    qs = 1.0 / math.sqrt(D)
+    use_chunk = True
+    try:
+        ws = torch.empty(max(1, k3.kda_chunk_workspace(T, H, D, 64)), dtype=torch.uint8, device="cuda")
+    except k3.K3HipError:
+        use_chunk = False
+    alpha = torch.empty((T, P), **f32)
+
+    def step(evk=None):
+        S.zero_()
+        conv_state.zero_()
+        k3.kda_prep(q_in, k_in, v_in, z, b_logit, conv[0], conv[1], conv[2], A_log, dt_bias,
+                    conv_state, q, k, v, gg, None if use_chunk else alpha, beta, H, D, K, c["gate_lb"])
+        if evk:
+            evk[0].record()
+        if use_chunk:
+            k3.kda_chunk(q, k, v, gg, beta, S, o, H, D, qs, 64, ws)
+        else:
+            k3.kda_recurrent(q, k, v, alpha, beta, S, o, H, D, qs)
+        if evk:
+            evk[1].record()
+        k3.kda_epilogue(o, gate, o_norm, y, H, D, c["rms_eps"])
+
+    try:
+        step()
+        torch.cuda.synchronize()
+    except k3.K3HipError:
+        use_chunk = False
+        step()
+        torch.cuda.synchronize()
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [ev_pair(torch) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(evs[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ks = sorted(a.elapsed_time(b) * 1e-3 for a, b in evs)
+    kavg = sum(ks) / len(ks)
+    step_s = wall / steps
+    flops_launch = prefill_core_flops_per_token(H, D, 64) * T
+    bytes_launch = chunk_bytes_per_token(H, D) * T
+    kname = "kda_chunk (K2, bf16 MFMA)" if use_chunk else "kda_recurrent_kernel<128> (sequential)"
+    out = {
+        "value": T / step_s, "unit": "tokens/s", "ms_per_step": step_s * 1e3,
+        "k2_ms_avg": kavg * 1e3, "k2_ms_median": ks[len(ks) // 2] * 1e3,
+        "config": {"workload": "kda_prefill_core", "hidden": c["hidden"], "heads": H, "head_dim": D,
+                   "T": T, "chunk": 64, "batch": 1, "conv_k": K, "activations": "bf16",
+                   "state": "fp32", "k2_kernel": kname},
+        "roofline": {"kernel": kname, "bound": "mfma", "achieved": flops_launch / kavg / 1e12,
+                     "peak": BF16_PEAK / 1e12, "unit": "TFLOP/s", "frac": flops_launch / kavg / BF16_PEAK,
+                     "traffic": None, "hbm_achieved_GBs": bytes_launch / kavg / 1e9,
+                     "hbm_frac": bytes_launch / kavg / HBM_PEAK,
+                     "flops_per_launch": flops_launch, "bytes_per_launch": bytes_launch},
+    }
+    if cpu:
+        out["cpu_baseline"] = cpu_prefill(torch, q_in, k_in, v_in, z, b_logit, gate, conv, A_log,
+                                          dt_bias, o_norm)
+    return out
+
+
+def cpu_prefill(torch, q_in, k_in, v_in, z, b_logit, gate, conv, A_log, dt_bias, o_norm) -> dict:
+    """orc_kda_core (conv .. gate, the same steps as the GPU step) on the first Ts tokens."""
+    import numpy as np
+    sys.path.insert(0, str(REPO / "oracle"))
+    import k3_oracle as ko
+    c = PRE
+    H, D, K = c["H"], c["D"], c["K"]
+    nt = max(1, min(cpu_info()["threads_available"], 16))
+    cfg = ko.make_cfg(c["hidden"], H, D, K, c["gate_lb"], c["rms_eps"])
+    arrays = {"q_conv": conv[0].cpu().numpy(), "k_conv": conv[1].cpu().numpy(),
+              "v_conv": conv[2].cpu().numpy(), "A_log": A_log.cpu().numpy(),
+              "dt_bias": dt_bias.cpu().numpy(), "o_norm": o_norm.cpu().numpy()}
+    for n in ("q", "k", "v", "g", "f_a", "f_b", "b", "o"):
+        arrays[n] = np.zeros((1, 1), np.float32)
+    W = ko.Weights(arrays, 0)
+    Ts, runs = 64, []
+    while True:
+        sl = lambda t: t[:Ts].float().cpu().numpy()
+        ins = [sl(q_in), sl(k_in), sl(v_in), sl(z), sl(b_logit), sl(gate)]
+        t0 = time.perf_counter()
+        ko.core(*ins, W, cfg, Ts, None, nt)
+        el = time.perf_counter() - t0
+        runs.append((Ts, el))
+        if el > 3.0 or Ts >= c["T"]:
+            break
+        Ts = min(c["T"], Ts * 4)
+    Ts, el = runs[-1]
+    return {"value": Ts / el, "unit": "tokens/s", "cores": nt, "kind": "port",
+            "cpu": cpu_info()["model"],
+            "sample": f"C oracle orc_kda_core (conv+SiLU, L2, beta, decay, sequential recurrence, "
+                      f"RMSNorm, gate) on the first {Ts} of {c['T']} tokens, H={H}, D={D}, "
+                      f"OpenMP over heads, {el:.2f} s"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", choices=["all", "prefill", "decode"], default="all")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only; run with --gpus 1", file=sys.stderr)
+        return 2
+    import torch
+    import k3kda as k3
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 2
+    k3.lib()
+    res = {}
+    if a.workload in ("all", "decode"):
+        res["decode"] = bench_decode(torch, k3, max(a.steps, 50), a.warmup + 2, not a.no_cpu)
+    if a.workload in ("all", "prefill"):
+        res["prefill"] = bench_prefill(torch, k3, a.steps, a.warmup, not a.no_cpu)
+    head = res.get("prefill") or res["decode"]
+    line = {
+        "metric": "KDA prefill tokens/s (H=32,d=128,T=8k) + decode state-update GB/s, 1 GPU",
+        "value": head["value"], "unit": head["unit"], "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": head["ms_per_step"], "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "data": "synthetic (torch Philox on device, distributions of the benchmark configs)",
+        "config": head["config"], "roofline": head["roofline"],
+        "cpu_baseline": head.get("cpu_baseline"),
+        "device": torch.cuda.get_device_name(0),
+    }
+    if "prefill" in res and "decode" in res:
+        line["decode"] = res["decode"]
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,203 @@
+/* SPDX-License-Identifier: Apache-2.0 */
+/*
+ * k3kda.h - MI355X (gfx950) Kimi Delta Attention path, C ABI.
+ *
+ * Two surfaces live here.
+ *
+ *   1. The drop-in: k3_kda_scratch / k3_kda_layer with the exact signature and meaning of
+ *      the reference engine's CPU entry points (include/k3/k3.h:464-469, defined at
+ *      src/core/k3_ops.c:853-951). Host pointers in, host pointers out, `state` updated in
+ *      place in the reference layout, NULL state = fresh sequence. A fatal condition
+ *      aborts with a message, as the reference does (src/core/k3_ops.c:37-78).
+ *
+ *   2. The device API (k3hip_*): batched, stream-ordered entry points on device pointers
+ *      for the four kernels of the path. They return 0 or a K3HIP_E* code and never abort;
+ *      k3hip_last_error() gives the message for the calling thread.
+ *
+ * K3Cfg and K3KdaW below are LAYOUT MIRRORS of the reference's structs
+ * (include/k3/k3.h:73-120 and :448-462) so that an engine built against its own k3.h can
+ * pass its structs straight through. They are declared only when the reference header has
+ * not been included first (its include guard is K3_H).
+ *
+ * Tensor layouts (P = H*D, head-major, channel-minor, as in the reference):
+ *   activations  [T][P]          token-major rows
+ *   beta         [T][H]
+ *   state S      [H][D][D]       row i = key channel, column j = value channel
+ *   conv state   [3][P][K-1]     q block, k block, v block, oldest input first
+ *   full state   S then conv     H*D*D + 3*P*(K-1) floats (src/cli/k3_state.c:23-29)
+ */
+#ifndef K3KDA_H
+#define K3KDA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#ifndef K3_H
+/* Field-for-field mirror of the reference K3Cfg (include/k3/k3.h:73-120). Only the KDA
+ * fields (hidden, rms_eps, kda_heads, kda_head_dim, conv_k, gate_lb) are read here. */
+typedef struct {
+    int hidden;
+    int n_layers;
+    int vocab;
+    float rms_eps;
+    int kda_heads;
+    int kda_head_dim;
+    int conv_k;
+    float gate_lb;
+    int n_heads;
+    int q_lora;
+    int kv_lora;
+    int qk_nope;
+    int qk_rope;
+    int v_head;
+    int mla_out_gate;
+    int n_experts;
+    int topk;
+    int n_shared;
+    int latent;
+    int moe_inter;
+    float routed_scale;
+    int moe_renorm;
+    int latent_norm;
+    int first_dense;
+    int dense_inter;
+    int attn_res_block;
+    float situ_b1;
+    float situ_b2;
+    int  n_full_attn;
+    int *full_attn;
+} K3Cfg;
+
+/* Weight-storage tags of the reference (include/k3/k3.h:270). */
+enum { K3_WF32 = 0, K3_WBF16 = 1, K3_WI8 = 2 };
+
+/* Field-for-field mirror of the reference K3KdaW (include/k3/k3.h:448-462). Matrices are
+ * tagged by wdt; conv kernels, A_log, dt_bias and o_norm are always fp32. */
+typedef struct {
+    const void  *q, *k, *v;                 /* [P][hidden]                   */
+    const float *q_conv, *k_conv, *v_conv;  /* [P][conv_k]                   */
+    const void  *f_a, *f_b;                 /* [D][hidden], [P][D]           */
+    const float *A_log;                     /* [H]  per head                 */
+    const float *dt_bias;                   /* [P]                           */
+    const void  *b;                         /* [H][hidden]                   */
+    const void  *g;                         /* [P][hidden]                   */
+    const float *o_norm;                    /* [D]                           */
+    const void  *o;                         /* [hidden][P]                   */
+    int          wdt;
+} K3KdaW;
+
+/* Replaces k3_kda_scratch, include/k3/k3.h:464 (src/core/k3_ops.c:853-862). Returns the
+ * same float count, so a caller that sizes scratch from it is unchanged. The GPU path
+ * keeps its intermediates in device memory and does not touch the host scratch. */
+size_t k3_kda_scratch(const K3Cfg *c, int T);
+
+/* Replaces k3_kda_layer, include/k3/k3.h:468-469 (src/core/k3_ops.c:864-951).
+ * out[T][hidden] = KDA(x[T][hidden]); state (nullable) is H*D*D recurrent floats then
+ * 3*P*(conv_k-1) conv floats, read and written in place. Weights are uploaded on every
+ * call: the reference engine re-binds streamed weights through a ring buffer, so a cache
+ * keyed on host pointers would read stale bytes. Use k3hip_kda_upload for resident ones. */
+void   k3_kda_layer(float *out, const float *x, const K3KdaW *w, const K3Cfg *c,
+                    int T, float *state, float *scratch);
+#endif /* K3_H */
+
+/* ------------------------------------------------------------ device API ---- */
+enum {
+    K3HIP_OK          = 0,
+    K3HIP_EINVAL      = 1,   /* a size, pointer or dtype the kernels do not accept  */
+    K3HIP_EHIP        = 2,   /* the HIP runtime reported an error                   */
+    K3HIP_EUNSUPPORTED= 3,   /* a configuration no kernel here is built for         */
+    K3HIP_ENOMEM      = 4    /* device allocation failed                            */
+};
+
+/* Activation storage for k3hip_* inputs/outputs that accept either. */
+enum { K3HIP_F32 = 0, K3HIP_BF16 = 1 };
+
+/* Message for the last non-zero return on the calling thread ("" when none). */
+const char *k3hip_last_error(void);
+
+/* Version string of this build (kernel set and target). */
+const char *k3hip_version(void);
+
+/* Number of HIP devices visible (0 on a machine without one); never aborts. */
+int k3hip_device_count(void);
+
+/* K3: batched single-token recurrence, one (sequence, head) per workgroup.
+ * Replaces, per (b, h), the call k3_kda_step(S, o, q*q_scale, k, v, alpha, beta, D, D)
+ * of src/core/k3_ops.c:930-937 (k3_kda_step is include/k3/k3.h:164, defined at
+ * src/core/k3_ops.c:186-243): decay rows by alpha, u = S^T k, S += k (beta (v-u))^T,
+ * o = S^T q read from the UPDATED state. One read and one write of S.
+ *   S      [B][H][D][D] fp32, in/out         q,k,v,alpha  [B][H][D] fp32
+ *   o      [B][H][D]    fp32, out            beta         [B][H]    fp32
+ * D in {16, 32, 64, 128}. */
+int k3hip_kda_decode(int B, int H, int D, float *S, float *o,
+                     const float *q, const float *k, const float *v,
+                     const float *alpha, const float *beta, float q_scale, void *stream);
+
+/* K1: ShortConv + SiLU on q, k, v, L2-norm on q and k, beta and the decay chain, for one
+ * sequence of T tokens. Replaces steps 2-5 of src/core/k3_ops.c:888-906: k3_shortconv
+ * (:133-165) x3 with the history carried in conv_state, l2norm_ (:845-851, eps 1e-6,
+ * sum of squares), beta = sigmoid(b_logit) (:903), and k3_kda_decay (:168-183).
+ *   q_in,k_in,v_in [T][P] (in_dtype)  z [T][P] fp32 = f_b(f_a(x)) before dt_bias
+ *   b_logit [T][H] fp32               q_conv,k_conv,v_conv [P][K]; A_log [H]; dt_bias [P]
+ *   conv_state [3][P][K-1] in/out, NULL = zero history, not written back
+ *   q_out,k_out,v_out [T][P] fp32     g_out, alpha_out [T][P] fp32 (either may be NULL)
+ *   beta_out [T][H] fp32 */
+int k3hip_kda_prep(int T, int H, int D, int K, float gate_lb, int in_dtype,
+                   const void *q_in, const void *k_in, const void *v_in,
+                   const float *z, const float *b_logit,
+                   const float *q_conv, const float *k_conv, const float *v_conv,
+                   const float *A_log, const float *dt_bias, float *conv_state,
+                   float *q_out, float *k_out, float *v_out,
+                   float *g_out, float *alpha_out, float *beta_out, void *stream);
+
+/* K2: chunked gated delta-rule prefill over T tokens of one sequence, all H heads.
+ * Equal (to the stated tolerance) to T sequential k3_kda_step calls per head
+ * (src/core/k3_ops.c:927-938) from state S, with q scaled by q_scale. Inputs are K1's
+ * outputs: q,k L2-normalised (unscaled), v, g = log-decay, beta.
+ *   q,k,v,g [T][P] fp32   beta [T][H] fp32   S [H][D][D] in/out   o [T][P] fp32
+ * D = 128 or 64, chunk = 64. workspace: NULL = library-managed, else at least
+ * k3hip_kda_chunk_workspace(T,H,D,chunk) bytes of device memory. */
+size_t k3hip_kda_chunk_workspace(int T, int H, int D, int chunk);
+int k3hip_kda_chunk(int T, int H, int D, int chunk,
+                    const float *q, const float *k, const float *v,
+                    const float *g, const float *beta, float q_scale,
+                    float *S, float *o, void *workspace, size_t workspace_bytes,
+                    void *stream);
+
+/* Sequential-in-T prefill on the GPU, parallel over heads and value columns only. The
+ * exact step order of k3_kda_step per token; used for gate bounds outside the chunked
+ * kernel's exponent range (|gate_lb| * 15 > 80) and as a second GPU opinion in tests.
+ * Same arguments and layouts as k3hip_kda_chunk. */
+int k3hip_kda_recurrent(int T, int H, int D,
+                        const float *q, const float *k, const float *v,
+                        const float *alpha, const float *beta, float q_scale,
+                        float *S, float *o, void *stream);
+
+/* K4: per (token, head) RMSNorm over D with the shared weight o_norm[D] (eps inside the
+ * root, double-width mean in the reference, src/core/k3_ops.c:94-102), THEN multiply by
+ * sigmoid(gate). Replaces src/core/k3_ops.c:940-947 up to the o_proj matmul.
+ *   o [T][P] fp32   gate [T][P] (gate_dtype)   o_norm [D]   y [T][P] (y_dtype) */
+int k3hip_kda_epilogue(int T, int H, int D, float rms_eps,
+                       const float *o, const void *gate, int gate_dtype,
+                       const float *o_norm, void *y, int y_dtype, void *stream);
+
+/* Device-resident weights for the full layer. Matrices keep their wdt (fp32 or bf16);
+ * the small fp32 vectors are copied as is. */
+typedef struct k3hip_kda_weights k3hip_kda_weights;
+int k3hip_kda_upload(const K3KdaW *w, const K3Cfg *c, k3hip_kda_weights **out);
+int k3hip_kda_release(k3hip_kda_weights *w);
+
+/* The whole k3_kda_layer on device pointers: projections, K1, K2 (T>1) or K3 (T==1),
+ * K4, o_proj. x,out [T][hidden] fp32; state as in k3_kda_layer (device, nullable). */
+int k3hip_kda_layer_dev(const k3hip_kda_weights *w, int T, float *out, const float *x,
+                        float *state, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* K3KDA_H */

@@ -1,0 +1,101 @@
+// SPDX-License-Identifier: Apache-2.0
+// kda_epilogue.hip - K4: head-wise RMSNorm, then the sigmoid output gate (gfx950).
+//
+// Replaces src/core/k3_ops.c:940-947 up to the o_proj matmul: per (token, head)
+//   y = (o_norm[d] * o[d]) * (float)(1/sqrt(mean(o^2) + eps))     k3_rmsnorm, :94-102
+//   y = y * sigmoid(gate[d])                                        norm FIRST, then gate
+// o_norm[D] is shared by all heads. The mean of squares is a double, as in the reference.
+//
+// Bound by HBM: one wave per (token, head) row, CPL adjacent channels per lane, the sum
+// of squares is a wave reduction in double. Rows are visited grid-stride.
+#include "k3kda_common.h"
+
+namespace k3kda {
+
+template <int D, int GDT, int YDT>
+__global__ __launch_bounds__(256) void kda_epilogue_kernel(long rows, int H, float eps,
+                                                           const float *__restrict__ o,
+                                                           const void *__restrict__ gate,
+                                                           const float *__restrict__ wn,
+                                                           void *__restrict__ y)
+{
+#pragma clang fp contract(off)
+    constexpr int CPL = D >= 64 ? D / 64 : 1;
+    constexpr int NL = D / CPL;
+    const int lane = threadIdx.x & 63;
+    const bool active = lane < NL;
+    const int d0 = (active ? lane : 0) * CPL;
+    float w[CPL];
+#pragma unroll
+    for (int e = 0; e < CPL; e++) w[e] = wn[d0 + e];
+    const long nw = (long)gridDim.x * (blockDim.x >> 6);
+    for (long r = (long)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); r < rows; r += nw) {
+        const size_t base = (size_t)r * D + d0;   // rows are (t, h) in [T][H][D] order
+        float x[CPL];
+        double ss = 0.0;
+#pragma unroll
+        for (int e = 0; e < CPL; e++) {
+            x[e] = o[base + e];
+            if (active) ss += (double)x[e] * (double)x[e];
+        }
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+        const float inv = (float)(1.0 / sqrt(ss / (double)D + (double)eps));
+        if (active) {
+#pragma unroll
+            for (int e = 0; e < CPL; e++) {
+                const float n = (w[e] * x[e]) * inv;
+                const float v = n * sigmoid_ref(load_act<GDT>(gate, base + e));
+                if constexpr (YDT == K3HIP_BF16) reinterpret_cast<uint16_t *>(y)[base + e] = f2bf(v);
+                else reinterpret_cast<float *>(y)[base + e] = v;
+            }
+        }
+    }
+    (void)H;
+}
+
+template <int D, int GDT, int YDT>
+static int launch_epi(long rows, int H, float eps, const float *o, const void *g,
+                      const float *wn, void *y, hipStream_t st)
+{
+    long blocks = (rows + 3) / 4;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL((kda_epilogue_kernel<D, GDT, YDT>), dim3((unsigned)blocks), dim3(256), 0, st,
+                       rows, H, eps, o, g, wn, y);
+    K3_LAUNCHED();
+    return K3HIP_OK;
+}
+
+template <int D>
+static int epi_types(int gdt, int ydt, long rows, int H, float eps, const float *o,
+                     const void *g, const float *wn, void *y, hipStream_t st)
+{
+    if (gdt == K3HIP_F32 && ydt == K3HIP_F32) return launch_epi<D, K3HIP_F32, K3HIP_F32>(rows, H, eps, o, g, wn, y, st);
+    if (gdt == K3HIP_F32 && ydt == K3HIP_BF16) return launch_epi<D, K3HIP_F32, K3HIP_BF16>(rows, H, eps, o, g, wn, y, st);
+    if (gdt == K3HIP_BF16 && ydt == K3HIP_F32) return launch_epi<D, K3HIP_BF16, K3HIP_F32>(rows, H, eps, o, g, wn, y, st);
+    if (gdt == K3HIP_BF16 && ydt == K3HIP_BF16) return launch_epi<D, K3HIP_BF16, K3HIP_BF16>(rows, H, eps, o, g, wn, y, st);
+    K3_FAIL(K3HIP_EINVAL, "k3hip_kda_epilogue: gate_dtype=%d y_dtype=%d", gdt, ydt);
+}
+
+}  // namespace k3kda
+
+using namespace k3kda;
+
+extern "C" int k3hip_kda_epilogue(int T, int H, int D, float rms_eps, const float *o,
+                                  const void *gate, int gate_dtype, const float *o_norm, void *y,
+                                  int y_dtype, void *stream)
+{
+    clear_error();
+    if (T < 0 || H < 0) K3_FAIL(K3HIP_EINVAL, "k3hip_kda_epilogue: T=%d H=%d", T, H);
+    const long rows = (long)T * H;
+    if (rows == 0) return K3HIP_OK;
+    if (!o || !gate || !o_norm || !y) K3_FAIL(K3HIP_EINVAL, "k3hip_kda_epilogue: NULL tensor");
+    hipStream_t st = as_stream(stream);
+    switch (D) {
+    case 16: return epi_types<16>(gate_dtype, y_dtype, rows, H, rms_eps, o, gate, o_norm, y, st);
+    case 32: return epi_types<32>(gate_dtype, y_dtype, rows, H, rms_eps, o, gate, o_norm, y, st);
+    case 64: return epi_types<64>(gate_dtype, y_dtype, rows, H, rms_eps, o, gate, o_norm, y, st);
+    case 128: return epi_types<128>(gate_dtype, y_dtype, rows, H, rms_eps, o, gate, o_norm, y, st);
+    default: K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_epilogue: D=%d not in {16,32,64,128}", D);
+    }
+}

@@ -1,0 +1,29 @@
+// SPDX-License-Identifier: Apache-2.0
+// kda_internal.h - library-internal entry points shared between translation units.
+#pragma once
+
+#include "k3kda_common.h"
+
+namespace k3kda {
+
+// y[T][out] = W[out][in] . x[T][in] with double accumulation; wdt = K3_WF32 | K3_WBF16.
+int proj(int T, int in, int out, const float *x, const void *W, int wdt, float *y, hipStream_t st);
+
+// Stream-ordered scratch: hipMallocAsync on `st`, freed with hipFreeAsync on the same stream.
+struct StreamBuf {
+    void *p = nullptr;
+    hipStream_t st = nullptr;
+    ~StreamBuf()
+    {
+        if (p) (void)hipFreeAsync(p, st);
+    }
+};
+int stream_alloc(StreamBuf &b, size_t bytes, hipStream_t st);
+
+// p[0..n) = 0 on `st` with a kernel (never a memset node).
+int zero_fill(float *p, size_t n, hipStream_t st);
+
+// True once the chunked prefill kernel is built into this library.
+bool chunk_ready();
+
+}  // namespace k3kda

@@ -1,0 +1,262 @@
+// SPDX-License-Identifier: Apache-2.0
+// kda_layer.hip - the C-ABI shim: error state, device-resident weights, the full layer on
+// device pointers, and the drop-in k3_kda_layer / k3_kda_scratch on host pointers.
+//
+// The layer follows the reference k3_kda_layer (src/core/k3_ops.c:864-951) step for step:
+//   1 projections q, k, v, b, f_a -> f_b, g            (:877-886, :946)
+//   2-5 K1: conv+SiLU, L2(q,k), beta, decay             (:888-906)
+//   6 recurrence with q * (1/sqrtf(D)): K3 decode for T == 1, K2 chunked for T > 1
+//     (the sequential GPU recurrence when the gate bound is outside K2's range)
+//   7-8 K4: head RMSNorm then sigmoid gate              (:940-947)
+//   9 o_proj                                            (:948)
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "kda_internal.h"
+
+namespace k3kda {
+
+static thread_local char g_err[1024];
+
+void set_error(const char *fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+}
+
+void clear_error() { g_err[0] = 0; }
+
+// A kernel rather than hipMemsetAsync, so the call stays correct under graph capture.
+__global__ void zero_fill_kernel(float *p, size_t n)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x)
+        p[i] = 0.0f;
+}
+
+int zero_fill(float *p, size_t n, hipStream_t st)
+{
+    if (n == 0) return K3HIP_OK;
+    size_t blocks = (n + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(zero_fill_kernel, dim3((unsigned)blocks), dim3(256), 0, st, p, n);
+    K3_LAUNCHED();
+    return K3HIP_OK;
+}
+
+int stream_alloc(StreamBuf &b, size_t bytes, hipStream_t st)
+{
+    b.st = st;
+    if (bytes == 0) bytes = 256;
+    hipError_t e = hipMallocAsync(&b.p, bytes, st);
+    if (e != hipSuccess) {
+        b.p = nullptr;
+        (void)hipGetLastError();
+        K3_FAIL(K3HIP_ENOMEM, "hipMallocAsync(%zu bytes): %s", bytes, hipGetErrorString(e));
+    }
+    return K3HIP_OK;
+}
+
+}  // namespace k3kda
+
+using namespace k3kda;
+
+struct k3hip_kda_weights {
+    int hidden, H, D, K, wdt;
+    float gate_lb, rms_eps;
+    void *q, *k, *v, *f_a, *f_b, *b, *g, *o;        // matrices, wdt storage
+    float *q_conv, *k_conv, *v_conv, *A_log, *dt_bias, *o_norm;
+};
+
+extern "C" const char *k3hip_last_error(void) { return g_err; }
+
+extern "C" const char *k3hip_version(void)
+{
+    return "k3kda-hip 0.1 gfx950 (K1 prep, K2 chunked prefill, K3 decode, K4 epilogue)";
+}
+
+extern "C" int k3hip_device_count(void)
+{
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    return n;
+}
+
+static int upload(void **dst, const void *src, size_t bytes)
+{
+    *dst = nullptr;
+    if (!src) K3_FAIL(K3HIP_EINVAL, "k3hip_kda_upload: NULL weight");
+    K3_HIP(hipMalloc(dst, bytes ? bytes : 4));
+    K3_HIP(hipMemcpy(*dst, src, bytes, hipMemcpyHostToDevice));
+    return K3HIP_OK;
+}
+
+extern "C" int k3hip_kda_release(k3hip_kda_weights *w)
+{
+    clear_error();
+    if (!w) return K3HIP_OK;
+    void *ptrs[] = {w->q, w->k, w->v, w->f_a, w->f_b, w->b, w->g, w->o,
+                    w->q_conv, w->k_conv, w->v_conv, w->A_log, w->dt_bias, w->o_norm};
+    for (void *p : ptrs)
+        if (p) (void)hipFree(p);
+    free(w);
+    return K3HIP_OK;
+}
+
+extern "C" int k3hip_kda_upload(const K3KdaW *w, const K3Cfg *c, k3hip_kda_weights **out)
+{
+    clear_error();
+    if (!w || !c || !out) K3_FAIL(K3HIP_EINVAL, "k3hip_kda_upload: NULL argument");
+    *out = nullptr;
+    const int E = c->hidden, H = c->kda_heads, D = c->kda_head_dim, K = c->conv_k;
+    if (E <= 0 || H <= 0 || D <= 0 || K <= 0)
+        K3_FAIL(K3HIP_EINVAL, "k3hip_kda_upload: hidden=%d H=%d D=%d conv_k=%d", E, H, D, K);
+    if (w->wdt != K3_WF32 && w->wdt != K3_WBF16)
+        K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_upload: weight tag %d (fp32=0, bf16=1 only)", w->wdt);
+    k3hip_kda_weights *d = (k3hip_kda_weights *)calloc(1, sizeof *d);
+    if (!d) K3_FAIL(K3HIP_ENOMEM, "k3hip_kda_upload: host allocation");
+    d->hidden = E; d->H = H; d->D = D; d->K = K; d->wdt = w->wdt;
+    d->gate_lb = c->gate_lb; d->rms_eps = c->rms_eps;
+    const size_t P = (size_t)H * D, es = w->wdt == K3_WBF16 ? 2 : 4;
+    int rc = K3HIP_OK;
+#define UP(field, src, bytes) if (rc == K3HIP_OK) rc = upload((void **)&d->field, src, bytes)
+    UP(q, w->q, P * E * es);
+    UP(k, w->k, P * E * es);
+    UP(v, w->v, P * E * es);
+    UP(f_a, w->f_a, (size_t)D * E * es);
+    UP(f_b, w->f_b, P * D * es);
+    UP(b, w->b, (size_t)H * E * es);
+    UP(g, w->g, P * E * es);
+    UP(o, w->o, (size_t)E * P * es);
+    UP(q_conv, w->q_conv, P * K * 4);
+    UP(k_conv, w->k_conv, P * K * 4);
+    UP(v_conv, w->v_conv, P * K * 4);
+    UP(A_log, w->A_log, (size_t)H * 4);
+    UP(dt_bias, w->dt_bias, P * 4);
+    UP(o_norm, w->o_norm, (size_t)D * 4);
+#undef UP
+    if (rc != K3HIP_OK) {
+        char keep[1024];
+        snprintf(keep, sizeof keep, "%s", g_err);
+        k3hip_kda_release(d);
+        set_error("%s", keep);
+        return rc;
+    }
+    *out = d;
+    return K3HIP_OK;
+}
+
+// Largest |gate_lb| * 15 the chunked kernel's exponent factoring accepts (e^80 < FLT_MAX
+// and e^-80 is still a normal float); beyond it the sequential GPU recurrence runs.
+static bool chunk_gate_ok(float lb) { return fabsf(lb) * 15.0f <= 80.0f; }
+
+extern "C" int k3hip_kda_layer_dev(const k3hip_kda_weights *w, int T, float *out, const float *x,
+                                   float *state, void *stream)
+{
+    clear_error();
+    if (!w || !out || !x) K3_FAIL(K3HIP_EINVAL, "k3hip_kda_layer_dev: NULL argument");
+    if (T < 0) K3_FAIL(K3HIP_EINVAL, "k3hip_kda_layer_dev: T=%d", T);
+    if (T == 0) return K3HIP_OK;
+    hipStream_t st = as_stream(stream);
+    const int E = w->hidden, H = w->H, D = w->D, K = w->K;
+    const size_t P = (size_t)H * D, TP = (size_t)T * P;
+
+    // device intermediates, stream-ordered: qp kp vp z gl | q k v g alpha o y | bl beta | fa
+    const size_t nf = 12 * TP + 2 * (size_t)T * H + (size_t)T * D + (state ? 0 : (size_t)H * D * D);
+    StreamBuf ws;
+    int rc = stream_alloc(ws, nf * sizeof(float), st);
+    if (rc) return rc;
+    float *f = (float *)ws.p;
+    float *qp = f, *kp = qp + TP, *vp = kp + TP, *z = vp + TP, *gl = z + TP;
+    float *q = gl + TP, *k = q + TP, *v = k + TP, *g = v + TP, *al = g + TP, *o = al + TP;
+    float *y = o + TP, *bl = y + TP, *bt = bl + (size_t)T * H, *fa = bt + (size_t)T * H;
+    float *S = state;
+    if (!S) {
+        S = fa + (size_t)T * D;
+        if ((rc = zero_fill(S, (size_t)H * D * D, st))) return rc;
+    }
+    float *cs = state ? state + (size_t)H * D * D : nullptr;
+
+    if ((rc = proj(T, E, (int)P, x, w->q, w->wdt, qp, st))) return rc;
+    if ((rc = proj(T, E, (int)P, x, w->k, w->wdt, kp, st))) return rc;
+    if ((rc = proj(T, E, (int)P, x, w->v, w->wdt, vp, st))) return rc;
+    if ((rc = proj(T, E, H, x, w->b, w->wdt, bl, st))) return rc;
+    if ((rc = proj(T, E, D, x, w->f_a, w->wdt, fa, st))) return rc;
+    if ((rc = proj(T, D, (int)P, fa, w->f_b, w->wdt, z, st))) return rc;
+    if ((rc = proj(T, E, (int)P, x, w->g, w->wdt, gl, st))) return rc;
+
+    if ((rc = k3hip_kda_prep(T, H, D, K, w->gate_lb, K3HIP_F32, qp, kp, vp, z, bl, w->q_conv,
+                             w->k_conv, w->v_conv, w->A_log, w->dt_bias, cs, q, k, v, g, al, bt,
+                             stream)))
+        return rc;
+    const float qscale = 1.0f / sqrtf((float)D);
+    if (T == 1)
+        rc = k3hip_kda_decode(1, H, D, S, o, q, k, v, al, bt, qscale, stream);
+    else if (chunk_ready() && chunk_gate_ok(w->gate_lb) && (D == 64 || D == 128))
+        rc = k3hip_kda_chunk(T, H, D, 64, q, k, v, g, bt, qscale, S, o, nullptr, 0, stream);
+    else
+        rc = k3hip_kda_recurrent(T, H, D, q, k, v, al, bt, qscale, S, o, stream);
+    if (rc) return rc;
+    if ((rc = k3hip_kda_epilogue(T, H, D, w->rms_eps, o, gl, K3HIP_F32, w->o_norm, y, K3HIP_F32,
+                                 stream)))
+        return rc;
+    return proj(T, (int)P, E, y, w->o, w->wdt, out, st);
+}
+
+// ------------------------------------------------------------------ drop-in ----
+static void fatal(const char *where)
+{
+    fprintf(stderr,
+            "k3kda: FATAL in %s: %s\n"
+            "    Aborting rather than returning an unwritten output buffer.\n",
+            where, g_err[0] ? g_err : "(no message)");
+    abort();
+}
+
+extern "C" size_t k3_kda_scratch(const K3Cfg *c, int T)
+{
+    const size_t P = (size_t)c->kda_heads * c->kda_head_dim;
+    return 6 * (size_t)T * P + (size_t)T * c->kda_heads + 2 * P + (size_t)c->kda_head_dim;
+}
+
+extern "C" void k3_kda_layer(float *out, const float *x, const K3KdaW *w, const K3Cfg *c, int T,
+                             float *state, float *scratch)
+{
+    (void)scratch;
+    if (T <= 0) return;
+    const int E = c->hidden, H = c->kda_heads, D = c->kda_head_dim, K = c->conv_k;
+    const size_t P = (size_t)H * D;
+    const size_t nstate = P * D + 3 * P * (size_t)(K - 1);
+    k3hip_kda_weights *dw = nullptr;
+    if (k3hip_kda_upload(w, c, &dw)) fatal("k3_kda_layer (weight upload)");
+    float *dx = nullptr, *dout = nullptr, *dst = nullptr;
+    const size_t xb = (size_t)T * E * sizeof(float);
+    if (hipMalloc((void **)&dx, xb) != hipSuccess || hipMalloc((void **)&dout, xb) != hipSuccess ||
+        (state && hipMalloc((void **)&dst, nstate * sizeof(float)) != hipSuccess)) {
+        set_error("hipMalloc of %zu activation bytes failed", 2 * xb + nstate * 4);
+        fatal("k3_kda_layer");
+    }
+    if (hipMemcpy(dx, x, xb, hipMemcpyHostToDevice) != hipSuccess ||
+        (state && hipMemcpy(dst, state, nstate * 4, hipMemcpyHostToDevice) != hipSuccess)) {
+        set_error("host-to-device copy failed");
+        fatal("k3_kda_layer");
+    }
+    if (k3hip_kda_layer_dev(dw, T, dout, dx, dst, nullptr)) fatal("k3_kda_layer");
+    if (hipMemcpy(out, dout, xb, hipMemcpyDeviceToHost) != hipSuccess ||
+        (state && hipMemcpy(state, dst, nstate * 4, hipMemcpyDeviceToHost) != hipSuccess)) {
+        set_error("device-to-host copy failed: %s", hipGetErrorString(hipGetLastError()));
+        fatal("k3_kda_layer");
+    }
+    (void)hipFree(dx);
+    (void)hipFree(dout);
+    if (dst) (void)hipFree(dst);
+    k3hip_kda_release(dw);
+}
