@@ -268,12 +268,32 @@ def cpu_prefill(torch, q_in, k_in, v_in, z, b_logit, gate, conv, A_log, dt_bias,
                       f"OpenMP over heads, {el:.2f} s"}
 
 
+def bench_copy(torch, steps: int) -> dict:
+    """A plain device-to-device copy of 1 GiB: the calibration kernel for the HBM traffic
+    counters (FETCH_SIZE / WRITE_SIZE read per byte actually moved)."""
+    n = 1 << 28
+    src = torch.empty(n, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = ev_pair(torch)
+    e0.record()
+    for _ in range(steps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    s = e0.elapsed_time(e1) * 1e-3 / steps
+    return {"bytes_per_copy": 4 * n, "read_bytes": 4 * n, "write_bytes": 4 * n,
+            "ms": s * 1e3, "GBs_rw": 8 * n / s / 1e9}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["all", "prefill", "decode"], default="all")
+    ap.add_argument("--workload", choices=["all", "prefill", "decode", "copy"], default="all",
+                    help="copy: the 1 GiB device copy used to calibrate HBM traffic counters")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -285,6 +305,9 @@ def main() -> int:
         print("bench.py: no GPU visible", file=sys.stderr)
         return 2
     k3.lib()
+    if a.workload == "copy":
+        print(json.dumps({"workload": "copy_calibration", **bench_copy(torch, a.steps)}))
+        return 0
     res = {}
     if a.workload in ("all", "decode"):
         res["decode"] = bench_decode(torch, k3, max(a.steps, 50), a.warmup + 2, not a.no_cpu)

@@ -19,17 +19,22 @@
 // MFMA operands needs a pivot. Row block a (16 rows) uses the pivot p = 16a: the row
 // factor e^(G_t - G_p) <= 1, the column factor e^(G_p - G_s) is <= 1 for s < p and at
 // most e^(15 |gate_lb|) inside the block. The host only takes this path when
-// 15 |gate_lb| <= 80, so every factor is a normal fp32 / bf16 number.
+// 15 |gate_lb| <= 80, so every factor is a normal fp32 / bf16 number. Exponentials are
+// v_exp_f32 (2^x) on G pre-multiplied by log2(e).
 //
 // Precision. Every product whose operands are not exact bf16 is a split-bf16 product:
 // x = hi + lo (both bf16), a.b ~ ah.bh + ah.bl + al.bh with fp32 accumulation, i.e. about
 // 2^-17 relative per product. The 16x16 block products of the inverse use the fp32 MFMA.
 //
-// Phase 1 (kda_chunk_intra) is parallel over (chunk, head): everything that does not
-// depend on the state. Phase 2 (kda_chunk_state) walks the chunks in order, one workgroup
-// per (head, 16-column tile of S): value columns of S are independent of each other, so
-// the tiles never exchange data. Its blocks are mapped so that all tiles of one head sit
-// on one XCD and share that XCD's L2 copy of the phase-1 operands.
+// Phase 1 (kda_chunk_intra) is parallel over (chunk, head) and does everything that does
+// not depend on the state. It leaves its results in a workspace already split into hi/lo
+// bf16 and laid out in MFMA fragment order, so the sequential phase loads each operand
+// with one 16-byte access per lane and no conversion work.
+// Phase 2 (kda_chunk_state) walks the chunks in order, one workgroup per (head, 16-column
+// tile of S): value columns of S are independent of each other, so the tiles never
+// exchange data. It prefetches chunk c+1's operands into registers while it computes
+// chunk c. Its blocks are mapped so that all tiles of one head sit on one XCD and share
+// that XCD's L2 copy of the phase-1 operands.
 #include "kda_internal.h"
 
 namespace k3kda {
@@ -37,19 +42,24 @@ namespace k3kda {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int CH = 64;     // chunk length
-constexpr int SB = 16;     // sub-block (MFMA tile) edge
-constexpr int NT2 = 16;    // columns of S per phase-2 workgroup
+constexpr int CH = 64;          // chunk length
+constexpr int SB = 16;          // sub-block (MFMA tile) edge
+constexpr int P1_THREADS = 512; // phase-1 workgroup
+constexpr float LOG2E = 1.4426950408889634f;
 
-// Per-(chunk, head) workspace block, in floats.
-template <int D> struct WsLayout {
-    static constexpr size_t W = 0;                   // [64][D]   Tm beta K e^G
-    static constexpr size_t U = W + (size_t)CH * D;  // [64][D]   Tm beta V
-    static constexpr size_t Q = U + (size_t)CH * D;  // [64][D]   q e^G (q scaled)
-    static constexpr size_t KT = Q + (size_t)CH * D; // [D][64]   (k e^(G_last - G))^T
-    static constexpr size_t A = KT + (size_t)CH * D; // [64][64]  A_qk, zero above the diagonal
-    static constexpr size_t GL = A + (size_t)CH * CH;// [D]       e^G_last
-    static constexpr size_t SIZE = GL + D;
+// Per-(chunk, head) workspace block, in BYTES. A fragment block (16 rows x 32 K) is 64
+// lanes x 8 bf16 hi followed by 64 lanes x 8 bf16 lo (2 KiB). A C block (16 x 16 fp32) is
+// 64 lanes x 4 floats (1 KiB).
+template <int D> struct Ws {
+    static constexpr int KSI = D / 32;                          // K-steps over channels
+    static constexpr int NCT = D / 16;                          // 16-column tiles
+    static constexpr size_t WF = 0;                             // W    A-frags [4][KSI]
+    static constexpr size_t QF = WF + (size_t)4 * KSI * 2048;   // Q e^G A-frags [4][KSI]
+    static constexpr size_t AF = QF + (size_t)4 * KSI * 2048;   // A_qk A-frags [4][2]
+    static constexpr size_t KF = AF + (size_t)4 * 2 * 2048;     // (K e^(GL-G))^T A-frags [D/16][2]
+    static constexpr size_t UC = KF + (size_t)NCT * 2 * 2048;   // U C blocks [4][NCT]
+    static constexpr size_t GL = UC + (size_t)4 * NCT * 1024;   // e^G_last [D] fp32
+    static constexpr size_t SIZE = GL + (size_t)D * 4;
 };
 
 __device__ __forceinline__ void split8(const float (&x)[8], bf16x8 &hi, bf16x8 &lo)
@@ -80,15 +90,47 @@ __device__ __forceinline__ void load8(float (&x)[8], const float *p)
     x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
 }
 
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// 8 consecutive floats of a 16-byte aligned LDS row as two 128-bit reads.
+__device__ __forceinline__ void lds8(float (&x)[8], const float *p)
+{
+    const f4 a = *reinterpret_cast<const f4 *>(p);
+    const f4 b = *reinterpret_cast<const f4 *>(p + 4);
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+    x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+}
+
+// Split x and store it as lane `lane` of the fragment block at `blk`.
+__device__ __forceinline__ void store_frag(char *blk, int lane, const float (&x)[8])
+{
+    bf16x8 hi, lo;
+    split8(x, hi, lo);
+    *reinterpret_cast<bf16x8 *>(blk + lane * 16) = hi;
+    *reinterpret_cast<bf16x8 *>(blk + 1024 + lane * 16) = lo;
+}
+
+struct Frag {
+    bf16x8 hi, lo;
+};
+
+__device__ __forceinline__ Frag load_frag(const char *blk, int lane)
+{
+    Frag f;
+    f.hi = *reinterpret_cast<const bf16x8 *>(blk + lane * 16);
+    f.lo = *reinterpret_cast<const bf16x8 *>(blk + 1024 + lane * 16);
+    return f;
+}
+
 // --------------------------------------------------------------- phase 1 ----
-// LDS: G, K, V [64][D+4]; A, Tm [64][68]; beta [64]; Y [4][16][17].
+// LDS (floats): G*log2e, K, X (staging) [64][D+4]; A, Tm [64][68]; beta [64]; Y [4][16][17].
 template <int D> struct P1Lds {
     static constexpr int PD = D + 4;
     static constexpr int PA = CH + 4;
     static constexpr size_t G = 0;
     static constexpr size_t K = G + (size_t)CH * PD;
-    static constexpr size_t V = K + (size_t)CH * PD;
-    static constexpr size_t A = V + (size_t)CH * PD;
+    static constexpr size_t X = K + (size_t)CH * PD;
+    static constexpr size_t A = X + (size_t)CH * PD;
     static constexpr size_t TM = A + (size_t)CH * PA;
     static constexpr size_t B = TM + (size_t)CH * PA;
     static constexpr size_t Y = B + CH;
@@ -96,98 +138,112 @@ template <int D> struct P1Lds {
 };
 
 template <int D>
-__global__ __launch_bounds__(256) void kda_chunk_intra(int T, int H, float qs,
-                                                       const float *__restrict__ q,
-                                                       const float *__restrict__ k,
-                                                       const float *__restrict__ v,
-                                                       const float *__restrict__ g,
-                                                       const float *__restrict__ beta,
-                                                       float *__restrict__ ws)
+__global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra(int T, int H, float qs,
+                                                              const float *__restrict__ q,
+                                                              const float *__restrict__ k,
+                                                              const float *__restrict__ v,
+                                                              const float *__restrict__ g,
+                                                              const float *__restrict__ beta,
+                                                              char *__restrict__ ws)
 {
     using L = P1Lds<D>;
-    using WL = WsLayout<D>;
-    constexpr int PD = L::PD, PA = L::PA;
-    constexpr int KSI = D / 32;   // K-steps over channels
-    extern __shared__ float lds[];
-    float *sG = lds + L::G, *sK = lds + L::K, *sV = lds + L::V;
+    using WL = Ws<D>;
+    constexpr int PD = L::PD, PA = L::PA, KSI = WL::KSI, NCT = WL::NCT;
+    constexpr int NW = P1_THREADS / 64;
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    float *sG = lds + L::G, *sK = lds + L::K, *sX = lds + L::X;
     float *sA = lds + L::A, *sT = lds + L::TM, *sB = lds + L::B, *sY = lds + L::Y;
 
     const int c = blockIdx.x, h = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int m = lane & 15, kg = lane >> 4;
     const int t0 = c * CH;
     const int Tc = min(CH, T - t0);
     const size_t P = (size_t)H * D;
-    float *blk = ws + ((size_t)c * H + h) * WL::SIZE;
+    char *blk = ws + ((size_t)c * H + h) * WL::SIZE;
 
-    // (1) stage g, k, v (zero past the end of the sequence), beta; clear A and Tm
-    for (int e = tid; e < CH * D / 4; e += 256) {
+    // (1) every global read of the kernel is issued here, up front: v for this wave's
+    //     column tile of U into registers; g, k and q staged in LDS (zero past the end of
+    //     the sequence); beta. A is cleared.
+    float vreg[2][8];
+    {
+        const int n0 = SB * w;
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int s = 32 * ks + 8 * kg + e;
+                vreg[ks][e] = (w < NCT && s < Tc) ? v[(size_t)(t0 + s) * P + (size_t)h * D + n0 + m] : 0.0f;
+            }
+    }
+    for (int e = tid; e < CH * D / 4; e += P1_THREADS) {
         const int t = e / (D / 4), i4 = (e % (D / 4)) * 4;
-        f4 gv = 0.0f, kv = 0.0f, vv = 0.0f;
+        f4 gv = 0.0f, kv = 0.0f, qv = 0.0f;
         if (t < Tc) {
             const size_t at = (size_t)(t0 + t) * P + (size_t)h * D + i4;
             gv = *reinterpret_cast<const f4 *>(g + at);
             kv = *reinterpret_cast<const f4 *>(k + at);
-            vv = *reinterpret_cast<const f4 *>(v + at);
+            qv = *reinterpret_cast<const f4 *>(q + at);
         }
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            sG[t * PD + i4 + u] = gv[u];
-            sK[t * PD + i4 + u] = kv[u];
-            sV[t * PD + i4 + u] = vv[u];
-        }
+        *reinterpret_cast<f4 *>(&sG[t * PD + i4]) = gv;
+        *reinterpret_cast<f4 *>(&sK[t * PD + i4]) = kv;
+        *reinterpret_cast<f4 *>(&sX[t * PD + i4]) = qv * qs;
     }
-    for (int e = tid; e < CH * PA; e += 256) {
-        sA[e] = 0.0f;
-        sT[e] = 0.0f;
-    }
+    for (int e = tid; e < CH * PA; e += P1_THREADS) sA[e] = 0.0f;
     if (tid < CH) sB[tid] = tid < Tc ? beta[(size_t)(t0 + tid) * H + h] : 0.0f;
     __syncthreads();
 
-    // (2) G = cumulative sum of g down the chunk, per channel (padded rows add 0)
-    if (tid < D) {
-        float run = 0.0f;
-#pragma unroll 16
-        for (int t = 0; t < CH; t++) {
-            run += sG[t * PD + tid];
-            sG[t * PD + tid] = run;
-        }
+    // (2) G = cumulative sum of g down the chunk (padded rows add 0), kept as G*log2(e):
+    //     each channel's 64 rows are four 16-row segments scanned in registers, then each
+    //     segment adds the totals of the segments before it.
+    constexpr int SEGS = P1_THREADS / D;   // 4 for D = 128, 8 for D = 64
+    constexpr int SEGR = CH / SEGS;
+    float *sTot = sY;                      // [SEGS][D] segment totals (sY is free here)
+    {
+        const int i = tid % D, sg = tid / D;
+        float x[SEGR];
+#pragma unroll
+        for (int r = 0; r < SEGR; r++) x[r] = sG[(sg * SEGR + r) * PD + i];
+#pragma unroll
+        for (int r = 1; r < SEGR; r++) x[r] += x[r - 1];
+        sTot[sg * D + i] = x[SEGR - 1];
+        __syncthreads();
+        float off = 0.0f;
+        for (int p2 = 0; p2 < sg; p2++) off += sTot[p2 * D + i];
+#pragma unroll
+        for (int r = 0; r < SEGR; r++) sG[(sg * SEGR + r) * PD + i] = (x[r] + off) * LOG2E;
     }
     __syncthreads();
 
-    const int m = lane & 15, kg = lane >> 4;
-
-    // (3) A_kk (to LDS, times beta_t, strictly lower) and A_qk (to the workspace, lower with
-    //     the diagonal) for every 16x16 block (a, b), b <= a; blocks above are zero.
-    for (int job = w; job < 16; job += 4) {
+    // (3) A_kk (times beta_t, strictly lower) into sA; A_qk (lower with the diagonal) staged
+    //     in sT. Each 16x16 block (a, b); blocks above the diagonal are zero.
+    for (int job = w; job < 16; job += NW) {
         const int a = job >> 2, b = job & 3;
-        float *gA = blk + WL::A;
-        if (b > a) {   // zero block of A_qk
+        if (b > a) {
 #pragma unroll
-            for (int e = 0; e < 4; e++)
-                gA[(size_t)(SB * a + 4 * kg + e) * CH + SB * b + m] = 0.0f;
+            for (int e = 0; e < 4; e++) sT[(SB * a + 4 * kg + e) * PA + SB * b + m] = 0.0f;
             continue;
         }
         const int p = SB * a;        // pivot row
         const int t = SB * a + m;    // A-operand row (token t)
         const int s = SB * b + m;    // B-operand row (token s)
         f32x4 akk = 0.0f, aqk = 0.0f;
-        const size_t qrow = (size_t)(t0 + t) * P + (size_t)h * D;
 #pragma unroll
         for (int ks = 0; ks < KSI; ks++) {
             const int i0 = 32 * ks + 8 * kg;
-            float lk[8], lq[8], r[8], qv[8];
-            if (t < Tc) load8(qv, q + qrow + i0);
-            else {
-#pragma unroll
-                for (int e = 0; e < 8; e++) qv[e] = 0.0f;
-            }
+            float lk[8], lq[8], r[8], gp[8], gt[8], gs[8];
+            lds8(gp, &sG[p * PD + i0]);
+            lds8(gt, &sG[t * PD + i0]);
+            lds8(gs, &sG[s * PD + i0]);
+            lds8(lk, &sK[t * PD + i0]);
+            lds8(lq, &sX[t * PD + i0]);
+            lds8(r, &sK[s * PD + i0]);
 #pragma unroll
             for (int e = 0; e < 8; e++) {
-                const float gp = sG[p * PD + i0 + e];
-                const float ft = expf(sG[t * PD + i0 + e] - gp);
-                lk[e] = sK[t * PD + i0 + e] * ft;
-                lq[e] = (qv[e] * qs) * ft;
-                r[e] = sK[s * PD + i0 + e] * expf(gp - sG[s * PD + i0 + e]);
+                const float ft = exp2_fast(gt[e] - gp[e]);
+                lk[e] = lk[e] * ft;
+                lq[e] = lq[e] * ft;
+                r[e] = r[e] * exp2_fast(gp[e] - gs[e]);
             }
             bf16x8 kh, kl, qh, ql, rh, rl;
             split8(lk, kh, kl);
@@ -196,19 +252,40 @@ __global__ __launch_bounds__(256) void kda_chunk_intra(int T, int H, float qs,
             akk = mma3(akk, kh, kl, rh, rl);
             aqk = mma3(aqk, qh, ql, rh, rl);
         }
-        float *gAq = blk + WL::A;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const int tt = SB * a + 4 * kg + e, ss = SB * b + m;
             sA[tt * PA + ss] = ss < tt ? akk[e] * sB[tt] : 0.0f;
-            gAq[(size_t)tt * CH + ss] = ss <= tt ? aqk[e] : 0.0f;
+            sT[tt * PA + ss] = ss <= tt ? aqk[e] : 0.0f;
         }
     }
     __syncthreads();
 
-    // (4a) diagonal blocks of Tm = (I + A)^-1: wave w inverts block w by forward
+    // (3b) A_qk as A-fragments [rt 4][ks 2], one fragment lane per thread; q e^G (q scaled)
+    //      as A-fragments [rt 4][KSI] from the staged q.
+    {
+        const int fb = tid >> 6, rt = fb >> 1, ks = fb & 1;
+        float x[8];
+        lds8(x, &sT[(SB * rt + m) * PA + 32 * ks + 8 * kg]);
+        store_frag(blk + WL::AF + (size_t)fb * 2048, lane, x);
+    }
+    for (int f = tid; f < 4 * KSI * 64; f += P1_THREADS) {
+        const int fb = f >> 6, rt = fb / KSI, ks = fb % KSI;
+        const int t = SB * rt + m, i0 = 32 * ks + 8 * kg;
+        float x[8], gx[8];
+        lds8(x, &sX[t * PD + i0]);
+        lds8(gx, &sG[t * PD + i0]);
+#pragma unroll
+        for (int e = 0; e < 8; e++) x[e] = x[e] * exp2_fast(gx[e]);
+        store_frag(blk + WL::QF + (size_t)fb * 2048, lane, x);
+    }
+    __syncthreads();
+    for (int e = tid; e < CH * PA; e += P1_THREADS) sT[e] = 0.0f;
+    __syncthreads();
+
+    // (4a) diagonal blocks of Tm = (I + A)^-1: wave w < 4 inverts block w by forward
     //      substitution; lane s < 16 owns column s and keeps it in registers.
-    if (lane < SB) {
+    if (w < 4 && lane < SB) {
         const int s = lane, o = SB * w;
         float col[SB];
 #pragma unroll
@@ -228,11 +305,11 @@ __global__ __launch_bounds__(256) void kda_chunk_intra(int T, int H, float qs,
     __syncthreads();
 
     // (4b) off-diagonal blocks, by distance d = a - b:
-    //      Tm_ab = -Tm_aa * sum_{c=b}^{a-1} A_ac Tm_cb   (fp32 MFMA, exact-width products)
+    //      Tm_ab = -Tm_aa * sum_{c=b}^{a-1} A_ac Tm_cb   (fp32 MFMA)
     for (int d = 1; d < 4; d++) {
         const bool act = w < 4 - d;
         const int a = w + d, b = w;
-        float *Yw = sY + w * 16 * 17;
+        float *Yw = sY + (w & 3) * 16 * 17;
         if (act) {
             f32x4 y = 0.0f;
             for (int cc = b; cc < a; cc++)
@@ -260,8 +337,10 @@ __global__ __launch_bounds__(256) void kda_chunk_intra(int T, int H, float qs,
         __syncthreads();
     }
 
-    // (5) W = Tm (beta K e^G), U = Tm (beta V); wave w takes column tiles w, w+4, ...
-    for (int nt = w; nt < D / SB; nt += 4) {
+    // (5) W = Tm (beta K e^G) staged in sX, U = Tm (beta V) written as C blocks;
+    //     wave w takes column tiles w, w+NW, ...
+    static_assert(NCT <= NW, "one column tile per wave (v is prefetched for tile w)");
+    for (int nt = w; nt < NCT; nt += NW) {
         const int n0 = SB * nt;
         f32x4 aw[4], au[4];
 #pragma unroll
@@ -273,8 +352,8 @@ __global__ __launch_bounds__(256) void kda_chunk_intra(int T, int H, float qs,
             for (int e = 0; e < 8; e++) {
                 const int s = 32 * ks + 8 * kg + e;
                 const float bs = sB[s];
-                xk[e] = (bs * sK[s * PD + n0 + m]) * expf(sG[s * PD + n0 + m]);
-                xv[e] = bs * sV[s * PD + n0 + m];
+                xk[e] = (bs * sK[s * PD + n0 + m]) * exp2_fast(sG[s * PD + n0 + m]);
+                xv[e] = bs * vreg[ks][e];
             }
             bf16x8 kh, kl, vh, vl;
             split8(xk, kh, kl);
@@ -283,8 +362,7 @@ __global__ __launch_bounds__(256) void kda_chunk_intra(int T, int H, float qs,
             for (int a = 0; a < 4; a++) {
                 if (a < 2 * ks) continue;   // Tm rows of block a vanish past column 16a+15
                 float tv[8];
-#pragma unroll
-                for (int e = 0; e < 8; e++) tv[e] = sT[(SB * a + m) * PA + 32 * ks + 8 * kg + e];
+                lds8(tv, &sT[(SB * a + m) * PA + 32 * ks + 8 * kg]);
                 bf16x8 th, tl;
                 split8(tv, th, tl);
                 aw[a] = mma3(aw[a], th, tl, kh, kl);
@@ -292,139 +370,239 @@ __global__ __launch_bounds__(256) void kda_chunk_intra(int T, int H, float qs,
             }
         }
 #pragma unroll
-        for (int a = 0; a < 4; a++)
+        for (int a = 0; a < 4; a++) {
+            *reinterpret_cast<f32x4 *>(blk + WL::UC + ((size_t)(a * NCT + nt) * 64 + lane) * 16) = au[a];
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int t = SB * a + 4 * kg + e;
-                blk[WL::W + (size_t)t * D + n0 + m] = aw[a][e];
-                blk[WL::U + (size_t)t * D + n0 + m] = au[a][e];
-            }
+            for (int e = 0; e < 4; e++) sX[(SB * a + 4 * kg + e) * PD + n0 + m] = aw[a][e];
+        }
+    }
+    __syncthreads();
+
+    // (5b) W as A-fragments [rt 4][KSI]
+    for (int f = tid; f < 4 * KSI * 64; f += P1_THREADS) {
+        const int fb = f >> 6, rt = fb / KSI, ks = fb % KSI;
+        float x[8];
+        lds8(x, &sX[(SB * rt + m) * PD + 32 * ks + 8 * kg]);
+        store_frag(blk + WL::WF + (size_t)fb * 2048, lane, x);
     }
 
-    // (6) elementwise operands: q e^G (scaled), (k e^(G_last - G))^T, e^G_last
-    for (int e = tid; e < CH * D; e += 256) {
-        const int t = e / D, i = e % D;
-        float val = 0.0f;
-        if (t < Tc) val = (q[(size_t)(t0 + t) * P + (size_t)h * D + i] * qs) * expf(sG[t * PD + i]);
-        blk[WL::Q + e] = val;
+    // (6) (k e^(G_last - G))^T as A-fragments [D/16][2]; e^G_last.
+    for (int f = tid; f < NCT * 2 * 64; f += P1_THREADS) {
+        const int fb = f >> 6, rt = fb >> 1, ks = fb & 1;
+        const int i = SB * rt + m;
+        const float gl = sG[(CH - 1) * PD + i];
+        float x[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int s = 32 * ks + 8 * kg + e;
+            x[e] = sK[s * PD + i] * exp2_fast(gl - sG[s * PD + i]);
+        }
+        store_frag(blk + WL::KF + (size_t)fb * 2048, lane, x);
     }
-    for (int e = tid; e < CH * D; e += 256) {
-        const int i = e / CH, s = e % CH;
-        blk[WL::KT + e] = sK[s * PD + i] * expf(sG[(CH - 1) * PD + i] - sG[s * PD + i]);
-    }
-    if (tid < D) blk[WL::GL + tid] = expf(sG[(CH - 1) * PD + tid]);
+    if (tid < D) reinterpret_cast<float *>(blk + WL::GL)[tid] = exp2_fast(sG[(CH - 1) * PD + tid]);
 }
 
 // --------------------------------------------------------------- phase 2 ----
+// Eight waves per workgroup, in two roles, for one head and 16 columns j0..j0+15 of S:
+//   row waves   (w = 0..3)  own token rows 16w..16w+15 of the chunk:
+//                           Vn = U - W S and Q S, then O = Q S + A_qk Vn
+//   state waves (w = 4..7)  own state rows 32(w-4)..32(w-4)+31 (two 16-row tiles):
+//                           S = diag(e^G_last) S + (K e^(G_last - G))^T Vn
+// Per chunk: state waves publish S to LDS -> barrier -> row waves publish Vn -> barrier
+// -> row waves finish O while state waves update S. Each role prefetches the next chunk's
+// operands into a second register set (used alternately, no copies).
+template <int D> struct RowOps {
+    static constexpr int KSI = D / 32;
+    Frag wf[KSI], qf[KSI], af[2];
+    f32x4 u;
+};
+template <int D> struct StateOps {
+    static constexpr int RTW = D / 64;   // 16-row tiles per state wave
+    Frag kf[RTW][2];
+    f32x4 gl[RTW];
+};
+
 template <int D>
-__global__ __launch_bounds__(256) void kda_chunk_state(int T, int H, const float *__restrict__ ws,
+__device__ __forceinline__ void load_row_ops(RowOps<D> &op, const char *blk, int w, int lane, int ct)
+{
+    using WL = Ws<D>;
+    constexpr int KSI = WL::KSI;
+#pragma unroll
+    for (int ks = 0; ks < KSI; ks++) {
+        op.wf[ks] = load_frag(blk + WL::WF + (size_t)(w * KSI + ks) * 2048, lane);
+        op.qf[ks] = load_frag(blk + WL::QF + (size_t)(w * KSI + ks) * 2048, lane);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++)   // af[1] of waves 0-1 is all zero and unused
+        op.af[ks] = load_frag(blk + WL::AF + (size_t)(w * 2 + ks) * 2048, lane);
+    op.u = *reinterpret_cast<const f32x4 *>(blk + WL::UC + ((size_t)(w * WL::NCT + ct) * 64 + lane) * 16);
+}
+
+// sw = state-wave index 0..3; its tiles are rows 16*(RTW*sw + r) .. +15
+template <int D>
+__device__ __forceinline__ void load_state_ops(StateOps<D> &op, const char *blk, int sw, int lane)
+{
+    using WL = Ws<D>;
+    constexpr int RTW = D / 64;
+    const int kg = lane >> 4;
+#pragma unroll
+    for (int r = 0; r < RTW; r++) {
+        const int rt = RTW * sw + r;
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) op.kf[r][ks] = load_frag(blk + WL::KF + (size_t)(rt * 2 + ks) * 2048, lane);
+        op.gl[r] = *reinterpret_cast<const f32x4 *>(blk + WL::GL + (size_t)(16 * rt + 4 * kg) * 4);
+    }
+}
+
+constexpr int PS2 = 18;   // LDS pitch of the S and Vn tiles: conflict-free B-operand reads
+
+// B-operand fragment (rows 32ks + 8kg .. +7, column m) of a [rows][PS2] LDS tile, split.
+__device__ __forceinline__ void b_frag(const float *t, int ks, int kg, int m, bf16x8 &hi, bf16x8 &lo)
+{
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) x[e] = t[(32 * ks + 8 * kg + e) * PS2 + m];
+    split8(x, hi, lo);
+}
+
+template <int D>
+__device__ __forceinline__ void row_step(const RowOps<D> &op, const float *sS, float *sW, int w,
+                                         int lane, int nrows, float *ob, size_t P)
+{
+    constexpr int KSI = D / 32;
+    const int m = lane & 15, kg = lane >> 4;
+    // Vn = U - W S and O = Q S; two accumulators per product shorten the MFMA chains
+    f32x4 aw0 = 0.0f, aw1 = 0.0f, ao0 = 0.0f, ao1 = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < KSI; ks++) {
+        bf16x8 sh, sl;
+        b_frag(sS, ks, kg, m, sh, sl);
+        if (ks & 1) {
+            aw1 = mma3(aw1, op.wf[ks].hi, op.wf[ks].lo, sh, sl);
+            ao1 = mma3(ao1, op.qf[ks].hi, op.qf[ks].lo, sh, sl);
+        } else {
+            aw0 = mma3(aw0, op.wf[ks].hi, op.wf[ks].lo, sh, sl);
+            ao0 = mma3(ao0, op.qf[ks].hi, op.qf[ks].lo, sh, sl);
+        }
+    }
+    const f32x4 vn = op.u - (aw0 + aw1);
+#pragma unroll
+    for (int e = 0; e < 4; e++) sW[(16 * w + 4 * kg + e) * PS2 + m] = vn[e];
+    __syncthreads();   // (2) Vn published
+    bf16x8 vh, vl;
+    b_frag(sW, 0, kg, m, vh, vl);
+    f32x4 ao = mma3(ao0 + ao1, op.af[0].hi, op.af[0].lo, vh, vl);
+    if (w >= 2) {
+        b_frag(sW, 1, kg, m, vh, vl);
+        ao = mma3(ao, op.af[1].hi, op.af[1].lo, vh, vl);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int t = 16 * w + 4 * kg + e;
+        if (t < nrows) ob[(size_t)t * P + m] = ao[e];
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void state_publish(const f32x4 (&accS)[D / 64], float *sS, int sw, int lane)
+{
+    constexpr int RTW = D / 64;
+    const int m = lane & 15, kg = lane >> 4;
+#pragma unroll
+    for (int r = 0; r < RTW; r++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) sS[(16 * (RTW * sw + r) + 4 * kg + e) * PS2 + m] = accS[r][e];
+}
+
+template <int D>
+__device__ __forceinline__ void state_update(const StateOps<D> &op, f32x4 (&accS)[D / 64],
+                                             const float *sW, int lane)
+{
+    constexpr int RTW = D / 64;
+    const int m = lane & 15, kg = lane >> 4;
+    bf16x8 vh[2], vl[2];
+    b_frag(sW, 0, kg, m, vh[0], vl[0]);
+    b_frag(sW, 1, kg, m, vh[1], vl[1]);
+#pragma unroll
+    for (int r = 0; r < RTW; r++) {
+        accS[r] = accS[r] * op.gl[r];
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) accS[r] = mma3(accS[r], op.kf[r][ks].hi, op.kf[r][ks].lo, vh[ks], vl[ks]);
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(512) void kda_chunk_state(int T, int H, const char *__restrict__ ws,
                                                        float *__restrict__ S,
                                                        float *__restrict__ o)
 {
-    using WL = WsLayout<D>;
-    constexpr int NTILE = D / NT2;       // column tiles per head
-    constexpr int RT = D / 64;           // 16-row tiles of S per wave
-    constexpr int KSI = D / 32;
-    constexpr int PS = 18;               // LDS pitch (conflict-free B-operand reads)
-    __shared__ float sS[D * PS];
-    __shared__ float sW[CH * PS];
+    using WL = Ws<D>;
+    constexpr int NTILE = D / 16;        // workgroups per head
+    constexpr int RTW = D / 64;
+    __shared__ float sS[D * PS2];
+    __shared__ float sW[CH * PS2];
 
     // XCD-aware: block b runs on XCD b % 8; give each XCD whole heads.
     const int nb = gridDim.x, b = blockIdx.x;
     int idx = b;
     if (nb % 8 == 0) idx = (b % 8) * (nb / 8) + b / 8;
-    const int h = idx / NTILE, j0 = (idx % NTILE) * NT2;
-    if (h >= H) return;
+    const int h = idx / NTILE, ct = idx % NTILE, j0 = ct * 16;
 
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int m = lane & 15, kg = lane >> 4;
+    const int kg = lane >> 4, m = lane & 15;
     const size_t P = (size_t)H * D;
     float *Sh = S + (size_t)h * D * D;
     const int nch = (T + CH - 1) / CH;
+    // The prefetch is unconditional (the last chunk re-reads itself) so that the compiler's
+    // count of outstanding loads is exact on every path and no wait drains the prefetch.
+    auto blk_of = [&](int c) { return ws + ((size_t)min(c, nch - 1) * H + h) * WL::SIZE; };
 
-    f32x4 accS[RT];
+    if (w < 4) {
+        RowOps<D> opA, opB;
+        float *ob = o + (size_t)h * D + j0;
+        load_row_ops<D>(opA, blk_of(0), w, lane, ct);
+        for (int c = 0; c < nch; c += 2) {
+            load_row_ops<D>(opB, blk_of(c + 1), w, lane, ct);
+            __builtin_amdgcn_sched_barrier(0);   // keep the prefetch ahead of the step
+            __syncthreads();   // (1) S published
+            row_step<D>(opA, sS, sW, w, lane, T - c * CH, ob + (size_t)c * CH * P, P);
+            if (c + 1 >= nch) break;
+            load_row_ops<D>(opA, blk_of(c + 2), w, lane, ct);
+            __builtin_amdgcn_sched_barrier(0);
+            __syncthreads();
+            row_step<D>(opB, sS, sW, w, lane, T - (c + 1) * CH, ob + (size_t)(c + 1) * CH * P, P);
+        }
+    } else {
+        const int sw = w - 4;
+        f32x4 accS[RTW];
 #pragma unroll
-    for (int r = 0; r < RT; r++)
+        for (int r = 0; r < RTW; r++)
 #pragma unroll
-        for (int e = 0; e < 4; e++) accS[r][e] = Sh[(size_t)(64 * r + 16 * w + 4 * kg + e) * D + j0 + m];
-
-    for (int c = 0; c < nch; c++) {
-        const float *blk = ws + ((size_t)c * H + h) * WL::SIZE;
-        const int t0 = c * CH;
-        // (a) S tile -> LDS (B-operand source)
-#pragma unroll
-        for (int r = 0; r < RT; r++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) sS[(64 * r + 16 * w + 4 * kg + e) * PS + m] = accS[r][e];
-        __syncthreads();
-
-        // (b) rows 16w..16w+15: Vn = U - W S, O = Q S
-        f32x4 aw = 0.0f, ao = 0.0f;
-#pragma unroll
-        for (int ks = 0; ks < KSI; ks++) {
-            float wv[8], qv[8], sv[8];
-            load8(wv, blk + WL::W + (size_t)(16 * w + m) * D + 32 * ks + 8 * kg);
-            load8(qv, blk + WL::Q + (size_t)(16 * w + m) * D + 32 * ks + 8 * kg);
-#pragma unroll
-            for (int e = 0; e < 8; e++) sv[e] = sS[(32 * ks + 8 * kg + e) * PS + m];
-            bf16x8 wh, wl, qh, ql, sh, sl;
-            split8(wv, wh, wl);
-            split8(qv, qh, ql);
-            split8(sv, sh, sl);
-            aw = mma3(aw, wh, wl, sh, sl);
-            ao = mma3(ao, qh, ql, sh, sl);
+            for (int e = 0; e < 4; e++)
+                accS[r][e] = Sh[(size_t)(16 * (RTW * sw + r) + 4 * kg + e) * D + j0 + m];
+        StateOps<D> opA, opB;
+        load_state_ops<D>(opA, blk_of(0), sw, lane);
+        for (int c = 0; c < nch; c += 2) {
+            load_state_ops<D>(opB, blk_of(c + 1), sw, lane);
+            __builtin_amdgcn_sched_barrier(0);
+            state_publish<D>(accS, sS, sw, lane);
+            __syncthreads();   // (1)
+            __syncthreads();   // (2) Vn published
+            state_update<D>(opA, accS, sW, lane);
+            if (c + 1 >= nch) break;
+            load_state_ops<D>(opA, blk_of(c + 2), sw, lane);
+            __builtin_amdgcn_sched_barrier(0);
+            state_publish<D>(accS, sS, sw, lane);
+            __syncthreads();
+            __syncthreads();
+            state_update<D>(opB, accS, sW, lane);
         }
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int t = 16 * w + 4 * kg + e;
-            sW[t * PS + m] = blk[WL::U + (size_t)t * D + j0 + m] - aw[e];
-        }
-        __syncthreads();
-
-        // (c) O += A_qk Vn over the columns s <= t (K-steps of 32)
-        bf16x8 vh[2], vl[2];
+        for (int r = 0; r < RTW; r++)
 #pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
-            float vv[8];
-#pragma unroll
-            for (int e = 0; e < 8; e++) vv[e] = sW[(32 * ks + 8 * kg + e) * PS + m];
-            split8(vv, vh[ks], vl[ks]);
-        }
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
-            if (ks == 1 && w < 2) continue;
-            float av[8];
-            load8(av, blk + WL::A + (size_t)(16 * w + m) * CH + 32 * ks + 8 * kg);
-            bf16x8 ah, al;
-            split8(av, ah, al);
-            ao = mma3(ao, ah, al, vh[ks], vl[ks]);
-        }
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int t = 16 * w + 4 * kg + e;
-            if (t0 + t < T) o[(size_t)(t0 + t) * P + (size_t)h * D + j0 + m] = ao[e];
-        }
-
-        // (d) S = diag(e^G_last) S + (K e^(G_last - G))^T Vn
-#pragma unroll
-        for (int r = 0; r < RT; r++) {
-            const int i0 = 64 * r + 16 * w;
-#pragma unroll
-            for (int e = 0; e < 4; e++) accS[r][e] *= blk[WL::GL + i0 + 4 * kg + e];
-#pragma unroll
-            for (int ks = 0; ks < 2; ks++) {
-                float kv[8];
-                load8(kv, blk + WL::KT + (size_t)(i0 + m) * CH + 32 * ks + 8 * kg);
-                bf16x8 kh, kl;
-                split8(kv, kh, kl);
-                accS[r] = mma3(accS[r], kh, kl, vh[ks], vl[ks]);
-            }
-        }
+            for (int e = 0; e < 4; e++)
+                Sh[(size_t)(16 * (RTW * sw + r) + 4 * kg + e) * D + j0 + m] = accS[r][e];
     }
-#pragma unroll
-    for (int r = 0; r < RT; r++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) Sh[(size_t)(64 * r + 16 * w + 4 * kg + e) * D + j0 + m] = accS[r][e];
 }
 
 bool chunk_ready() { return true; }
@@ -432,7 +610,7 @@ bool chunk_ready() { return true; }
 template <int D>
 static int launch_chunk(int T, int H, const float *q, const float *k, const float *v,
                         const float *g, const float *beta, float qs, float *S, float *o,
-                        float *ws, hipStream_t st)
+                        char *ws, hipStream_t st)
 {
     const int nch = (T + CH - 1) / CH;
     const size_t lds = P1Lds<D>::FLOATS * sizeof(float);
@@ -442,10 +620,10 @@ static int launch_chunk(int T, int H, const float *q, const float *k, const floa
                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         attr_set = true;
     }
-    hipLaunchKernelGGL((kda_chunk_intra<D>), dim3(nch, H), dim3(256), lds, st, T, H, qs, q, k, v, g,
-                       beta, ws);
+    hipLaunchKernelGGL((kda_chunk_intra<D>), dim3(nch, H), dim3(P1_THREADS), lds, st, T, H, qs, q, k,
+                       v, g, beta, ws);
     K3_LAUNCHED();
-    hipLaunchKernelGGL((kda_chunk_state<D>), dim3(H * (D / NT2)), dim3(256), 0, st, T, H, ws, S, o);
+    hipLaunchKernelGGL((kda_chunk_state<D>), dim3(H * (D / 16)), dim3(512), 0, st, T, H, ws, S, o);
     K3_LAUNCHED();
     return K3HIP_OK;
 }
@@ -458,8 +636,8 @@ extern "C" size_t k3hip_kda_chunk_workspace(int T, int H, int D, int chunk)
 {
     if (T <= 0 || H <= 0 || chunk != CH) return 0;
     const size_t nch = ((size_t)T + CH - 1) / CH;
-    if (D == 128) return nch * H * WsLayout<128>::SIZE * sizeof(float);
-    if (D == 64) return nch * H * WsLayout<64>::SIZE * sizeof(float);
+    if (D == 128) return nch * H * Ws<128>::SIZE;
+    if (D == 64) return nch * H * Ws<64>::SIZE;
     return 0;
 }
 
@@ -477,12 +655,12 @@ extern "C" int k3hip_kda_chunk(int T, int H, int D, int chunk, const float *q, c
     if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)g) & 15)
         K3_FAIL(K3HIP_EINVAL, "k3hip_kda_chunk: q, k, v, g must be 16-byte aligned");
     const long nch = ((long)T + CH - 1) / CH;
-    if (nch > 0x7fffffffL || H > 65535 || (long)H * (D / NT2) > 0x7fffffffL)
+    if (nch > 0x7fffffffL || H > 65535)
         K3_FAIL(K3HIP_EINVAL, "k3hip_kda_chunk: T=%d H=%d too large", T, H);
     const size_t need = k3hip_kda_chunk_workspace(T, H, D, chunk);
     hipStream_t st = as_stream(stream);
     StreamBuf own;
-    float *ws = (float *)workspace;
+    char *ws = (char *)workspace;
     if (ws) {
         if (workspace_bytes < need)
             K3_FAIL(K3HIP_EINVAL, "k3hip_kda_chunk: workspace %zu bytes < %zu needed", workspace_bytes, need);
@@ -490,7 +668,7 @@ extern "C" int k3hip_kda_chunk(int T, int H, int D, int chunk, const float *q, c
     } else {
         int rc = stream_alloc(own, need, st);
         if (rc) return rc;
-        ws = (float *)own.p;
+        ws = (char *)own.p;
     }
     if (D == 128) return launch_chunk<128>(T, H, q, k, v, g, beta, q_scale, S, o, ws, st);
     return launch_chunk<64>(T, H, q, k, v, g, beta, q_scale, S, o, ws, st);
