@@ -71,6 +71,16 @@ def cpu_info() -> dict:
     return {"model": model, "threads_available": cores}
 
 
+def measured_traffic(*kernels: str):
+    """HBM bytes per launch of the named kernels from the committed counter profile
+    (profiles/traffic.json: FETCH_SIZE and WRITE_SIZE runs, copy-calibrated), or None."""
+    try:
+        t = json.loads((REPO / "profiles" / "traffic.json").read_text())["kernels"]
+        return sum(t[k]["read_bytes"] + t[k]["write_bytes"] for k in kernels)
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def ev_pair(torch):
     return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
@@ -114,7 +124,8 @@ def bench_decode(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
                    "state_sets_rotated": nsets, "bytes_per_step": bytes_step},
         "roofline": {"kernel": "kda_decode_kernel<128,256>", "bound": "hbm",
                      "achieved": bytes_step / kavg / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": bytes_step / kavg / HBM_PEAK, "traffic": None},
+                     "frac": bytes_step / kavg / HBM_PEAK,
+                     "traffic": measured_traffic("kda_decode_kernel<128,256>")},
         "tolerance": "rtol 1e-4, atol 1e-4*rms (tests/test_gpu_kernels.py)",
     }
     if cpu:
@@ -224,7 +235,8 @@ def bench_prefill(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
                    "state": "fp32", "k2_kernel": kname},
         "roofline": {"kernel": kname, "bound": "mfma", "achieved": flops_launch / kavg / 1e12,
                      "peak": BF16_PEAK / 1e12, "unit": "TFLOP/s", "frac": flops_launch / kavg / BF16_PEAK,
-                     "traffic": None, "hbm_achieved_GBs": bytes_launch / kavg / 1e9,
+                     "traffic": measured_traffic("kda_chunk_intra<128>", "kda_chunk_state<128>") if use_chunk else None,
+                     "hbm_achieved_GBs": bytes_launch / kavg / 1e9,
                      "hbm_frac": bytes_launch / kavg / HBM_PEAK,
                      "flops_per_launch": flops_launch, "bytes_per_launch": bytes_launch},
     }
