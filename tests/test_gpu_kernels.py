@@ -47,7 +47,7 @@ def decode_inputs(rng, B, H, D):
     return S, f32(q), f32(k), f32(v), f32(np.exp(g)), f32(rng.uniform(0, 1, (B, H)))
 
 
-@pytest.mark.parametrize("B,H,D", [(2, 3, 16), (3, 2, 32), (4, 8, 64), (4, 8, 128), (64, 32, 128)])
+@pytest.mark.parametrize("B,H,D", [(2, 3, 16), (3, 2, 32), (4, 8, 64), (4, 8, 128), (37, 32, 128), (64, 32, 128)])
 def test_decode_vs_oracle(gpu, B, H, D):
     import torch
     rng = np.random.default_rng(0x4B334441 + 1 + B + D)
