@@ -61,6 +61,9 @@ __device__ __forceinline__ float load_act(const void *p, size_t i)
 // 1 / (1 + expf(-x)), the reference's sigmoid (src/core/k3_ops.c:105).
 __device__ __forceinline__ float sigmoid_ref(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+// log(1 + e^x), taken as x above 20 where the two agree in fp32.
+__device__ __forceinline__ float softplus_ref(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+
 inline bool is_pow2_head(int D) { return D == 16 || D == 32 || D == 64 || D == 128; }
 
 }  // namespace k3kda

@@ -454,19 +454,40 @@ __device__ __forceinline__ void load_state_ops(StateOps<D> &op, const char *blk,
     }
 }
 
-constexpr int PS2 = 18;   // LDS pitch of the S and Vn tiles: conflict-free B-operand reads
-
-// B-operand fragment (rows 32ks + 8kg .. +7, column m) of a [rows][PS2] LDS tile, split.
-__device__ __forceinline__ void b_frag(const float *t, int ks, int kg, int m, bf16x8 &hi, bf16x8 &lo)
+// S and Vn cross between the two roles through LDS as B-operand fragments that the
+// producer has already split: block (ks, part) holds, for each lane n + 16 kg, the 8 bf16
+// of rows 32 ks + 8 kg .. +7 of column n (part 0 = hi, part 1 = lo). Each value is split
+// once by its owner and read back with two 128-bit loads per K-step.
+// A producer lane holds 4 consecutive rows (C layout: rows 16 tile + 4 kg' + e', column m);
+// they land in lane m + 16 (2 (tile & 1) + kg' / 2) at elements 4 (kg' & 1) .. +3 of K-step
+// tile / 2.
+__device__ __forceinline__ void publish_frag4(char *buf, int tile, int lane, const f32x4 &x)
 {
-    float x[8];
+    const int m = lane & 15, kgp = lane >> 4;
+    const int ks = tile >> 1, kg = 2 * (tile & 1) + (kgp >> 1), e0 = 4 * (kgp & 1);
+    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+    bf16x4 hi, lo;
 #pragma unroll
-    for (int e = 0; e < 8; e++) x[e] = t[(32 * ks + 8 * kg + e) * PS2 + m];
-    split8(x, hi, lo);
+    for (int e = 0; e < 4; e++) {
+        const __bf16 hv = (__bf16)x[e];
+        hi[e] = hv;
+        lo[e] = (__bf16)(x[e] - (float)hv);
+    }
+    char *d = buf + ((size_t)(ks * 2) * 64 + m + 16 * kg) * 16 + e0 * 2;
+    *reinterpret_cast<bf16x4 *>(d) = hi;
+    *reinterpret_cast<bf16x4 *>(d + 1024) = lo;
+}
+
+__device__ __forceinline__ Frag read_frag(const char *buf, int ks, int lane)
+{
+    Frag f;
+    f.hi = *reinterpret_cast<const bf16x8 *>(buf + ((size_t)(ks * 2) * 64 + lane) * 16);
+    f.lo = *reinterpret_cast<const bf16x8 *>(buf + ((size_t)(ks * 2 + 1) * 64 + lane) * 16);
+    return f;
 }
 
 template <int D>
-__device__ __forceinline__ void row_step(const RowOps<D> &op, const float *sS, float *sW, int w,
+__device__ __forceinline__ void row_step(const RowOps<D> &op, const char *sSF, char *sVF, int w,
                                          int lane, int nrows, float *ob, size_t P)
 {
     constexpr int KSI = D / 32;
@@ -475,26 +496,22 @@ __device__ __forceinline__ void row_step(const RowOps<D> &op, const float *sS, f
     f32x4 aw0 = 0.0f, aw1 = 0.0f, ao0 = 0.0f, ao1 = 0.0f;
 #pragma unroll
     for (int ks = 0; ks < KSI; ks++) {
-        bf16x8 sh, sl;
-        b_frag(sS, ks, kg, m, sh, sl);
+        const Frag sf = read_frag(sSF, ks, lane);
         if (ks & 1) {
-            aw1 = mma3(aw1, op.wf[ks].hi, op.wf[ks].lo, sh, sl);
-            ao1 = mma3(ao1, op.qf[ks].hi, op.qf[ks].lo, sh, sl);
+            aw1 = mma3(aw1, op.wf[ks].hi, op.wf[ks].lo, sf.hi, sf.lo);
+            ao1 = mma3(ao1, op.qf[ks].hi, op.qf[ks].lo, sf.hi, sf.lo);
         } else {
-            aw0 = mma3(aw0, op.wf[ks].hi, op.wf[ks].lo, sh, sl);
-            ao0 = mma3(ao0, op.qf[ks].hi, op.qf[ks].lo, sh, sl);
+            aw0 = mma3(aw0, op.wf[ks].hi, op.wf[ks].lo, sf.hi, sf.lo);
+            ao0 = mma3(ao0, op.qf[ks].hi, op.qf[ks].lo, sf.hi, sf.lo);
         }
     }
-    const f32x4 vn = op.u - (aw0 + aw1);
-#pragma unroll
-    for (int e = 0; e < 4; e++) sW[(16 * w + 4 * kg + e) * PS2 + m] = vn[e];
+    publish_frag4(sVF, w, lane, op.u - (aw0 + aw1));
     __syncthreads();   // (2) Vn published
-    bf16x8 vh, vl;
-    b_frag(sW, 0, kg, m, vh, vl);
-    f32x4 ao = mma3(ao0 + ao1, op.af[0].hi, op.af[0].lo, vh, vl);
+    const Frag v0 = read_frag(sVF, 0, lane);
+    f32x4 ao = mma3(ao0 + ao1, op.af[0].hi, op.af[0].lo, v0.hi, v0.lo);
     if (w >= 2) {
-        b_frag(sW, 1, kg, m, vh, vl);
-        ao = mma3(ao, op.af[1].hi, op.af[1].lo, vh, vl);
+        const Frag v1 = read_frag(sVF, 1, lane);
+        ao = mma3(ao, op.af[1].hi, op.af[1].lo, v1.hi, v1.lo);
     }
 #pragma unroll
     for (int e = 0; e < 4; e++) {
@@ -504,30 +521,24 @@ __device__ __forceinline__ void row_step(const RowOps<D> &op, const float *sS, f
 }
 
 template <int D>
-__device__ __forceinline__ void state_publish(const f32x4 (&accS)[D / 64], float *sS, int sw, int lane)
+__device__ __forceinline__ void state_publish(const f32x4 (&accS)[D / 64], char *sSF, int sw, int lane)
 {
     constexpr int RTW = D / 64;
-    const int m = lane & 15, kg = lane >> 4;
 #pragma unroll
-    for (int r = 0; r < RTW; r++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) sS[(16 * (RTW * sw + r) + 4 * kg + e) * PS2 + m] = accS[r][e];
+    for (int r = 0; r < RTW; r++) publish_frag4(sSF, RTW * sw + r, lane, accS[r]);
 }
 
 template <int D>
 __device__ __forceinline__ void state_update(const StateOps<D> &op, f32x4 (&accS)[D / 64],
-                                             const float *sW, int lane)
+                                             const char *sVF, int lane)
 {
     constexpr int RTW = D / 64;
-    const int m = lane & 15, kg = lane >> 4;
-    bf16x8 vh[2], vl[2];
-    b_frag(sW, 0, kg, m, vh[0], vl[0]);
-    b_frag(sW, 1, kg, m, vh[1], vl[1]);
+    const Frag v0 = read_frag(sVF, 0, lane), v1 = read_frag(sVF, 1, lane);
 #pragma unroll
     for (int r = 0; r < RTW; r++) {
         accS[r] = accS[r] * op.gl[r];
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++) accS[r] = mma3(accS[r], op.kf[r][ks].hi, op.kf[r][ks].lo, vh[ks], vl[ks]);
+        accS[r] = mma3(accS[r], op.kf[r][0].hi, op.kf[r][0].lo, v0.hi, v0.lo);
+        accS[r] = mma3(accS[r], op.kf[r][1].hi, op.kf[r][1].lo, v1.hi, v1.lo);
     }
 }
 
@@ -539,8 +550,8 @@ __global__ __launch_bounds__(512) void kda_chunk_state(int T, int H, const char 
     using WL = Ws<D>;
     constexpr int NTILE = D / 16;        // workgroups per head
     constexpr int RTW = D / 64;
-    __shared__ float sS[D * PS2];
-    __shared__ float sW[CH * PS2];
+    __shared__ __attribute__((aligned(16))) char sSF[(D / 32) * 2 * 1024];   // S fragments
+    __shared__ __attribute__((aligned(16))) char sVF[2 * 2 * 1024];          // Vn fragments
 
     // XCD-aware: block b runs on XCD b % 8; give each XCD whole heads.
     const int nb = gridDim.x, b = blockIdx.x;
@@ -565,12 +576,12 @@ __global__ __launch_bounds__(512) void kda_chunk_state(int T, int H, const char 
             load_row_ops<D>(opB, blk_of(c + 1), w, lane, ct);
             __builtin_amdgcn_sched_barrier(0);   // keep the prefetch ahead of the step
             __syncthreads();   // (1) S published
-            row_step<D>(opA, sS, sW, w, lane, T - c * CH, ob + (size_t)c * CH * P, P);
+            row_step<D>(opA, sSF, sVF, w, lane, T - c * CH, ob + (size_t)c * CH * P, P);
             if (c + 1 >= nch) break;
             load_row_ops<D>(opA, blk_of(c + 2), w, lane, ct);
             __builtin_amdgcn_sched_barrier(0);
             __syncthreads();
-            row_step<D>(opB, sS, sW, w, lane, T - (c + 1) * CH, ob + (size_t)(c + 1) * CH * P, P);
+            row_step<D>(opB, sSF, sVF, w, lane, T - (c + 1) * CH, ob + (size_t)(c + 1) * CH * P, P);
         }
     } else {
         const int sw = w - 4;
@@ -582,20 +593,21 @@ __global__ __launch_bounds__(512) void kda_chunk_state(int T, int H, const char 
                 accS[r][e] = Sh[(size_t)(16 * (RTW * sw + r) + 4 * kg + e) * D + j0 + m];
         StateOps<D> opA, opB;
         load_state_ops<D>(opA, blk_of(0), sw, lane);
+        state_publish<D>(accS, sSF, sw, lane);
         for (int c = 0; c < nch; c += 2) {
             load_state_ops<D>(opB, blk_of(c + 1), sw, lane);
             __builtin_amdgcn_sched_barrier(0);
-            state_publish<D>(accS, sS, sw, lane);
             __syncthreads();   // (1)
             __syncthreads();   // (2) Vn published
-            state_update<D>(opA, accS, sW, lane);
+            state_update<D>(opA, accS, sVF, lane);
+            state_publish<D>(accS, sSF, sw, lane);   // row waves read sSF before (2)
             if (c + 1 >= nch) break;
             load_state_ops<D>(opA, blk_of(c + 2), sw, lane);
             __builtin_amdgcn_sched_barrier(0);
-            state_publish<D>(accS, sS, sw, lane);
             __syncthreads();
             __syncthreads();
-            state_update<D>(opB, accS, sW, lane);
+            state_update<D>(opB, accS, sVF, lane);
+            state_publish<D>(accS, sSF, sw, lane);
         }
 #pragma unroll
         for (int r = 0; r < RTW; r++)

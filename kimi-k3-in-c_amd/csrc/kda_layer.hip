@@ -154,9 +154,11 @@ extern "C" int k3hip_kda_upload(const K3KdaW *w, const K3Cfg *c, k3hip_kda_weigh
     return K3HIP_OK;
 }
 
-// Largest |gate_lb| * 15 the chunked kernel's exponent factoring accepts (e^80 < FLT_MAX
-// and e^-80 is still a normal float); beyond it the sequential GPU recurrence runs.
-static bool chunk_gate_ok(float lb) { return fabsf(lb) * 15.0f <= 80.0f; }
+// The chunked kernel factors e^(G_t - G_s) over 16-token blocks, which needs every log-decay
+// in [gate_lb, 0] with 15 |gate_lb| <= 80 (e^80 < FLT_MAX, e^-80 still a normal float).
+// The unbounded softplus gate (gate_lb == 0) and steeper bounds take the sequential GPU
+// recurrence.
+static bool chunk_gate_ok(float lb) { return lb < 0.0f && fabsf(lb) * 15.0f <= 80.0f; }
 
 extern "C" int k3hip_kda_layer_dev(const k3hip_kda_weights *w, int T, float *out, const float *x,
                                    float *state, void *stream)

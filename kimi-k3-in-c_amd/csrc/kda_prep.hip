@@ -8,6 +8,9 @@
 //   beta = sigmoid(b_logit) (:903)         one scalar per (token, head)
 //   k3_kda_decay (:168-183)                g = lb*sigmoid(expf(A_log[h])*(z+dt_bias)),
 //                                           alpha = expf(g)
+// gate_lb == 0 selects the gate without a lower bound, g = -expf(A_log[h])*softplus(z+dt_bias)
+// (the form the reference records as the one it replaced, tools/k3_ref.py:54-59; it has no
+// reference implementation and is checked against its closed form only).
 //
 // Bound by HBM. A run of consecutive tokens of one head belongs to one (half-)wave; each
 // lane owns adjacent channels of the head, so a row of the head is one coalesced access.
@@ -112,8 +115,9 @@ __global__ __launch_bounds__(64 * PREP_WAVES) void kda_prep_kernel(
                 q_out[i] = y[0][e];
                 k_out[i] = y[1][e];
                 v_out[i] = y[2][e];
-                const float u = a * (z[i] + dtb[e]);
-                const float gi = lb * sigmoid_ref(u);
+                float gi;
+                if (lb != 0.0f) gi = lb * sigmoid_ref(a * (z[i] + dtb[e]));
+                else gi = -a * softplus_ref(z[i] + dtb[e]);   // no lower bound: softplus gate
                 if (g_out) g_out[i] = gi;
                 if (alpha_out) alpha_out[i] = expf(gi);
             }
@@ -253,8 +257,8 @@ __global__ __launch_bounds__(256) void kda_prep2_kernel(
             RowIO<CPL, K3HIP_F32>::load(zz, z, row + c0);
 #pragma unroll
             for (int e = 0; e < CPL; e++) {
-                const float u = a * (zz[e] + dtb[e]);
-                gv[e] = lb * fast_sigmoid(u);
+                if (lb != 0.0f) gv[e] = lb * fast_sigmoid(a * (zz[e] + dtb[e]));
+                else gv[e] = -a * softplus_ref(zz[e] + dtb[e]);   // no lower bound: softplus gate
                 av[e] = fast_exp(gv[e]);
             }
             store_row<CPL>(q_out, row + c0, y[0]);

@@ -22,7 +22,10 @@
  *   orc_kda_layer      kda_layer1/8.json (out + recurrent state); bitwise vs reference
  *   orc_kda_core       equals orc_kda_layer minus the projections (tested by composing)
  *   orc_kda_decay_softplus  PARITY UNPINNED: the reference has no softplus gate; only
- *                      its closed form is checked.
+ *                      its closed form is checked. Selected by gate_lb == 0 in orc_kda_core
+ *                      and orc_kda_layer (the reference itself would give g = 0 there: no
+ *                      decay at all), which is the convention of the benchmark's small
+ *                      configuration "-exp(A) softplus(.)" and of gates without a bound.
  */
 #include "k3_oracle.h"
 
@@ -314,8 +317,12 @@ void orc_kda_core(float *y, float *o_rec, const float *q_in, const float *k_in,
     for (int t = 0; t < T; t++) {
         for (int h = 0; h < H; h++)
             bt[(size_t)t * H + h] = orc_sigmoid(b_logit[(size_t)t * H + h]);
-        orc_kda_decay(g + (size_t)t * P, al + (size_t)t * P, z + (size_t)t * P,
-                      w->A_log, w->dt_bias, H, D, c->gate_lb);
+        if (c->gate_lb != 0.0f)
+            orc_kda_decay(g + (size_t)t * P, al + (size_t)t * P, z + (size_t)t * P,
+                          w->A_log, w->dt_bias, H, D, c->gate_lb);
+        else   /* no lower bound: the softplus gate (parity unpinned, see orc_kda_decay_softplus) */
+            orc_kda_decay_softplus(g + (size_t)t * P, al + (size_t)t * P, z + (size_t)t * P,
+                                   w->A_log, w->dt_bias, H, D);
     }
     float *S = state;
     float *Sown = NULL;

@@ -88,10 +88,12 @@ def ref():
 
 
 def ptr(a: np.ndarray | None):
+    """Pointer to a C-contiguous array. data_as keeps a reference to the array, so a
+    temporary passed as ptr(f32(x)) stays alive for the duration of the call."""
     if a is None:
         return None
     assert a.flags["C_CONTIGUOUS"], "oracle buffers must be C-contiguous"
-    return C.c_void_p(a.ctypes.data)
+    return a.ctypes.data_as(C.c_void_p)
 
 
 def f32(a) -> np.ndarray:
@@ -188,7 +190,10 @@ def prep(q_in, k_in, v_in, z, b_logit, W: Weights, cfg: K3Cfg, T: int, conv_stat
     g = np.zeros((T, P), np.float32)
     al = np.zeros((T, P), np.float32)
     for t in range(T):
-        L.orc_kda_decay(C.c_void_p(g.ctypes.data + 4 * t * P), C.c_void_p(al.ctypes.data + 4 * t * P),
-                        C.c_void_p(zz.ctypes.data + 4 * t * P), ptr(W.arrays["A_log"]),
-                        ptr(W.arrays["dt_bias"]), H, D, cfg.gate_lb)
+        gp, ap, zp = (C.c_void_p(a.ctypes.data + 4 * t * P) for a in (g, al, zz))
+        if cfg.gate_lb != 0.0:
+            L.orc_kda_decay(gp, ap, zp, ptr(W.arrays["A_log"]), ptr(W.arrays["dt_bias"]), H, D,
+                            cfg.gate_lb)
+        else:   # no lower bound: the softplus gate
+            L.orc_kda_decay_softplus(gp, ap, zp, ptr(W.arrays["A_log"]), ptr(W.arrays["dt_bias"]), H, D)
     return q, k, v, g, al, beta.reshape(T, H)

@@ -1,0 +1,131 @@
+# SPDX-License-Identifier: Apache-2.0
+"""The benchmark configurations that are parity cases, on the GPU against the CPU oracle.
+
+c0  one KDA layer, hidden 256, H=4, D=64, conv 4, T=32 prefill then 8 single-token decode
+    steps carrying the state, fp32, weights N(0,0.02), x N(0,1), A_log U(0,1.5), dt_bias
+    N(0,1); every output element of every step and the full state compared. Both gates:
+    the reference's bounded gate (gate_lb = -5) and the unbounded softplus gate
+    (gate_lb = 0, parity unpinned: the oracle's softplus form is checked only against its
+    closed form in tests/test_oracle_invariants.py).
+    Tolerance: rtol 1e-4, atol 1e-4 * rms (fp32 path; the T=32 prefill runs the chunked
+    kernel for the bounded gate).
+c3  long-context drift: D=128, a 65,536-token chunked prefill (state carried across 1024
+    chunks) then 256 decode steps at batch 1, against the sequential oracle over the same
+    65,792 tokens; the error is recorded at every 4096th position and may not grow past the
+    chunked bar (rtol 2e-3, atol 2e-3 * rms). Heads are independent, so 4 of the 32 heads
+    are run (the per-head work and drift are those of the full configuration).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import assert_close, worst_ratio
+import k3_oracle as ko
+from k3_oracle import f32
+
+pytestmark = pytest.mark.gpu
+
+
+def rms(a):
+    return float(np.sqrt(np.mean(np.asarray(a, np.float64) ** 2)))
+
+
+def c0_weights(rng, hidden=256, H=4, D=64, K=4):
+    P = H * D
+    nrm = lambda *s: f32(rng.standard_normal(s) * 0.02)
+    arrays = {"q": nrm(P, hidden), "k": nrm(P, hidden), "v": nrm(P, hidden), "g": nrm(P, hidden),
+              "o": nrm(hidden, P), "f_a": nrm(D, hidden), "f_b": nrm(P, D), "b": nrm(H, hidden),
+              "q_conv": nrm(P, K), "k_conv": nrm(P, K), "v_conv": nrm(P, K),
+              "A_log": f32(rng.uniform(0, 1.5, H)), "dt_bias": f32(rng.standard_normal(P)),
+              "o_norm": f32(1 + 0.02 * rng.standard_normal(D))}
+    return ko.Weights(arrays, 0)
+
+
+@pytest.mark.parametrize("gate_lb", [-5.0, 0.0])
+def test_c0_prefill_then_decode(gpu, gate_lb):
+    import torch
+    rng = np.random.default_rng(0x4B334441 + 0)
+    hidden, H, D, K = 256, 4, 64, 4
+    P = H * D
+    W = c0_weights(rng, hidden, H, D, K)
+    cfg = ko.make_cfg(hidden, H, D, K, gate_lb, 1e-5)
+    nst = P * D + 3 * P * (K - 1)
+    st_ref = np.zeros(nst, np.float32)
+    dw = gpu.DeviceWeights(W.w, cfg)
+    dst = torch.zeros(nst, device="cuda")
+    st_host = np.zeros(nst, np.float32)
+    for step, T in enumerate([32] + [1] * 8):
+        x = f32(rng.standard_normal((T, hidden)))
+        want = ko.kda_layer(ko.orc(), x, W, cfg, T, st_ref)
+        out = torch.zeros((T, hidden), device="cuda")
+        dw.layer(out, torch.from_numpy(x).cuda(), dst, T)
+        torch.cuda.synchronize()
+        assert_close(out.cpu().numpy(), want, 1e-4 * rms(want), 1e-4, f"c0 lb={gate_lb} step {step} out")
+        assert_close(dst.cpu().numpy(), st_ref, 1e-4 * rms(st_ref), 1e-4, f"c0 lb={gate_lb} step {step} state")
+        if gate_lb != 0.0:   # the host drop-in on the same sequence
+            out_h = np.zeros((T, hidden), np.float32)
+            gpu.kda_layer_host(out_h, x, W.w, cfg, T, st_host)
+            assert_close(out_h, want, 1e-4 * rms(want), 1e-4, f"c0 drop-in step {step} out")
+            assert_close(st_host, st_ref, 1e-4 * rms(st_ref), 1e-4, f"c0 drop-in step {step} state")
+    dw.close()
+
+
+def test_c3_long_context_drift(gpu):
+    import torch
+    rng = np.random.default_rng(0x4B334441 + 3)
+    H, D, K = 4, 128, 4
+    P = H * D
+    T, NDEC = 65536, 256
+    Tall = T + NDEC
+    # raw activations N(0,1) through the oracle's conv + SiLU + L2 + decay (c0 gate spread)
+    arrays = {"q_conv": f32(rng.standard_normal((P, K)) * 0.5), "k_conv": f32(rng.standard_normal((P, K)) * 0.5),
+              "v_conv": f32(rng.standard_normal((P, K)) * 0.5), "A_log": f32(rng.uniform(0, 1.5, H)),
+              "dt_bias": f32(rng.standard_normal(P)), "o_norm": f32(np.ones(D))}
+    for n in ("q", "k", "v", "g", "f_a", "f_b", "b", "o"):
+        arrays[n] = np.zeros((1, 1), np.float32)
+    W = ko.Weights(arrays, 0)
+    cfg = ko.make_cfg(8, H, D, K, -5.0, 1e-5)
+    raw = [f32(rng.standard_normal((Tall, P))) for _ in range(3)]
+    z = f32(rng.standard_normal((Tall, P)) * 0.5)
+    bl = f32(rng.standard_normal((Tall, H)))
+    q, k, v, g, al, beta = ko.prep(*raw, z, bl, W, cfg, Tall, None)
+    qs = float(np.float32(1) / np.sqrt(np.float32(D)))
+    S_ref = np.zeros((H, D, D), np.float32)
+    o_ref = ko.recurrence(S_ref, q, k, v, al, beta, H, D, qs, nthreads=H)
+
+    cu = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    dS = torch.zeros((H, D, D), device="cuda")
+    do = torch.zeros((T, P), device="cuda")
+    gpu.kda_chunk(cu(q[:T]), cu(k[:T]), cu(v[:T]), cu(g[:T]), cu(beta[:T]), dS, do, H, D, qs)
+    torch.cuda.synchronize()
+    got = do.cpu().numpy()
+    curve = []
+    for t in range(4095, T, 4096):
+        seg = slice(t - 4095, t + 1)
+        curve.append((t + 1, worst_ratio(got[seg], o_ref[seg], 2e-3 * rms(o_ref[seg]), 2e-3)))
+    print("c3 drift (position, worst fraction of the 2e-3 bar):",
+          " ".join(f"{p}:{r:.3f}" for p, r in curve))
+    assert max(r for _, r in curve) <= 1.0
+    # decode tail at batch 1 from the GPU's own state
+    S_gpu = dS.cpu().numpy()
+    S_chk = S_gpu.copy()
+    dec = []
+    dS1 = dS.reshape(1, H, D, D)
+    for t in range(T, Tall):
+        o1 = torch.zeros((1, H, D), device="cuda")
+        sl = lambda a: cu(a[t:t + 1].reshape(1, H, D))
+        gpu.kda_decode(dS1, o1, sl(q), sl(k), sl(v), sl(al), cu(beta[t:t + 1]), qs)
+        if t == T:   # the kernel itself, from the same state, at the decode bar
+            torch.cuda.synchronize()
+            w1 = ko.decode_batch(S_chk[None].copy(), q[t:t + 1].reshape(1, H, D),
+                                 k[t:t + 1].reshape(1, H, D), v[t:t + 1].reshape(1, H, D),
+                                 al[t:t + 1].reshape(1, H, D), beta[t:t + 1], qs, 1)
+            assert_close(o1.cpu().numpy(), w1, 1e-4 * rms(w1), 1e-4, "c3 first decode step, same state")
+        dec.append(o1)
+    torch.cuda.synchronize()
+    got_dec = torch.cat(dec).cpu().numpy().reshape(NDEC, P)
+    r_dec = worst_ratio(got_dec, o_ref[T:], 2e-3 * rms(o_ref[T:]), 2e-3)
+    r_state = worst_ratio(dS.cpu().numpy(), S_ref, 2e-3 * rms(S_ref), 2e-3)
+    print(f"c3 decode tail (256 steps): worst {r_dec:.3f}x; final state {r_state:.3f}x of the 2e-3 bar")
+    assert r_dec <= 1.0 and r_state <= 1.0
