@@ -62,13 +62,26 @@ template <int D> struct Ws {
     static constexpr size_t SIZE = GL + (size_t)D * 4;
 };
 
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// x = hi + lo with hi = bf16_rne(x) and lo = bf16_rne(x - hi), two elements per packed
+// conversion: the pair's hi bits come back to fp32 with a shift and a mask.
+__device__ __forceinline__ void split2(float a, float b, bf16x2 &hi, bf16x2 &lo)
+{
+    hi = __builtin_convertvector(f2{a, b}, bf16x2);
+    const uint32_t u = __builtin_bit_cast(uint32_t, hi);
+    const float ha = __uint_as_float(u << 16), hb = __uint_as_float(u & 0xffff0000u);
+    lo = __builtin_convertvector(f2{a - ha, b - hb}, bf16x2);
+}
+
 __device__ __forceinline__ void split8(const float (&x)[8], bf16x8 &hi, bf16x8 &lo)
 {
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-        const __bf16 h = (__bf16)x[e];
-        hi[e] = h;
-        lo[e] = (__bf16)(x[e] - (float)h);
+    for (int e = 0; e < 8; e += 2) {
+        bf16x2 h, l;
+        split2(x[e], x[e + 1], h, l);
+        hi[e] = h[0]; hi[e + 1] = h[1];
+        lo[e] = l[0]; lo[e + 1] = l[1];
     }
 }
 
@@ -123,7 +136,8 @@ __device__ __forceinline__ Frag load_frag(const char *blk, int lane)
 }
 
 // --------------------------------------------------------------- phase 1 ----
-// LDS (floats): G*log2e, K, X (staging) [64][D+4]; A, Tm [64][68]; beta [64]; Y [4][16][17].
+// LDS (floats): G*log2e, K, X (staging) [64][D+4]; A, Tm [64][68]; beta [64]; Y [4][16][17];
+// per-wave scratch for the diagonal-block inverses [4][3][16][17].
 template <int D> struct P1Lds {
     static constexpr int PD = D + 4;
     static constexpr int PA = CH + 4;
@@ -134,7 +148,8 @@ template <int D> struct P1Lds {
     static constexpr size_t TM = A + (size_t)CH * PA;
     static constexpr size_t B = TM + (size_t)CH * PA;
     static constexpr size_t Y = B + CH;
-    static constexpr size_t FLOATS = Y + 4 * 16 * 17;
+    static constexpr size_t NS = Y + 4 * 16 * 17;       // [4 waves][3][16][17] scratch
+    static constexpr size_t FLOATS = NS + 4 * 3 * 16 * 17;
 };
 
 template <int D>
@@ -153,6 +168,7 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra(int T, int H, floa
     extern __shared__ __attribute__((aligned(16))) float lds[];
     float *sG = lds + L::G, *sK = lds + L::K, *sX = lds + L::X;
     float *sA = lds + L::A, *sT = lds + L::TM, *sB = lds + L::B, *sY = lds + L::Y;
+    float *sNS = lds + L::NS;
 
     const int c = blockIdx.x, h = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -283,23 +299,63 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra(int T, int H, floa
     for (int e = tid; e < CH * PA; e += P1_THREADS) sT[e] = 0.0f;
     __syncthreads();
 
-    // (4a) diagonal blocks of Tm = (I + A)^-1: wave w < 4 inverts block w by forward
-    //      substitution; lane s < 16 owns column s and keeps it in registers.
-    if (w < 4 && lane < SB) {
-        const int s = lane, o = SB * w;
-        float col[SB];
+    // (4a) diagonal blocks of Tm = (I + A)^-1. A 16x16 strictly lower block N is nilpotent
+    //      (N^16 = 0), so (I + N)^-1 = (I - N)(I + N^2)(I + N^4)(I + N^8) exactly: three
+    //      squarings and three products, each a 16x16x16 fp32 MFMA product (4 x 16x16x4).
+    //      Wave w < 4 inverts block w with all 64 lanes; the factors commute, so X is built
+    //      as X = I + N^8, X += N^4 X, X += N^2 X, X -= N X.
+    if (w < 4) {
+        const int o = SB * w;
+        float *N2 = sNS + (size_t)w * 3 * 272, *N4 = N2 + 272, *X = N4 + 272;
+        const float *Nb = sA + o * PA + o;   // N, pitch PA
+        // C = L (pitch pl) * R (pitch pr), both 16x16 in LDS
+        auto mm = [&](const float *Lm, int pl, const float *Rm, int pr) {
+            f32x4 acc = 0.0f;
 #pragma unroll
-        for (int t = 0; t < SB; t++) {
-            float val = (t == s) ? 1.0f : 0.0f;
-            if (t > s) {
-                float acc = sA[(o + t) * PA + o + s];
+            for (int kk = 0; kk < 4; kk++)
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Lm[m * pl + 4 * kk + kg], Rm[(4 * kk + kg) * pr + m], acc, 0, 0, 0);
+            return acc;
+        };
+        auto put = [&](float *Dm, const f32x4 &v) {
 #pragma unroll
-                for (int r = 0; r < t; r++)
-                    if (r > s) acc += sA[(o + t) * PA + o + r] * col[r];
-                val = -acc;
+            for (int e = 0; e < 4; e++) Dm[(4 * kg + e) * 17 + m] = v[e];
+        };
+        put(N2, mm(Nb, PA, Nb, PA));
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        put(N4, mm(N2, 17, N2, 17));
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        {
+            f32x4 x = mm(N4, 17, N4, 17);   // N^8
+#pragma unroll
+            for (int e = 0; e < 4; e++) x[e] += (4 * kg + e == m) ? 1.0f : 0.0f;
+            put(X, x);
+        }
+        const float *Ps[3] = {N4, N2, Nb};
+        const int pp[3] = {17, 17, PA};
+#pragma unroll
+        for (int st = 0; st < 3; st++) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const f32x4 px = mm(Ps[st], pp[st], X, 17);
+            f32x4 x;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float old = X[(4 * kg + e) * 17 + m];
+                x[e] = st < 2 ? old + px[e] : old - px[e];
             }
-            col[t] = val;
-            sT[(o + t) * PA + o + s] = val;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            if (st < 2) put(X, x);
+            else {
+#pragma unroll
+                for (int e = 0; e < 4; e++) sT[(o + 4 * kg + e) * PA + o + m] = x[e];
+            }
         }
     }
     __syncthreads();
@@ -468,10 +524,11 @@ __device__ __forceinline__ void publish_frag4(char *buf, int tile, int lane, con
     typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
     bf16x4 hi, lo;
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-        const __bf16 hv = (__bf16)x[e];
-        hi[e] = hv;
-        lo[e] = (__bf16)(x[e] - (float)hv);
+    for (int e = 0; e < 4; e += 2) {
+        bf16x2 h, l;
+        split2(x[e], x[e + 1], h, l);
+        hi[e] = h[0]; hi[e + 1] = h[1];
+        lo[e] = l[0]; lo[e + 1] = l[1];
     }
     char *d = buf + ((size_t)(ks * 2) * 64 + m + 16 * kg) * 16 + e0 * 2;
     *reinterpret_cast<bf16x4 *>(d) = hi;

@@ -6,8 +6,9 @@
 //   y = y * sigmoid(gate[d])                                        norm FIRST, then gate
 // o_norm[D] is shared by all heads. The mean of squares is a double, as in the reference.
 //
-// Bound by HBM: one wave per (token, head) row, CPL adjacent channels per lane, the sum
-// of squares is a wave reduction in double. Rows are visited grid-stride.
+// Bound by HBM. Rows are visited grid-stride. kda_epilogue2_kernel (D = 64, 128) packs
+// several rows per wave with 16-byte accesses; kda_epilogue_kernel (every D, the small
+// shapes of the reference's fixtures) keeps one row per wave, libm expf and a double sum.
 #include "k3kda_common.h"
 
 namespace k3kda {
@@ -54,14 +55,74 @@ __global__ __launch_bounds__(256) void kda_epilogue_kernel(long rows, int H, flo
     (void)H;
 }
 
+// Wide form for D = 64 / 128: LPR = D/4 lanes own one (token, head) row, 4 adjacent
+// channels each (16-byte fp32 / 8-byte bf16 accesses), 64/LPR rows per wave instruction.
+// The mean of squares is fp32 per lane and double across lanes; sigmoid uses the hardware
+// 2^x and reciprocal (about 1 ulp).
+template <int D, int GDT, int YDT>
+__global__ __launch_bounds__(256) void kda_epilogue2_kernel(long rows, float eps,
+                                                            const float *__restrict__ o,
+                                                            const void *__restrict__ gate,
+                                                            const float *__restrict__ wn,
+                                                            void *__restrict__ y)
+{
+#pragma clang fp contract(off)
+    constexpr int LPR = D / 4, RPW = 64 / LPR;
+    const int lane = threadIdx.x & 63, sub = lane / LPR, cl = lane % LPR;
+    const f4 w = reinterpret_cast<const f4 *>(wn)[cl];
+    const long nw = (long)gridDim.x * (blockDim.x >> 6) * RPW;
+    for (long r0 = ((long)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * RPW; r0 < rows; r0 += nw) {
+        const long r = r0 + sub;
+        const bool live = r < rows;
+        const size_t base = (size_t)(live ? r : rows - 1) * D + 4 * cl;
+        const f4 x = *reinterpret_cast<const f4 *>(o + base);
+        f4 gt;
+        if constexpr (GDT == K3HIP_BF16) {
+            const uint2 u = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(gate) + base);
+            gt = f4{__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                    __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u)};
+        } else {
+            gt = *reinterpret_cast<const f4 *>(reinterpret_cast<const float *>(gate) + base);
+        }
+        double ss = (double)(((x.x * x.x) + (x.y * x.y)) + ((x.z * x.z) + (x.w * x.w)));
+#pragma unroll
+        for (int m = LPR / 2; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+        const float inv = (float)(1.0 / sqrt(ss / (double)D + (double)eps));
+        f4 v;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-gt[e] * 1.4426950408889634f));
+            v[e] = ((w[e] * x[e]) * inv) * sg;
+        }
+        if (live) {
+            if constexpr (YDT == K3HIP_BF16) {
+                const uint2 u = {(uint32_t)f2bf(v.x) | ((uint32_t)f2bf(v.y) << 16),
+                                 (uint32_t)f2bf(v.z) | ((uint32_t)f2bf(v.w) << 16)};
+                *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(y) + base) = u;
+            } else {
+                *reinterpret_cast<f4 *>(reinterpret_cast<float *>(y) + base) = v;
+            }
+        }
+    }
+}
+
 template <int D, int GDT, int YDT>
 static int launch_epi(long rows, int H, float eps, const float *o, const void *g,
                       const float *wn, void *y, hipStream_t st)
 {
-    long blocks = (rows + 3) / 4;
-    if (blocks > 8192) blocks = 8192;
-    hipLaunchKernelGGL((kda_epilogue_kernel<D, GDT, YDT>), dim3((unsigned)blocks), dim3(256), 0, st,
-                       rows, H, eps, o, g, wn, y);
+    const bool wide = D >= 64 && ((uintptr_t)o | (uintptr_t)g | (uintptr_t)y | (uintptr_t)wn) % 16 == 0;
+    if (wide) {
+        long blocks = (rows + 4 * (256 / D) - 1) / (4 * (256 / D));
+        if (blocks > 16384) blocks = 16384;
+        if constexpr (D >= 64)
+            hipLaunchKernelGGL((kda_epilogue2_kernel<D, GDT, YDT>), dim3((unsigned)blocks), dim3(256), 0,
+                               st, rows, eps, o, g, wn, y);
+    } else {
+        long blocks = (rows + 3) / 4;
+        if (blocks > 8192) blocks = 8192;
+        hipLaunchKernelGGL((kda_epilogue_kernel<D, GDT, YDT>), dim3((unsigned)blocks), dim3(256), 0,
+                           st, rows, H, eps, o, g, wn, y);
+    }
     K3_LAUNCHED();
     return K3HIP_OK;
 }
