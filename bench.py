@@ -3,7 +3,7 @@
 
 Workloads (synthetic inputs resident in HBM before the timed region):
   prefill  hidden 4096, H=32, D=128, chunk 64, T=8192, batch 1: one step = K1 (conv +
-           SiLU + L2 + decay + beta, bf16 activations in) -> K2 (chunked delta-rule
+           SiLU + L2 + decay + beta, bf16 activations in) fused with K2 (chunked delta-rule
            prefill, fp32 state) -> K4 (head RMSNorm + sigmoid gate, bf16 out). The
            projections are not part of the step (they are plain GEMMs).
   decode   H=32, D=128, B=64 sequences, one token each: one step = K3 over all 2048
@@ -49,10 +49,11 @@ def prefill_core_flops_per_token(H: int, D: int, C: int) -> float:
     return 2.0 * H * (5 * C * D + 3 * D * D + C * C / 6.0)
 
 
-def chunk_bytes_per_token(H: int, D: int) -> int:
-    """Algorithmic HBM bytes of K2 per token: q k v g in (fp32) 16*P, beta 4*H, o out 4*P."""
+def prefill_core_bytes_per_token(H: int, D: int) -> int:
+    """Algorithmic HBM bytes of the fused K1+K2 core per token: conv inputs q k v (bf16)
+    6*P, gate pre-activation z (fp32) 4*P, beta logits 4*H, o out (fp32) 4*P."""
     P = H * D
-    return 16 * P + 4 * H + 4 * P
+    return 6 * P + 4 * P + 4 * H + 4 * P
 
 
 def cpu_info() -> dict:
@@ -189,35 +190,40 @@ def bench_prefill(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
     S = torch.zeros((H, D, D), **f32)
     conv_state = torch.zeros(3 * P * (K - 1), **f32)
     qs = 1.0 / math.sqrt(D)
-    use_chunk = True
-    try:
-        ws = torch.empty(max(1, k3.kda_chunk_workspace(T, H, D, 64)), dtype=torch.uint8, device="cuda")
-    except k3.K3HipError:
-        use_chunk = False
+    # core: "fused" = k3hip_kda_prefill (K1 + K2 in one pass over the activations), else
+    # k3hip_kda_prep + k3hip_kda_chunk, else the sequential GPU recurrence
+    mode = "fused"
+    ws = torch.empty(max(1, k3.kda_chunk_workspace(T, H, D, 64)), dtype=torch.uint8, device="cuda")
     alpha = torch.empty((T, P), **f32)
 
     def step(evk=None):
         S.zero_()
         conv_state.zero_()
-        k3.kda_prep(q_in, k_in, v_in, z, b_logit, conv[0], conv[1], conv[2], A_log, dt_bias,
-                    conv_state, q, k, v, gg, None if use_chunk else alpha, beta, H, D, K, c["gate_lb"])
         if evk:
             evk[0].record()
-        if use_chunk:
-            k3.kda_chunk(q, k, v, gg, beta, S, o, H, D, qs, 64, ws)
+        if mode == "fused":
+            k3.kda_prefill(q_in, k_in, v_in, z, b_logit, conv[0], conv[1], conv[2], A_log, dt_bias,
+                           conv_state, S, o, H, D, K, c["gate_lb"], qs, ws)
         else:
-            k3.kda_recurrent(q, k, v, alpha, beta, S, o, H, D, qs)
+            k3.kda_prep(q_in, k_in, v_in, z, b_logit, conv[0], conv[1], conv[2], A_log, dt_bias,
+                        conv_state, q, k, v, gg, alpha, beta, H, D, K, c["gate_lb"])
+            if mode == "chunk":
+                k3.kda_chunk(q, k, v, gg, beta, S, o, H, D, qs, 64, ws)
+            else:
+                k3.kda_recurrent(q, k, v, alpha, beta, S, o, H, D, qs)
         if evk:
             evk[1].record()
         k3.kda_epilogue(o, gate, o_norm, y, H, D, c["rms_eps"])
 
-    try:
-        step()
-        torch.cuda.synchronize()
-    except k3.K3HipError:
-        use_chunk = False
-        step()
-        torch.cuda.synchronize()
+    for fallback in ("chunk", "recurrent", None):
+        try:
+            step()
+            torch.cuda.synchronize()
+            break
+        except k3.K3HipError:
+            if fallback is None:
+                raise
+            mode = fallback
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -231,17 +237,22 @@ def bench_prefill(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
     kavg = sum(ks) / len(ks)
     step_s = wall / steps
     flops_launch = prefill_core_flops_per_token(H, D, 64) * T
-    bytes_launch = chunk_bytes_per_token(H, D) * T
-    kname = "kda_chunk (K2, bf16 MFMA)" if use_chunk else "kda_recurrent_kernel<128> (sequential)"
+    bytes_launch = prefill_core_bytes_per_token(H, D) * T
+    kname = {"fused": "kda_prefill (K1+K2: kda_chunk_intra_act<128,4> + kda_chunk_state<128>)",
+             "chunk": "kda_prep2 + kda_chunk (K1, K2)",
+             "recurrent": "kda_prep2 + kda_recurrent_kernel<128> (sequential)"}[mode]
+    traffic = None
+    if mode == "fused":
+        traffic = measured_traffic("kda_chunk_intra_act<128, 4>", "kda_chunk_state<128>")
     out = {
         "value": T / step_s, "unit": "tokens/s", "ms_per_step": step_s * 1e3,
-        "k2_ms_avg": kavg * 1e3, "k2_ms_median": ks[len(ks) // 2] * 1e3,
+        "core_ms_avg": kavg * 1e3, "core_ms_median": ks[len(ks) // 2] * 1e3,
         "config": {"workload": "kda_prefill_core", "hidden": c["hidden"], "heads": H, "head_dim": D,
                    "T": T, "chunk": 64, "batch": 1, "conv_k": K, "activations": "bf16",
-                   "state": "fp32", "k2_kernel": kname},
+                   "state": "fp32", "core": kname},
         "roofline": {"kernel": kname, "bound": "mfma", "achieved": flops_launch / kavg / 1e12,
                      "peak": BF16_PEAK / 1e12, "unit": "TFLOP/s", "frac": flops_launch / kavg / BF16_PEAK,
-                     "traffic": measured_traffic("kda_chunk_intra<128>", "kda_chunk_state<128>") if use_chunk else None,
+                     "traffic": traffic,
                      "hbm_achieved_GBs": bytes_launch / kavg / 1e9,
                      "hbm_frac": bytes_launch / kavg / HBM_PEAK,
                      "flops_per_launch": flops_launch, "bytes_per_launch": bytes_launch},

@@ -168,6 +168,21 @@ int k3hip_kda_chunk(int T, int H, int D, int chunk,
                     float *S, float *o, void *workspace, size_t workspace_bytes,
                     void *stream);
 
+/* K1 + K2 fused for bf16 conv inputs: the same arguments as k3hip_kda_prep followed by
+ * k3hip_kda_chunk, and bit-identical results (o, S and the outgoing conv_state), without
+ * the prepared fp32 q, k, v, g ever being written to memory. Replaces steps 2-6 of
+ * src/core/k3_ops.c:888-938 for a T-token prefill.
+ *   in_dtype = K3HIP_BF16 only; D = 128 or 64; conv_k 1..4; -80/15 <= gate_lb < 0 (the
+ *   bounded gate of k3_kda_decay); q_in, k_in, v_in, z 16-byte aligned; workspace as for
+ *   k3hip_kda_chunk (chunk 64). Other shapes return K3HIP_EUNSUPPORTED: use prep + chunk. */
+int k3hip_kda_prefill(int T, int H, int D, int K, float gate_lb, int in_dtype,
+                      const void *q_in, const void *k_in, const void *v_in,
+                      const float *z, const float *b_logit,
+                      const float *q_conv, const float *k_conv, const float *v_conv,
+                      const float *A_log, const float *dt_bias, float *conv_state,
+                      float q_scale, float *S, float *o,
+                      void *workspace, size_t workspace_bytes, void *stream);
+
 /* Sequential-in-T prefill on the GPU, parallel over heads and value columns only. The
  * exact step order of k3_kda_step per token; used for gate bounds outside the chunked
  * kernel's exponent range (|gate_lb| * 15 > 80) and as a second GPU opinion in tests.

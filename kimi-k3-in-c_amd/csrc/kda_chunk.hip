@@ -36,6 +36,9 @@
 // chunk c. Its blocks are mapped so that all tiles of one head sit on one XCD and share
 // that XCD's L2 copy of the phase-1 operands.
 #include "kda_internal.h"
+#include "kda_prep_math.h"
+
+#include <type_traits>
 
 namespace k3kda {
 
@@ -152,62 +155,34 @@ template <int D> struct P1Lds {
     static constexpr size_t FLOATS = NS + 4 * 3 * 16 * 17;
 };
 
+// Workspace block of (chunk c, head h); blocks are chunk-major.
 template <int D>
-__global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra(int T, int H, float qs,
-                                                              const float *__restrict__ q,
-                                                              const float *__restrict__ k,
-                                                              const float *__restrict__ v,
-                                                              const float *__restrict__ g,
-                                                              const float *__restrict__ beta,
-                                                              char *__restrict__ ws)
+__device__ __forceinline__ char *blk_addr(char *ws, int c, int H, int h)
+{
+    return ws + ((size_t)c * H + h) * Ws<D>::SIZE;
+}
+
+// Everything of one (chunk, head) item after its inputs are staged: g in sG, k in sK,
+// q * q_scale in sX (rows past the end of the sequence zero), beta in sB, sA zero, and this
+// wave's column tile of v in vreg. Writes the item's workspace block. Every LDS read of the
+// item is complete when it returns.
+template <int D>
+__device__ __forceinline__ void p1_item(float *lds, const float (&vreg)[2][8], char *blk)
 {
     using L = P1Lds<D>;
     using WL = Ws<D>;
     constexpr int PD = L::PD, PA = L::PA, KSI = WL::KSI, NCT = WL::NCT;
     constexpr int NW = P1_THREADS / 64;
-    extern __shared__ __attribute__((aligned(16))) float lds[];
     float *sG = lds + L::G, *sK = lds + L::K, *sX = lds + L::X;
     float *sA = lds + L::A, *sT = lds + L::TM, *sB = lds + L::B, *sY = lds + L::Y;
     float *sNS = lds + L::NS;
-
-    const int c = blockIdx.x, h = blockIdx.y;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    // the lane index is re-derived opaquely per item so that a caller's item loop keeps
+    // the per-lane LDS addressing inside the loop instead of in registers across items
+    int tid_o = threadIdx.x;
+    asm volatile("" : "+v"(tid_o));
+    const int tid = tid_o, lane = tid & 63, w = threadIdx.x >> 6;
     const int m = lane & 15, kg = lane >> 4;
-    const int t0 = c * CH;
-    const int Tc = min(CH, T - t0);
-    const size_t P = (size_t)H * D;
-    char *blk = ws + ((size_t)c * H + h) * WL::SIZE;
 
-    // (1) every global read of the kernel is issued here, up front: v for this wave's
-    //     column tile of U into registers; g, k and q staged in LDS (zero past the end of
-    //     the sequence); beta. A is cleared.
-    float vreg[2][8];
-    {
-        const int n0 = SB * w;
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++)
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const int s = 32 * ks + 8 * kg + e;
-                vreg[ks][e] = (w < NCT && s < Tc) ? v[(size_t)(t0 + s) * P + (size_t)h * D + n0 + m] : 0.0f;
-            }
-    }
-    for (int e = tid; e < CH * D / 4; e += P1_THREADS) {
-        const int t = e / (D / 4), i4 = (e % (D / 4)) * 4;
-        f4 gv = 0.0f, kv = 0.0f, qv = 0.0f;
-        if (t < Tc) {
-            const size_t at = (size_t)(t0 + t) * P + (size_t)h * D + i4;
-            gv = *reinterpret_cast<const f4 *>(g + at);
-            kv = *reinterpret_cast<const f4 *>(k + at);
-            qv = *reinterpret_cast<const f4 *>(q + at);
-        }
-        *reinterpret_cast<f4 *>(&sG[t * PD + i4]) = gv;
-        *reinterpret_cast<f4 *>(&sK[t * PD + i4]) = kv;
-        *reinterpret_cast<f4 *>(&sX[t * PD + i4]) = qv * qs;
-    }
-    for (int e = tid; e < CH * PA; e += P1_THREADS) sA[e] = 0.0f;
-    if (tid < CH) sB[tid] = tid < Tc ? beta[(size_t)(t0 + tid) * H + h] : 0.0f;
-    __syncthreads();
 
     // (2) G = cumulative sum of g down the chunk (padded rows add 0), kept as G*log2(e):
     //     each channel's 64 rows are four 16-row segments scanned in registers, then each
@@ -456,6 +431,234 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra(int T, int H, floa
         store_frag(blk + WL::KF + (size_t)fb * 2048, lane, x);
     }
     if (tid < D) reinterpret_cast<float *>(blk + WL::GL)[tid] = exp2_fast(sG[(CH - 1) * PD + tid]);
+    __syncthreads();   // every LDS read of this item is done before the next one is staged
+}
+
+// Phase 1 from prepared inputs (fp32 q, k, v, g, beta). Persistent: workgroup b handles
+// items b, b + gridDim.x, ... (item = chunk * H + head). The next item's inputs are loaded
+// into registers while the current item computes; their row indices are clamped into the
+// sequence and padding rows are zeroed only when the values are consumed, so no
+// instruction waits on these loads before the next item.
+template <int D>
+__global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra(int T, int H, float qs,
+                                                              const float *__restrict__ q,
+                                                              const float *__restrict__ k,
+                                                              const float *__restrict__ v,
+                                                              const float *__restrict__ g,
+                                                              const float *__restrict__ beta,
+                                                              char *__restrict__ ws)
+{
+    using L = P1Lds<D>;
+    using WL = Ws<D>;
+    constexpr int PD = L::PD, PA = L::PA, NCT = WL::NCT;
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    float *sG = lds + L::G, *sK = lds + L::K, *sX = lds + L::X, *sA = lds + L::A, *sB = lds + L::B;
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int m = lane & 15, kg = lane >> 4;
+    const size_t P = (size_t)H * D;
+    const int nch = (T + CH - 1) / CH, nitems = nch * H;
+    constexpr int NPF = CH * D / 4 / P1_THREADS;   // float4s of each tensor per thread
+
+    f4 pg[NPF], pk[NPF], pq[NPF];
+    float pv[2][8], pb;
+    auto fetch = [&](int item) {
+        const int fc = item / H, fh = item % H, ft0 = fc * CH, fTc = min(CH, T - ft0);
+#pragma unroll
+        for (int j = 0; j < NPF; j++) {
+            const int e = tid + j * P1_THREADS, t = e / (D / 4), i4 = (e % (D / 4)) * 4;
+            const size_t at = (size_t)(ft0 + min(t, fTc - 1)) * P + (size_t)fh * D + i4;
+            pg[j] = *reinterpret_cast<const f4 *>(g + at);
+            pk[j] = *reinterpret_cast<const f4 *>(k + at);
+            pq[j] = *reinterpret_cast<const f4 *>(q + at);
+        }
+        const int n0 = SB * (w < NCT ? w : 0);
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int s = 32 * ks + 8 * kg + e;
+                pv[ks][e] = v[(size_t)(ft0 + min(s, fTc - 1)) * P + (size_t)fh * D + n0 + m];
+            }
+        pb = beta[(size_t)(ft0 + min(tid & (CH - 1), fTc - 1)) * H + fh];
+    };
+    fetch(min((int)blockIdx.x, nitems - 1));
+
+    for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
+        const int c = item / H, h = item % H;
+        const int Tc = min(CH, T - c * CH);
+        // (1) the prefetched inputs go to LDS (q pre-scaled), v stays in registers; A is
+        //     cleared; then the next item's loads are issued.
+        float vreg[2][8];
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int s = 32 * ks + 8 * kg + e;
+                vreg[ks][e] = (w < NCT && s < Tc) ? pv[ks][e] : 0.0f;
+            }
+#pragma unroll
+        for (int j = 0; j < NPF; j++) {
+            const int e = tid + j * P1_THREADS, t = e / (D / 4), i4 = (e % (D / 4)) * 4;
+            const bool live = t < Tc;
+            *reinterpret_cast<f4 *>(&sG[t * PD + i4]) = live ? pg[j] : f4(0.0f);
+            *reinterpret_cast<f4 *>(&sK[t * PD + i4]) = live ? pk[j] : f4(0.0f);
+            *reinterpret_cast<f4 *>(&sX[t * PD + i4]) = live ? pq[j] * qs : f4(0.0f);
+        }
+        for (int e = tid; e < CH * PA; e += P1_THREADS) sA[e] = 0.0f;
+        if (tid < CH) sB[tid] = tid < Tc ? pb : 0.0f;
+        __syncthreads();
+        fetch(min(item + (int)gridDim.x, nitems - 1));
+        p1_item<D>(lds, vreg, blk_addr<D>(ws, c, H, h));
+    }
+}
+
+// Phase 1 fused with the input preparation, from the raw bf16 conv inputs q_in, k_in,
+// v_in [T][H*D], the fp32 gate pre-activation z [T][H*D] and the beta logits [T][H]:
+// per token, short conv + SiLU (taps in order), L2 norm of q and k, the bounded decay gate
+// and beta, with the arithmetic of the stand-alone prep kernel (kda_prep_math.h), so the
+// staged values -- and hence the workspace -- are bit-identical to prep followed by
+// kda_chunk_intra. The prepared q, k, v, g never leave the chip.
+//
+// Half-wave hw (0..15) prepares tokens 4hw..4hw+3 of the chunk; its 32 lanes own CPL = D/32
+// adjacent channels each. The K-1 inputs before the first of its tokens come from the rows
+// before it (the previous chunk's last rows at hw = 0), or from the incoming conv history
+// before the first token of the sequence. v is staged through the A/Tm area (free at that
+// point) to reach the column layout of U.
+//
+// Persistent over a contiguous range of items in head-major order (item = head * nch +
+// chunk), so a workgroup keeps one head -- its conv taps and dt_bias sit in LDS -- for many
+// consecutive chunks. The next item's raw rows are prefetched into registers.
+template <int D, int K>
+__global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra_act(
+    int T, int H, float qs, float lb, const uint16_t *__restrict__ q_in,
+    const uint16_t *__restrict__ k_in, const uint16_t *__restrict__ v_in,
+    const float *__restrict__ z, const float *__restrict__ b_logit,
+    const float *__restrict__ q_conv, const float *__restrict__ k_conv,
+    const float *__restrict__ v_conv, const float *__restrict__ A_log,
+    const float *__restrict__ dt_bias, const float *__restrict__ conv_state,
+    char *__restrict__ ws)
+{
+    using L = P1Lds<D>;
+    using WL = Ws<D>;
+    constexpr int PD = L::PD, PA = L::PA, NCT = WL::NCT;
+    constexpr int CPL = D / 32, NH = K - 1, RL = CH / 16, NR = RL + NH;
+    static_assert(RL >= NH, "only the first run of a chunk reaches before the chunk");
+    typedef typename std::conditional<CPL == 4, uint2, uint32_t>::type Raw;
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    float *sG = lds + L::G, *sK = lds + L::K, *sX = lds + L::X, *sA = lds + L::A, *sB = lds + L::B;
+    float *sV = lds + L::A;                    // v staging [CH][PD], aliases A and Tm
+    float *sW = lds + L::FLOATS;               // conv taps [3][D][4]
+    float *sDT = sW + 3 * D * 4;               // dt_bias [D]
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int m = lane & 15, kg = lane >> 4;
+    const int hw = tid >> 5, c0 = (tid & 31) * CPL, r0 = hw * RL;
+    const size_t P = (size_t)H * D;
+    const int nch = (T + CH - 1) / CH;
+    const long nitems = (long)nch * H;
+    const int lo = (int)((long)blockIdx.x * nitems / gridDim.x);
+    const int hi = (int)((long)(blockIdx.x + 1) * nitems / gridDim.x);
+    const uint16_t *xin[3] = {q_in, k_in, v_in};
+    const float *convw[3] = {q_conv, k_conv, v_conv};
+
+    Raw raw[3][NR];
+    float zr[RL][CPL], pbl;
+    auto fetch = [&](int item) {
+        const int fh = item / nch, ft0 = (item % nch) * CH;
+#pragma unroll
+        for (int j = 0; j < NR; j++) {
+            const int p = min(max(ft0 + r0 - NH + j, 0), T - 1);
+#pragma unroll
+            for (int b = 0; b < 3; b++)
+                raw[b][j] = *reinterpret_cast<const Raw *>(xin[b] + (size_t)p * P + (size_t)fh * D + c0);
+        }
+#pragma unroll
+        for (int r = 0; r < RL; r++) {
+            float x[CPL];
+            RowIO<CPL, K3HIP_F32>::load(x, z, (size_t)min(ft0 + r0 + r, T - 1) * P + (size_t)fh * D + c0);
+#pragma unroll
+            for (int e = 0; e < CPL; e++) zr[r][e] = x[e];
+        }
+        pbl = b_logit[(size_t)min(ft0 + (tid & (CH - 1)), T - 1) * H + fh];
+    };
+    if (lo < hi) fetch(lo);
+
+    int head = -1;
+    float a = 0.0f;
+    for (int item = lo; item < hi; item++) {
+        const int h = item / nch, c = item % nch;
+        const int t0 = c * CH, Tc = min(CH, T - t0);
+        if (h != head) {   // uniform: a new head's conv taps and dt_bias into LDS
+            for (int i = tid; i < 3 * D * 4; i += P1_THREADS) {
+                const int b = i / (D * 4), ch = (i / 4) % D, j = i % 4;
+                sW[i] = j < K ? convw[b][((size_t)h * D + ch) * K + j] : 0.0f;
+            }
+            for (int i = tid; i < D; i += P1_THREADS) sDT[i] = dt_bias[(size_t)h * D + i];
+            a = expf(A_log[h]);
+            head = h;
+            __syncthreads();
+        }
+        // (1) prepare this half-wave's RL tokens from the prefetched raw rows
+        float y[3][RL][CPL];
+#pragma unroll
+        for (int b = 0; b < 3; b++)
+#pragma unroll
+            for (int e = 0; e < CPL; e++) {
+                float wt[K], xs[NR];
+#pragma unroll
+                for (int j = 0; j < K; j++) wt[j] = sW[(b * D + c0 + e) * 4 + j];
+#pragma unroll
+                for (int j = 0; j < NR; j++) {
+                    uint32_t u;
+                    if constexpr (CPL == 4) u = (e < 2) ? raw[b][j].x : raw[b][j].y;
+                    else u = raw[b][j];
+                    xs[j] = __uint_as_float((e & 1) ? (u & 0xffff0000u) : (u << 16));
+                }
+                if (t0 + r0 < NH) {   // first tokens of the sequence: incoming history or 0
+#pragma unroll
+                    for (int j = 0; j < NH; j++) {
+                        const int p = t0 + r0 - NH + j;
+                        if (p < 0)
+                            xs[j] = conv_state ? conv_state[((size_t)b * P + (size_t)h * D + c0 + e) * NH + (p + NH)] : 0.0f;
+                    }
+                }
+#pragma unroll
+                for (int r = 0; r < RL; r++) y[b][r][e] = conv_silu<K>(wt, &xs[r], xs[NH + r]);
+            }
+#pragma unroll
+        for (int r = 0; r < RL; r++) {
+            l2norm_half<CPL>(y[0][r]);
+            l2norm_half<CPL>(y[1][r]);
+            const int t = r0 + r;
+            const bool live = t < Tc;
+#pragma unroll
+            for (int e = 0; e < CPL; e++) {
+                const int i = t * PD + c0 + e;
+                sG[i] = live ? gate_bounded(lb, a, zr[r][e], sDT[c0 + e]) : 0.0f;
+                sK[i] = live ? y[1][r][e] : 0.0f;
+                sX[i] = live ? y[0][r][e] * qs : 0.0f;
+                sV[i] = live ? y[2][r][e] : 0.0f;
+            }
+        }
+        if (tid < CH) sB[tid] = tid < Tc ? fast_sigmoid(pbl) : 0.0f;
+        __syncthreads();
+        float vreg[2][8];
+        {
+            const int n0 = SB * (w < NCT ? w : 0);
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const float x = sV[(32 * ks + 8 * kg + e) * PD + n0 + m];
+                    vreg[ks][e] = w < NCT ? x : 0.0f;
+                }
+        }
+        __syncthreads();   // v staging read before A is cleared
+        for (int e = tid; e < CH * PA; e += P1_THREADS) sA[e] = 0.0f;
+        fetch(min(item + 1, hi - 1));
+        p1_item<D>(lds, vreg, blk_addr<D>(ws, c, H, h));
+    }
 }
 
 // --------------------------------------------------------------- phase 2 ----
@@ -676,25 +879,99 @@ __global__ __launch_bounds__(512) void kda_chunk_state(int T, int H, const char 
 
 bool chunk_ready() { return true; }
 
+// Compute units of the current device (cached per device).
+static int cu_count(int &ncu)
+{
+    static int cache[64];
+    int dev = 0;
+    K3_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) {
+        ncu = 256;
+        return K3HIP_OK;
+    }
+    if (!cache[dev]) {
+        int n = 0;
+        K3_HIP(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev));
+        cache[dev] = n > 0 ? n : 256;
+    }
+    ncu = cache[dev];
+    return K3HIP_OK;
+}
+
+// Opt a kernel into more than the default dynamic LDS, once.
+static int allow_lds(const void *fn, size_t bytes, bool &done)
+{
+    if (!done) {
+        K3_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes));
+        done = true;
+    }
+    return K3HIP_OK;
+}
+
+template <int D>
+static int launch_state(int T, int H, const char *ws, float *S, float *o, hipStream_t st)
+{
+    hipLaunchKernelGGL((kda_chunk_state<D>), dim3(H * (D / 16)), dim3(512), 0, st, T, H, ws, S, o);
+    K3_LAUNCHED();
+    return K3HIP_OK;
+}
+
 template <int D>
 static int launch_chunk(int T, int H, const float *q, const float *k, const float *v,
                         const float *g, const float *beta, float qs, float *S, float *o,
                         char *ws, hipStream_t st)
 {
-    const int nch = (T + CH - 1) / CH;
+    const long nitems = (long)((T + CH - 1) / CH) * H;
     const size_t lds = P1Lds<D>::FLOATS * sizeof(float);
-    static bool attr_set = false;
-    if (!attr_set) {
-        K3_HIP(hipFuncSetAttribute((const void *)kda_chunk_intra<D>,
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        attr_set = true;
-    }
-    hipLaunchKernelGGL((kda_chunk_intra<D>), dim3(nch, H), dim3(P1_THREADS), lds, st, T, H, qs, q, k,
+    static bool lds_ok = false;
+    int ncu = 0, rc;
+    if ((rc = allow_lds((const void *)kda_chunk_intra<D>, lds, lds_ok))) return rc;
+    if ((rc = cu_count(ncu))) return rc;
+    const int grid = (int)(nitems < ncu ? nitems : ncu);   // one 150 KiB-LDS workgroup per CU
+    hipLaunchKernelGGL((kda_chunk_intra<D>), dim3(grid), dim3(P1_THREADS), lds, st, T, H, qs, q, k,
                        v, g, beta, ws);
     K3_LAUNCHED();
-    hipLaunchKernelGGL((kda_chunk_state<D>), dim3(H * (D / 16)), dim3(512), 0, st, T, H, ws, S, o);
+    return launch_state<D>(T, H, ws, S, o, st);
+}
+
+struct PrefillArgs {
+    int T, H;
+    float lb, qs;
+    const uint16_t *qi, *ki, *vi;
+    const float *z, *bl, *qc, *kc, *vc, *A, *dt;
+    float *cs, *S, *o;
+    char *ws;
+};
+
+template <int D, int K>
+static int launch_prefill(const PrefillArgs &a, hipStream_t st)
+{
+    const long nitems = (long)((a.T + CH - 1) / CH) * a.H;
+    const size_t lds = (P1Lds<D>::FLOATS + 3 * D * 4 + D) * sizeof(float);
+    static bool lds_ok = false;
+    int ncu = 0, rc;
+    if ((rc = allow_lds((const void *)kda_chunk_intra_act<D, K>, lds, lds_ok))) return rc;
+    if ((rc = cu_count(ncu))) return rc;
+    const int grid = (int)(nitems < ncu ? nitems : ncu);
+    hipLaunchKernelGGL((kda_chunk_intra_act<D, K>), dim3(grid), dim3(P1_THREADS), lds, st, a.T, a.H,
+                       a.qs, a.lb, a.qi, a.ki, a.vi, a.z, a.bl, a.qc, a.kc, a.vc, a.A, a.dt, a.cs,
+                       a.ws);
     K3_LAUNCHED();
-    return K3HIP_OK;
+    // the outgoing conv history, after the kernel above has read the incoming one
+    if ((rc = conv_state_update(a.T, a.H * D, K, K3HIP_BF16, a.qi, a.ki, a.vi, a.cs, st))) return rc;
+    return launch_state<D>(a.T, a.H, a.ws, a.S, a.o, st);
+}
+
+template <int D>
+static int prefill_k(int K, const PrefillArgs &a, hipStream_t st)
+{
+    switch (K) {
+    case 1: return launch_prefill<D, 1>(a, st);
+    case 2: return launch_prefill<D, 2>(a, st);
+    case 3: return launch_prefill<D, 3>(a, st);
+    case 4: return launch_prefill<D, 4>(a, st);
+    default: K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_prefill: conv_k=%d not in 1..4", K);
+    }
 }
 
 }  // namespace k3kda
@@ -724,7 +1001,7 @@ extern "C" int k3hip_kda_chunk(int T, int H, int D, int chunk, const float *q, c
     if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)g) & 15)
         K3_FAIL(K3HIP_EINVAL, "k3hip_kda_chunk: q, k, v, g must be 16-byte aligned");
     const long nch = ((long)T + CH - 1) / CH;
-    if (nch > 0x7fffffffL || H > 65535)
+    if ((long)nch * H > 0x7fffffffL || H > 65535)
         K3_FAIL(K3HIP_EINVAL, "k3hip_kda_chunk: T=%d H=%d too large", T, H);
     const size_t need = k3hip_kda_chunk_workspace(T, H, D, chunk);
     hipStream_t st = as_stream(stream);
@@ -741,4 +1018,48 @@ extern "C" int k3hip_kda_chunk(int T, int H, int D, int chunk, const float *q, c
     }
     if (D == 128) return launch_chunk<128>(T, H, q, k, v, g, beta, q_scale, S, o, ws, st);
     return launch_chunk<64>(T, H, q, k, v, g, beta, q_scale, S, o, ws, st);
+}
+
+extern "C" int k3hip_kda_prefill(int T, int H, int D, int K, float gate_lb, int in_dtype,
+                                 const void *q_in, const void *k_in, const void *v_in,
+                                 const float *z, const float *b_logit, const float *q_conv,
+                                 const float *k_conv, const float *v_conv, const float *A_log,
+                                 const float *dt_bias, float *conv_state, float q_scale, float *S,
+                                 float *o, void *workspace, size_t workspace_bytes, void *stream)
+{
+    clear_error();
+    if (T < 0 || H < 0) K3_FAIL(K3HIP_EINVAL, "k3hip_kda_prefill: T=%d H=%d", T, H);
+    if (in_dtype != K3HIP_BF16)
+        K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_prefill: in_dtype=%d (bf16 only; use prep + chunk)", in_dtype);
+    if (D != 64 && D != 128) K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_prefill: D=%d (64 or 128)", D);
+    if (K < 1 || K > 4) K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_prefill: conv_k=%d not in 1..4", K);
+    if (!(gate_lb < 0.0f && 15.0f * -gate_lb <= 80.0f))
+        K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_prefill: gate_lb=%g (needs -80/15 <= lb < 0)", gate_lb);
+    if (T == 0 || H == 0) return K3HIP_OK;
+    if (!q_in || !k_in || !v_in || !z || !b_logit || !q_conv || !k_conv || !v_conv || !A_log ||
+        !dt_bias || !S || !o)
+        K3_FAIL(K3HIP_EINVAL, "k3hip_kda_prefill: NULL tensor");
+    if (((uintptr_t)q_in | (uintptr_t)k_in | (uintptr_t)v_in | (uintptr_t)z) & 15)
+        K3_FAIL(K3HIP_EINVAL, "k3hip_kda_prefill: q_in, k_in, v_in, z must be 16-byte aligned");
+    const long nch = ((long)T + CH - 1) / CH;
+    if (nch * H > 0x7fffffffL || H > 65535 || (long)T * H * D > 0x7fffffffL * 4L)
+        K3_FAIL(K3HIP_EINVAL, "k3hip_kda_prefill: T=%d H=%d too large", T, H);
+    const size_t need = k3hip_kda_chunk_workspace(T, H, D, CH);
+    hipStream_t st = as_stream(stream);
+    StreamBuf own;
+    char *ws = (char *)workspace;
+    if (ws) {
+        if (workspace_bytes < need)
+            K3_FAIL(K3HIP_EINVAL, "k3hip_kda_prefill: workspace %zu bytes < %zu needed", workspace_bytes, need);
+        if ((uintptr_t)ws & 15) K3_FAIL(K3HIP_EINVAL, "k3hip_kda_prefill: workspace must be 16-byte aligned");
+    } else {
+        int rc = stream_alloc(own, need, st);
+        if (rc) return rc;
+        ws = (char *)own.p;
+    }
+    const PrefillArgs a{T, H, gate_lb, q_scale, (const uint16_t *)q_in, (const uint16_t *)k_in,
+                        (const uint16_t *)v_in, z, b_logit, q_conv, k_conv, v_conv, A_log, dt_bias,
+                        conv_state, S, o, ws};
+    if (D == 128) return prefill_k<128>(K, a, st);
+    return prefill_k<64>(K, a, st);
 }

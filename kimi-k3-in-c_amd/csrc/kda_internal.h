@@ -23,6 +23,11 @@ int stream_alloc(StreamBuf &b, size_t bytes, hipStream_t st);
 // p[0..n) = 0 on `st` with a kernel (never a memset node).
 int zero_fill(float *p, size_t n, hipStream_t st);
 
+// Outgoing short-conv history (3 tensors x P channels x K-1 slots) after T new inputs of
+// dtype dt, launched after every reader of the incoming history on `st`.
+int conv_state_update(int T, int P, int K, int dt, const void *qi, const void *ki, const void *vi,
+                      float *cs, hipStream_t st);
+
 // True once the chunked prefill kernel is built into this library.
 bool chunk_ready();
 

@@ -23,7 +23,8 @@
 // The incoming conv history is only read here. kda_conv_state_kernel, launched after on
 // the same stream, writes the outgoing history, so no wave can overwrite history that
 // another wave has not read yet.
-#include "k3kda_common.h"
+#include "kda_internal.h"
+#include "kda_prep_math.h"
 
 namespace k3kda {
 
@@ -129,44 +130,9 @@ __global__ __launch_bounds__(64 * PREP_WAVES) void kda_prep_kernel(
 // Wide form for D = 64 / 128 (the throughput path). A wave holds two independent runs of
 // PREP2_TT tokens, one per half-wave; each of the 32 lanes of a half owns CPL = D/32
 // adjacent channels of the head, so rows are read and written with 8- or 16-byte accesses.
-// Transcendentals use the hardware 2^x and reciprocal (about 1 ulp): e^x = 2^(x log2 e),
-// sigmoid(x) = rcp(1 + 2^(-x log2 e)). The L2 sums are fp32 per lane and double across
-// lanes.
+// The arithmetic is that of kda_prep_math.h (hardware 2^x and reciprocal; L2 sums fp32 per
+// lane and double across lanes), shared with the fused prefill kernel.
 constexpr int PREP2_TT = 16;   // tokens per half-wave run
-
-__device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
-__device__ __forceinline__ float fast_sigmoid(float x) { return __builtin_amdgcn_rcpf(1.0f + fast_exp(-x)); }
-
-template <int CPL, int DT> struct RowIO;
-template <> struct RowIO<4, K3HIP_F32> {
-    static __device__ __forceinline__ void load(float (&x)[4], const void *p, size_t i)
-    {
-        const f4 v = *reinterpret_cast<const f4 *>(reinterpret_cast<const float *>(p) + i);
-        x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
-    }
-};
-template <> struct RowIO<4, K3HIP_BF16> {
-    static __device__ __forceinline__ void load(float (&x)[4], const void *p, size_t i)
-    {
-        const uint2 v = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(p) + i);
-        x[0] = __uint_as_float(v.x << 16); x[1] = __uint_as_float(v.x & 0xffff0000u);
-        x[2] = __uint_as_float(v.y << 16); x[3] = __uint_as_float(v.y & 0xffff0000u);
-    }
-};
-template <> struct RowIO<2, K3HIP_F32> {
-    static __device__ __forceinline__ void load(float (&x)[2], const void *p, size_t i)
-    {
-        const f2 v = *reinterpret_cast<const f2 *>(reinterpret_cast<const float *>(p) + i);
-        x[0] = v.x; x[1] = v.y;
-    }
-};
-template <> struct RowIO<2, K3HIP_BF16> {
-    static __device__ __forceinline__ void load(float (&x)[2], const void *p, size_t i)
-    {
-        const uint32_t v = *reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint16_t *>(p) + i);
-        x[0] = __uint_as_float(v << 16); x[1] = __uint_as_float(v & 0xffff0000u);
-    }
-};
 
 template <int CPL>
 __device__ __forceinline__ void store_row(float *p, size_t i, const float (&x)[CPL])
@@ -231,33 +197,20 @@ __global__ __launch_bounds__(256) void kda_prep2_kernel(
             RowIO<CPL, DT>::load(cur, xin[b], row + c0);
 #pragma unroll
             for (int e = 0; e < CPL; e++) {
-                float acc = w[b][e][NH] * cur[e];
-#pragma unroll
-                for (int j = 0; j < NH; j++) acc = acc + w[b][e][j] * win[b][e][j];
+                y[b][e] = conv_silu<K>(w[b][e], win[b][e], cur[e]);
 #pragma unroll
                 for (int j = 1; j < NH; j++) win[b][e][j - 1] = win[b][e][j];
                 if constexpr (NH > 0) win[b][e][NH - 1] = cur[e];
-                y[b][e] = acc * fast_sigmoid(acc);
             }
         }
-#pragma unroll
-        for (int b = 0; b < 2; b++) {
-            float part = 0.0f;
-#pragma unroll
-            for (int e = 0; e < CPL; e++) part = part + y[b][e] * y[b][e];
-            double ss = (double)part;
-#pragma unroll
-            for (int m = 16; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
-            const float r = (float)(1.0 / sqrt(ss + 1e-6));
-#pragma unroll
-            for (int e = 0; e < CPL; e++) y[b][e] = y[b][e] * r;
-        }
+        l2norm_half<CPL>(y[0]);
+        l2norm_half<CPL>(y[1]);
         if (live) {
             float zz[CPL], gv[CPL], av[CPL];
             RowIO<CPL, K3HIP_F32>::load(zz, z, row + c0);
 #pragma unroll
             for (int e = 0; e < CPL; e++) {
-                if (lb != 0.0f) gv[e] = lb * fast_sigmoid(a * (zz[e] + dtb[e]));
+                if (lb != 0.0f) gv[e] = gate_bounded(lb, a, zz[e], dtb[e]);
                 else gv[e] = -a * softplus_ref(zz[e] + dtb[e]);   // no lower bound: softplus gate
                 av[e] = fast_exp(gv[e]);
             }
@@ -304,6 +257,27 @@ __global__ void kda_conv_shift_kernel(int T, int P, int K, float *__restrict__ c
     for (int j = 0; j + T < NH; j++) hs[j] = hs[j + T];
 }
 
+int conv_state_update(int T, int P, int K, int dt, const void *qi, const void *ki, const void *vi,
+                      float *cs, hipStream_t st)
+{
+    if (!cs || K <= 1) return K3HIP_OK;
+    if (T < K - 1) {
+        const long n = 3L * P;
+        hipLaunchKernelGGL(kda_conv_shift_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                           T, P, K, cs);
+        K3_LAUNCHED();
+    }
+    const long n = 3L * P * (K - 1);
+    if (dt == K3HIP_BF16)
+        hipLaunchKernelGGL((kda_conv_state_kernel<K3HIP_BF16>), dim3((unsigned)((n + 255) / 256)),
+                           dim3(256), 0, st, T, P, K, qi, ki, vi, cs);
+    else
+        hipLaunchKernelGGL((kda_conv_state_kernel<K3HIP_F32>), dim3((unsigned)((n + 255) / 256)),
+                           dim3(256), 0, st, T, P, K, qi, ki, vi, cs);
+    K3_LAUNCHED();
+    return K3HIP_OK;
+}
+
 template <int D, int K, int DT>
 static int launch_prep(int T, int H, float lb, const void *qi, const void *ki, const void *vi,
                        const float *z, const float *bl, const float *qc, const float *kc,
@@ -327,20 +301,7 @@ static int launch_prep(int T, int H, float lb, const void *qi, const void *ki, c
                            lb, qi, ki, vi, z, bl, qc, kc, vc, A, dt, cs, qo, ko, vo, go, ao, bo);
     }
     K3_LAUNCHED();
-    if (cs && K > 1) {
-        const int P = H * D;
-        if (T < K - 1) {
-            const long n = 3L * P;
-            hipLaunchKernelGGL(kda_conv_shift_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
-                               st, T, P, K, cs);
-            K3_LAUNCHED();
-        }
-        const long n = 3L * P * (K - 1);
-        hipLaunchKernelGGL((kda_conv_state_kernel<DT>), dim3((unsigned)((n + 255) / 256)), dim3(256),
-                           0, st, T, P, K, qi, ki, vi, cs);
-        K3_LAUNCHED();
-    }
-    return K3HIP_OK;
+    return conv_state_update(T, H * D, K, DT, qi, ki, vi, cs, st);
 }
 
 template <int D, int DT>

@@ -24,8 +24,8 @@ OK, EINVAL, EHIP, EUNSUPPORTED, ENOMEM = 0, 1, 2, 3, 4
 EXPORTS = (
     "k3_kda_scratch", "k3_kda_layer", "k3hip_last_error", "k3hip_version",
     "k3hip_device_count", "k3hip_kda_decode", "k3hip_kda_prep", "k3hip_kda_chunk_workspace",
-    "k3hip_kda_chunk", "k3hip_kda_recurrent", "k3hip_kda_epilogue", "k3hip_kda_upload",
-    "k3hip_kda_release", "k3hip_kda_layer_dev",
+    "k3hip_kda_chunk", "k3hip_kda_prefill", "k3hip_kda_recurrent", "k3hip_kda_epilogue",
+    "k3hip_kda_upload", "k3hip_kda_release", "k3hip_kda_layer_dev",
 )
 
 
@@ -95,6 +95,8 @@ def lib() -> C.CDLL:
                                _P, _P, _P, _P, _P, _P, _P]),
         "k3hip_kda_chunk_workspace": (sz, [i, i, i, i]),
         "k3hip_kda_chunk": (i, [i, i, i, i, _P, _P, _P, _P, _P, f, _P, _P, _P, sz, _P]),
+        "k3hip_kda_prefill": (i, [i, i, i, i, f, i, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                  f, _P, _P, _P, sz, _P]),
         "k3hip_kda_recurrent": (i, [i, i, i, _P, _P, _P, _P, _P, f, _P, _P, _P]),
         "k3hip_kda_epilogue": (i, [i, i, i, f, _P, _P, i, _P, _P, i, _P]),
         "k3hip_kda_upload": (i, [C.POINTER(K3KdaW), C.POINTER(K3Cfg), C.POINTER(_P)]),
@@ -172,6 +174,19 @@ def kda_chunk(q, k, v, g, beta, S, o, H: int, D: int, q_scale: float, chunk: int
     _check(lib().k3hip_kda_chunk(T, H, D, chunk, _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta),
                                  q_scale, _ptr(S), _ptr(o), _ptr(workspace), ws_bytes,
                                  _stream(stream)))
+
+
+def kda_prefill(q_in, k_in, v_in, z, b_logit, q_conv, k_conv, v_conv, A_log, dt_bias,
+                conv_state, S, o, H: int, D: int, K: int, gate_lb: float, q_scale: float,
+                workspace=None, stream=None) -> None:
+    """K1 + K2 fused: bf16 inputs [T,P], z [T,P] fp32, b_logit [T,H]; S [H,D,D] in/out."""
+    T = q_in.shape[0]
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    _check(lib().k3hip_kda_prefill(T, H, D, K, gate_lb, _dt(q_in), _ptr(q_in), _ptr(k_in),
+                                   _ptr(v_in), _ptr(z), _ptr(b_logit), _ptr(q_conv),
+                                   _ptr(k_conv), _ptr(v_conv), _ptr(A_log), _ptr(dt_bias),
+                                   _ptr(conv_state), q_scale, _ptr(S), _ptr(o), _ptr(workspace),
+                                   ws_bytes, _stream(stream)))
 
 
 def kda_chunk_workspace(T: int, H: int, D: int, chunk: int = 64) -> int:
