@@ -523,8 +523,8 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra(int T, int H, floa
 // Half-wave hw (0..15) prepares tokens 4hw..4hw+3 of the chunk; its 32 lanes own CPL = D/32
 // adjacent channels each. The K-1 inputs before the first of its tokens come from the rows
 // before it (the previous chunk's last rows at hw = 0), or from the incoming conv history
-// before the first token of the sequence. v is staged through the A/Tm area (free at that
-// point) to reach the column layout of U.
+// before the first token of the sequence (staged in LDS at the head's first chunk). v is
+// staged through the A/Tm area (free at that point) to reach the column layout of U.
 //
 // Persistent over a contiguous range of items in head-major order (item = head * nch +
 // chunk), so a workgroup keeps one head -- its conv taps and dt_bias sit in LDS -- for many
@@ -544,15 +544,16 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra_act(
     constexpr int PD = L::PD, PA = L::PA, NCT = WL::NCT;
     constexpr int CPL = D / 32, NH = K - 1, RL = CH / 16, NR = RL + NH;
     static_assert(RL >= NH, "only the first run of a chunk reaches before the chunk");
+    static_assert(3 * D * NH <= 4 * 3 * 16 * 17, "conv history fits the inverse scratch area");
     typedef typename std::conditional<CPL == 4, uint2, uint32_t>::type Raw;
     extern __shared__ __attribute__((aligned(16))) float lds[];
     float *sG = lds + L::G, *sK = lds + L::K, *sX = lds + L::X, *sA = lds + L::A, *sB = lds + L::B;
     float *sV = lds + L::A;                    // v staging [CH][PD], aliases A and Tm
     float *sW = lds + L::FLOATS;               // conv taps [3][D][4]
     float *sDT = sW + 3 * D * 4;               // dt_bias [D]
+    float *sHist = lds + L::NS;                // incoming conv history [3][D][K-1] at chunk 0
 
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int m = lane & 15, kg = lane >> 4;
+    const int tid = threadIdx.x, w = tid >> 6;
     const int hw = tid >> 5, c0 = (tid & 31) * CPL, r0 = hw * RL;
     const size_t P = (size_t)H * D;
     const int nch = (T + CH - 1) / CH;
@@ -589,6 +590,13 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra_act(
     for (int item = lo; item < hi; item++) {
         const int h = item / nch, c = item % nch;
         const int t0 = c * CH, Tc = min(CH, T - t0);
+        // per-lane indices re-derived opaquely per item, so their LDS addresses are not
+        // held in registers across the item loop
+        int tid_o = threadIdx.x;
+        asm volatile("" : "+v"(tid_o));
+        const int tid = tid_o, lane = tid & 63;
+        const int m = lane & 15, kg = lane >> 4;
+        const int c0 = (tid & 31) * CPL, r0 = (tid >> 5) * RL;
         if (h != head) {   // uniform: a new head's conv taps and dt_bias into LDS
             for (int i = tid; i < 3 * D * 4; i += P1_THREADS) {
                 const int b = i / (D * 4), ch = (i / 4) % D, j = i % 4;
@@ -597,6 +605,14 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra_act(
             for (int i = tid; i < D; i += P1_THREADS) sDT[i] = dt_bias[(size_t)h * D + i];
             a = expf(A_log[h]);
             head = h;
+            __syncthreads();
+        }
+        if (NH > 0 && c == 0) {   // uniform: the head's incoming conv history into LDS, so
+                                  // the preparation below never waits on a global load
+            for (int i = tid; i < 3 * D * NH; i += P1_THREADS) {
+                const int b = i / (D * NH), r = i % (D * NH);
+                sHist[i] = conv_state ? conv_state[((size_t)b * P + (size_t)h * D) * NH + r] : 0.0f;
+            }
             __syncthreads();
         }
         // (1) prepare this half-wave's RL tokens from the prefetched raw rows
@@ -615,12 +631,11 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra_act(
                     else u = raw[b][j];
                     xs[j] = __uint_as_float((e & 1) ? (u & 0xffff0000u) : (u << 16));
                 }
-                if (t0 + r0 < NH) {   // first tokens of the sequence: incoming history or 0
+                if (t0 + r0 < NH) {   // first tokens of the sequence: incoming history
 #pragma unroll
                     for (int j = 0; j < NH; j++) {
                         const int p = t0 + r0 - NH + j;
-                        if (p < 0)
-                            xs[j] = conv_state ? conv_state[((size_t)b * P + (size_t)h * D + c0 + e) * NH + (p + NH)] : 0.0f;
+                        if (p < 0) xs[j] = sHist[(b * D + c0 + e) * NH + (p + NH)];
                     }
                 }
 #pragma unroll

@@ -9,7 +9,7 @@
 // Bound by HBM. Rows are visited grid-stride. kda_epilogue2_kernel (D = 64, 128) packs
 // several rows per wave with 16-byte accesses; kda_epilogue_kernel (every D, the small
 // shapes of the reference's fixtures) keeps one row per wave, libm expf and a double sum.
-#include "k3kda_common.h"
+#include "kda_internal.h"
 
 namespace k3kda {
 
@@ -59,8 +59,12 @@ __global__ __launch_bounds__(256) void kda_epilogue_kernel(long rows, int H, flo
 // channels each (16-byte fp32 / 8-byte bf16 accesses), 64/LPR rows per wave instruction.
 // The mean of squares is fp32 per lane and double across lanes; sigmoid uses the hardware
 // 2^x and reciprocal (about 1 ulp).
+// y as a bf16 hi/lo pair (y = hi + lo to about 2^-17), rows [T][2P]: hi in the first P
+// columns, lo in the last P -- the input of a K = 2P bf16 GEMM against [W | W].
+constexpr int Y_SPLIT = 2;
+
 template <int D, int GDT, int YDT>
-__global__ __launch_bounds__(256) void kda_epilogue2_kernel(long rows, float eps,
+__global__ __launch_bounds__(256) void kda_epilogue2_kernel(long rows, int H, float eps,
                                                             const float *__restrict__ o,
                                                             const void *__restrict__ gate,
                                                             const float *__restrict__ wn,
@@ -95,7 +99,21 @@ __global__ __launch_bounds__(256) void kda_epilogue2_kernel(long rows, float eps
             v[e] = ((w[e] * x[e]) * inv) * sg;
         }
         if (live) {
-            if constexpr (YDT == K3HIP_BF16) {
+            if constexpr (YDT == Y_SPLIT) {
+                // row r = t*H + h of y2 [T][2P]: hi at t*2P + h*D, lo P further
+                const size_t at = base + (size_t)(r / H) * (size_t)(H * D);
+                uint16_t hb[4], lb[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    hb[e] = f2bf(v[e]);
+                    lb[e] = f2bf(v[e] - __uint_as_float((uint32_t)hb[e] << 16));
+                }
+                uint16_t *yy = reinterpret_cast<uint16_t *>(y);
+                *reinterpret_cast<uint2 *>(yy + at) = uint2{(uint32_t)hb[0] | ((uint32_t)hb[1] << 16),
+                                                           (uint32_t)hb[2] | ((uint32_t)hb[3] << 16)};
+                *reinterpret_cast<uint2 *>(yy + at + (size_t)H * D) =
+                    uint2{(uint32_t)lb[0] | ((uint32_t)lb[1] << 16), (uint32_t)lb[2] | ((uint32_t)lb[3] << 16)};
+            } else if constexpr (YDT == K3HIP_BF16) {
                 const uint2 u = {(uint32_t)f2bf(v.x) | ((uint32_t)f2bf(v.y) << 16),
                                  (uint32_t)f2bf(v.z) | ((uint32_t)f2bf(v.w) << 16)};
                 *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(y) + base) = u;
@@ -116,7 +134,7 @@ static int launch_epi(long rows, int H, float eps, const float *o, const void *g
         if (blocks > 16384) blocks = 16384;
         if constexpr (D >= 64)
             hipLaunchKernelGGL((kda_epilogue2_kernel<D, GDT, YDT>), dim3((unsigned)blocks), dim3(256), 0,
-                               st, rows, eps, o, g, wn, y);
+                               st, rows, H, eps, o, g, wn, y);
     } else {
         long blocks = (rows + 3) / 4;
         if (blocks > 8192) blocks = 8192;
@@ -136,6 +154,28 @@ static int epi_types(int gdt, int ydt, long rows, int H, float eps, const float 
     if (gdt == K3HIP_BF16 && ydt == K3HIP_F32) return launch_epi<D, K3HIP_BF16, K3HIP_F32>(rows, H, eps, o, g, wn, y, st);
     if (gdt == K3HIP_BF16 && ydt == K3HIP_BF16) return launch_epi<D, K3HIP_BF16, K3HIP_BF16>(rows, H, eps, o, g, wn, y, st);
     K3_FAIL(K3HIP_EINVAL, "k3hip_kda_epilogue: gate_dtype=%d y_dtype=%d", gdt, ydt);
+}
+
+int epilogue_split(int T, int H, int D, float eps, const float *o, const void *gate, int gate_dtype,
+                   const float *o_norm, void *y2, hipStream_t st)
+{
+    const long rows = (long)T * H;
+    if (rows == 0) return K3HIP_OK;
+    if ((D != 64 && D != 128) ||
+        ((uintptr_t)o | (uintptr_t)gate | (uintptr_t)o_norm | (uintptr_t)y2) % 16)
+        K3_FAIL(K3HIP_EUNSUPPORTED, "epilogue_split: D=%d or unaligned buffers", D);
+    long blocks = (rows + 4 * (256 / D) - 1) / (4 * (256 / D));
+    if (blocks > 16384) blocks = 16384;
+    const bool g16 = gate_dtype == K3HIP_BF16;
+    if (D == 128) {
+        if (g16) hipLaunchKernelGGL((kda_epilogue2_kernel<128, K3HIP_BF16, Y_SPLIT>), dim3((unsigned)blocks), dim3(256), 0, st, rows, H, eps, o, gate, o_norm, y2);
+        else hipLaunchKernelGGL((kda_epilogue2_kernel<128, K3HIP_F32, Y_SPLIT>), dim3((unsigned)blocks), dim3(256), 0, st, rows, H, eps, o, gate, o_norm, y2);
+    } else {
+        if (g16) hipLaunchKernelGGL((kda_epilogue2_kernel<64, K3HIP_BF16, Y_SPLIT>), dim3((unsigned)blocks), dim3(256), 0, st, rows, H, eps, o, gate, o_norm, y2);
+        else hipLaunchKernelGGL((kda_epilogue2_kernel<64, K3HIP_F32, Y_SPLIT>), dim3((unsigned)blocks), dim3(256), 0, st, rows, H, eps, o, gate, o_norm, y2);
+    }
+    K3_LAUNCHED();
+    return K3HIP_OK;
 }
 
 }  // namespace k3kda

@@ -71,6 +71,7 @@ struct k3hip_kda_weights {
     float gate_lb, rms_eps;
     void *q, *k, *v, *f_a, *f_b, *b, *g, *o;        // matrices, wdt storage
     float *q_conv, *k_conv, *v_conv, *A_log, *dt_bias, *o_norm;
+    void *f_b2, *o2;   // bf16 only: [W | W] along K, for GEMMs on hi/lo-split inputs
 };
 
 extern "C" const char *k3hip_last_error(void) { return g_err; }
@@ -104,7 +105,7 @@ extern "C" int k3hip_kda_release(k3hip_kda_weights *w)
     clear_error();
     if (!w) return K3HIP_OK;
     void *ptrs[] = {w->q, w->k, w->v, w->f_a, w->f_b, w->b, w->g, w->o,
-                    w->q_conv, w->k_conv, w->v_conv, w->A_log, w->dt_bias, w->o_norm};
+                    w->q_conv, w->k_conv, w->v_conv, w->A_log, w->dt_bias, w->o_norm, w->f_b2, w->o2};
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
     free(w);
@@ -143,6 +144,18 @@ extern "C" int k3hip_kda_upload(const K3KdaW *w, const K3Cfg *c, k3hip_kda_weigh
     UP(dt_bias, w->dt_bias, P * 4);
     UP(o_norm, w->o_norm, (size_t)D * 4);
 #undef UP
+    // [W | W] copies of f_b (P x 2D) and o (E x 2P) for the bf16 prefill path
+    auto twice = [&](void **dst, const void *src, size_t rows, size_t cols) -> int {
+        const size_t rb = cols * 2;
+        K3_HIP(hipMalloc(dst, rows * rb * 2));
+        K3_HIP(hipMemcpy2D(*dst, 2 * rb, src, rb, rb, rows, hipMemcpyDeviceToDevice));
+        K3_HIP(hipMemcpy2D((char *)*dst + rb, 2 * rb, src, rb, rb, rows, hipMemcpyDeviceToDevice));
+        return K3HIP_OK;
+    };
+    if (rc == K3HIP_OK && w->wdt == K3_WBF16) {
+        rc = twice(&d->f_b2, d->f_b, P, (size_t)D);
+        if (rc == K3HIP_OK) rc = twice(&d->o2, d->o, (size_t)E, P);
+    }
     if (rc != K3HIP_OK) {
         char keep[1024];
         snprintf(keep, sizeof keep, "%s", g_err);
@@ -211,6 +224,116 @@ extern "C" int k3hip_kda_layer_dev(const k3hip_kda_weights *w, int T, float *out
                                  stream)))
         return rc;
     return proj(T, (int)P, E, y, w->o, w->wdt, out, st);
+}
+
+// fp32 -> bf16 (round to nearest even), for fp32 layer inputs of the bf16 prefill path.
+__global__ void to_bf16_kernel(const float *__restrict__ x, uint16_t *__restrict__ y, size_t n)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x)
+        y[i] = f2bf(x[i]);
+}
+
+// x [rows][cols] fp32 -> y [rows][2 cols] bf16 with x = hi + lo: hi in columns 0..cols-1,
+// lo = bf16(x - hi) in cols..2cols-1 (the input of a K = 2 cols GEMM against [W | W]).
+__global__ void split_rows_kernel(const float *__restrict__ x, uint16_t *__restrict__ y, int cols, size_t n)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const size_t r = i / (size_t)cols, c = i % (size_t)cols;
+        const uint16_t hi = f2bf(x[i]);
+        y[r * 2 * cols + c] = hi;
+        y[r * 2 * cols + cols + c] = f2bf(x[i] - __uint_as_float((uint32_t)hi << 16));
+    }
+}
+
+static unsigned grid_for(size_t n)
+{
+    size_t b = (n + 255) / 256;
+    return (unsigned)(b > 8192 ? 8192 : (b ? b : 1));
+}
+
+extern "C" int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *out, int out_dtype,
+                                       const void *x, int x_dtype, float *state, void *stream)
+{
+    clear_error();
+    if (!w || !out || !x) K3_FAIL(K3HIP_EINVAL, "k3hip_kda_layer_prefill: NULL argument");
+    if (T < 0) K3_FAIL(K3HIP_EINVAL, "k3hip_kda_layer_prefill: T=%d", T);
+    if ((x_dtype != K3HIP_F32 && x_dtype != K3HIP_BF16) || (out_dtype != K3HIP_F32 && out_dtype != K3HIP_BF16))
+        K3_FAIL(K3HIP_EINVAL, "k3hip_kda_layer_prefill: x_dtype=%d out_dtype=%d", x_dtype, out_dtype);
+    const int E = w->hidden, H = w->H, D = w->D, K = w->K;
+    if (w->wdt != K3_WBF16 || !w->o2 || !w->f_b2)
+        K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_layer_prefill: bf16 weights only (use k3hip_kda_layer_dev)");
+    if (!chunk_gate_ok(w->gate_lb) || (D != 64 && D != 128) || K > 4)
+        K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_layer_prefill: gate_lb=%g D=%d conv_k=%d outside the "
+                "chunked prefill (use k3hip_kda_layer_dev)", w->gate_lb, D, K);
+    if (T == 0) return K3HIP_OK;
+    hipStream_t st = as_stream(stream);
+    const size_t P = (size_t)H * D, TP = (size_t)T * P;
+    const size_t wsb = k3hip_kda_chunk_workspace(T, H, D, 64);
+    // scratch, 256-byte aligned pieces:
+    //   0 x bf16 | 1 q k v gate projections fp32 | 2 f_a fp32 | 3 f_a hi/lo bf16 | 4 z fp32 |
+    //   5 b logits | 6 prepared q k v g fp32 | 7 beta | 8 o fp32 | 9 y hi/lo bf16 |
+    //   10 zero state | 11 chunk workspace
+    size_t sizes[] = {x_dtype == K3HIP_F32 ? (size_t)T * E * 2 : 0, 4 * TP * 4, (size_t)T * D * 4,
+                      (size_t)T * D * 4, TP * 4, (size_t)T * H * 4, 4 * TP * 4, (size_t)T * H * 4,
+                      TP * 4, TP * 4, state ? 0 : (size_t)H * D * D * 4, wsb};
+    constexpr int NB = sizeof sizes / sizeof sizes[0];
+    size_t off[NB], total = 0;
+    for (int i = 0; i < NB; i++) {
+        off[i] = total;
+        total += (sizes[i] + 255) & ~(size_t)255;
+    }
+    StreamBuf buf;
+    int rc = stream_alloc(buf, total, st);
+    if (rc) return rc;
+    char *base = (char *)buf.p;
+    const void *xb = x;
+    if (x_dtype == K3HIP_F32) {
+        const size_t n = (size_t)T * E;
+        hipLaunchKernelGGL(to_bf16_kernel, dim3(grid_for(n)), dim3(256), 0, st, (const float *)x,
+                           (uint16_t *)(base + off[0]), n);
+        K3_LAUNCHED();
+        xb = base + off[0];
+    }
+    float *qp = (float *)(base + off[1]), *kp = qp + TP, *vp = kp + TP, *gl = vp + TP;
+    float *fa = (float *)(base + off[2]);
+    uint16_t *fa2 = (uint16_t *)(base + off[3]);
+    float *z = (float *)(base + off[4]), *bl = (float *)(base + off[5]);
+    float *q = (float *)(base + off[6]), *k = q + TP, *v = k + TP, *g = v + TP;
+    float *beta = (float *)(base + off[7]), *o = (float *)(base + off[8]);
+    uint16_t *y2 = (uint16_t *)(base + off[9]);
+    float *S = state;
+    if (!S) {
+        S = (float *)(base + off[10]);
+        if ((rc = zero_fill(S, (size_t)H * D * D, st))) return rc;
+    }
+    float *cs = state ? state + (size_t)H * D * D : nullptr;
+
+    // 1 projections on bf16 MFMA with fp32 accumulation and fp32 results; f_b takes f_a as a
+    //   bf16 hi/lo pair (K = 2D against [W_fb | W_fb]) so z keeps fp32 accuracy
+    if ((rc = gemm_bf16(T, (int)P, E, xb, w->q, qp, K3HIP_F32, st))) return rc;
+    if ((rc = gemm_bf16(T, (int)P, E, xb, w->k, kp, K3HIP_F32, st))) return rc;
+    if ((rc = gemm_bf16(T, (int)P, E, xb, w->v, vp, K3HIP_F32, st))) return rc;
+    if ((rc = gemm_bf16(T, (int)P, E, xb, w->g, gl, K3HIP_F32, st))) return rc;
+    if ((rc = gemm_bf16(T, H, E, xb, w->b, bl, K3HIP_F32, st))) return rc;
+    if ((rc = gemm_bf16(T, D, E, xb, w->f_a, fa, K3HIP_F32, st))) return rc;
+    hipLaunchKernelGGL(split_rows_kernel, dim3(grid_for((size_t)T * D)), dim3(256), 0, st, fa, fa2, D,
+                       (size_t)T * D);
+    K3_LAUNCHED();
+    if ((rc = gemm_bf16(T, (int)P, 2 * D, fa2, w->f_b2, z, K3HIP_F32, st))) return rc;
+    // 2-5 K1, 6 K2 (chunked)
+    if ((rc = k3hip_kda_prep(T, H, D, K, w->gate_lb, K3HIP_F32, qp, kp, vp, z, bl, w->q_conv,
+                             w->k_conv, w->v_conv, w->A_log, w->dt_bias, cs, q, k, v, g, nullptr,
+                             beta, stream)))
+        return rc;
+    if ((rc = k3hip_kda_chunk(T, H, D, 64, q, k, v, g, beta, 1.0f / sqrtf((float)D), S, o,
+                              base + off[11], wsb, stream)))
+        return rc;
+    // 7-8 head RMSNorm, then the gate; y as a bf16 hi/lo pair
+    if ((rc = epilogue_split(T, H, D, w->rms_eps, o, gl, K3HIP_F32, w->o_norm, y2, st))) return rc;
+    // 9 o_proj: K = 2P against [W_o | W_o]
+    return gemm_bf16(T, E, 2 * (int)P, y2, w->o2, out, out_dtype, st);
 }
 
 // ------------------------------------------------------------------ drop-in ----

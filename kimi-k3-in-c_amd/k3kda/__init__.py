@@ -25,7 +25,7 @@ EXPORTS = (
     "k3_kda_scratch", "k3_kda_layer", "k3hip_last_error", "k3hip_version",
     "k3hip_device_count", "k3hip_kda_decode", "k3hip_kda_prep", "k3hip_kda_chunk_workspace",
     "k3hip_kda_chunk", "k3hip_kda_prefill", "k3hip_kda_recurrent", "k3hip_kda_epilogue",
-    "k3hip_kda_upload", "k3hip_kda_release", "k3hip_kda_layer_dev",
+    "k3hip_kda_upload", "k3hip_kda_release", "k3hip_kda_layer_dev", "k3hip_kda_layer_prefill",
 )
 
 
@@ -102,6 +102,7 @@ def lib() -> C.CDLL:
         "k3hip_kda_upload": (i, [C.POINTER(K3KdaW), C.POINTER(K3Cfg), C.POINTER(_P)]),
         "k3hip_kda_release": (i, [_P]),
         "k3hip_kda_layer_dev": (i, [_P, i, _P, _P, _P, _P]),
+        "k3hip_kda_layer_prefill": (i, [_P, i, _P, i, _P, i, _P, _P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -218,6 +219,11 @@ class DeviceWeights:
     def layer(self, out, x, state, T: int, stream=None) -> None:
         _check(lib().k3hip_kda_layer_dev(self.handle, T, _ptr(out), _ptr(x), _ptr(state),
                                          _stream(stream)))
+
+    def layer_prefill(self, out, x, state, T: int, stream=None) -> None:
+        """bf16 full-layer prefill: x, out [T, hidden] float32 or bfloat16 tensors."""
+        _check(lib().k3hip_kda_layer_prefill(self.handle, T, _ptr(out), _dt(out), _ptr(x), _dt(x),
+                                             _ptr(state), _stream(stream)))
 
     def close(self) -> None:
         if self.handle:
