@@ -49,6 +49,14 @@ def prefill_core_flops_per_token(H: int, D: int, C: int) -> float:
     return 2.0 * H * (5 * C * D + 3 * D * D + C * C / 6.0)
 
 
+def layer_flops_per_token(hidden: int, H: int, D: int, C: int) -> float:
+    """Algorithmic flops of the full layer per token: projections q k v g (4P x hidden), f_a
+    (D x hidden), b (H x hidden), f_b (P x D), o_proj (hidden x P), plus the chunked core."""
+    P = H * D
+    return (2.0 * hidden * (4 * P + D + H) + 2.0 * D * P + 2.0 * P * hidden
+            + prefill_core_flops_per_token(H, D, C))
+
+
 def prefill_core_bytes_per_token(H: int, D: int) -> int:
     """Algorithmic HBM bytes of the fused K1+K2 core per token: conv inputs q k v (bf16)
     6*P, gate pre-activation z (fp32) 4*P, beta logits 4*H, o out (fp32) 4*P."""
@@ -263,6 +271,73 @@ def bench_prefill(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
     return out
 
 
+def bench_layer(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
+    """The full k3_kda_layer prefill at c2 on bf16 weights: projections (bf16 MFMA GEMMs),
+    K1, K2, K4, o_proj -- k3hip_kda_layer_prefill, x bf16 in, fp32 out, zero initial state."""
+    import ctypes as C
+    c = PRE
+    E, H, D, T, K = c["hidden"], c["H"], c["D"], c["T"], c["K"]
+    P = H * D
+    g = torch.Generator(device="cuda").manual_seed(0x4B334441 + 2)
+    bf = torch.bfloat16
+    host = {}
+    def mat(name, rows, cols):
+        t = (torch.randn((rows, cols), device="cuda", generator=g) * 0.02).to(bf)
+        host[name] = t.view(torch.int16).cpu().numpy()
+    for n, (r_, c_) in {"q": (P, E), "k": (P, E), "v": (P, E), "g": (P, E), "o": (E, P),
+                        "f_a": (D, E), "f_b": (P, D), "b": (H, E)}.items():
+        mat(n, r_, c_)
+    vec = lambda t: t.float().cpu().numpy().copy()
+    host["q_conv"], host["k_conv"], host["v_conv"] = (
+        vec(torch.randn((P, K), device="cuda", generator=g) * 0.5) for _ in range(3))
+    host["A_log"] = vec(torch.rand((H,), device="cuda", generator=g) * 1.5)
+    host["dt_bias"] = vec(torch.randn((P,), device="cuda", generator=g))
+    host["o_norm"] = vec(1 + 0.1 * torch.randn((D,), device="cuda", generator=g))
+    w = k3.K3KdaW()
+    C.memset(C.byref(w), 0, C.sizeof(w))
+    for n, a in host.items():
+        setattr(w, n, a.ctypes.data)
+    w.wdt = 1
+    cfg = k3.make_cfg(E, H, D, K, c["gate_lb"], c["rms_eps"])
+    dw = k3.DeviceWeights(w, cfg)
+    x = torch.randn((T, E), device="cuda", generator=g).to(bf)
+    out = torch.empty((T, E), device="cuda", dtype=torch.float32)
+    state = torch.zeros(P * D + 3 * P * (K - 1), device="cuda")
+
+    def step():
+        state.zero_()
+        dw.layer_prefill(out, x, state, T)
+
+    step()
+    torch.cuda.synchronize()
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = ev_pair(torch)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    step_s = e0.elapsed_time(e1) * 1e-3 / steps
+    flops = layer_flops_per_token(E, H, D, 64) * T
+    dw.close()
+    out_d = {
+        "value": T / step_s, "unit": "tokens/s", "ms_per_step": step_s * 1e3,
+        "wall_ms_per_step": wall / steps * 1e3,
+        "config": {"workload": "kda_layer_prefill", "hidden": E, "heads": H, "head_dim": D, "T": T,
+                   "chunk": 64, "batch": 1, "conv_k": K, "weights": "bf16", "activations": "bf16 in",
+                   "intermediates": "fp32 (hi/lo bf16 pairs into the f_b and o_proj GEMMs)"},
+        "roofline": {"kernel": "k3hip_kda_layer_prefill (full layer, full-layer accounting)",
+                     "bound": "mfma", "achieved": flops / step_s / 1e12, "peak": BF16_PEAK / 1e12,
+                     "unit": "TFLOP/s", "frac": flops / step_s / BF16_PEAK, "traffic": None,
+                     "flops_per_step": flops},
+    }
+    return out_d
+
+
 def cpu_prefill(torch, q_in, k_in, v_in, z, b_logit, gate, conv, A_log, dt_bias, o_norm) -> dict:
     """orc_kda_core (conv .. gate, the same steps as the GPU step) on the first Ts tokens."""
     import numpy as np
@@ -321,7 +396,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["all", "prefill", "decode", "copy"], default="all",
+    ap.add_argument("--workload", choices=["all", "prefill", "decode", "layer", "copy"], default="all",
                     help="copy: the 1 GiB device copy used to calibrate HBM traffic counters")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     a = ap.parse_args()
@@ -342,7 +417,9 @@ def main() -> int:
         res["decode"] = bench_decode(torch, k3, max(a.steps, 50), a.warmup + 2, not a.no_cpu)
     if a.workload in ("all", "prefill"):
         res["prefill"] = bench_prefill(torch, k3, a.steps, a.warmup, not a.no_cpu)
-    head = res.get("prefill") or res["decode"]
+    if a.workload in ("all", "layer"):
+        res["layer"] = bench_layer(torch, k3, max(3, a.steps // 2), a.warmup, not a.no_cpu)
+    head = res.get("prefill") or res.get("layer") or res["decode"]
     line = {
         "metric": "KDA prefill tokens/s (H=32,d=128,T=8k) + decode state-update GB/s, 1 GPU",
         "value": head["value"], "unit": head["unit"], "n_gpus": 1, "steps": a.steps,
@@ -355,6 +432,8 @@ def main() -> int:
     }
     if "prefill" in res and "decode" in res:
         line["decode"] = res["decode"]
+    if "layer" in res and head is not res["layer"]:
+        line["layer"] = res["layer"]
     print(json.dumps(line))
     return 0
 

@@ -9,8 +9,10 @@
 // column-major terms C^T = W . A^T, i.e. op(A) = T on W (K x N, ld K), op(B) = N on A
 // (K x M, ld K), D = C^T (N x M, ld N).
 //
-// Per device: one handle and one workspace, created on first use; the chosen algorithm is
-// cached per (M, N, K, C dtype). Calls are stream-ordered on the caller's stream.
+// Per device: one handle and one workspace, created on first use. On the first call of a
+// shape (M, N, K, C dtype) up to 8 heuristic candidates are timed on that call's buffers and
+// the fastest is cached; that first call synchronizes its stream (keep it out of graph
+// capture). Later calls are stream-ordered on the caller's stream.
 #include <hipblaslt/hipblaslt.h>
 
 #include <map>
@@ -64,7 +66,12 @@ const char *lt_status(hipblasStatus_t s)
                     __LINE__);                                                           \
     } while (0)
 
-int make_plan(DevGemm &d, int M, int N, int K, int cdt, Plan &p)
+// Candidates from the heuristic, each timed on the call's own buffers (first call of a
+// shape only; that call synchronizes the stream). The fastest is kept.
+constexpr int NCAND = 8;
+
+int make_plan(DevGemm &d, int M, int N, int K, int cdt, Plan &p, const void *A, const void *W,
+              void *Cm, hipStream_t st)
 {
     const hipDataType ct = cdt == K3HIP_BF16 ? HIP_R_16BF : HIP_R_32F;
     K3_LT(hipblasLtMatmulDescCreate(&p.op, HIPBLAS_COMPUTE_32F, HIP_R_32F));
@@ -79,16 +86,45 @@ int make_plan(DevGemm &d, int M, int N, int K, int cdt, Plan &p)
     const uint64_t wmax = GEMM_WS;
     hipblasStatus_t s = hipblasLtMatmulPreferenceSetAttribute(
         pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wmax, sizeof wmax);
-    hipblasLtMatmulHeuristicResult_t res[4];
+    hipblasLtMatmulHeuristicResult_t res[NCAND];
     int n = 0;
     if (s == HIPBLAS_STATUS_SUCCESS)
-        s = hipblasLtMatmulAlgoGetHeuristic(d.h, p.op, p.la, p.lb, p.lc, p.lc, pref, 4, res, &n);
+        s = hipblasLtMatmulAlgoGetHeuristic(d.h, p.op, p.la, p.lb, p.lc, p.lc, pref, NCAND, res, &n);
     (void)hipblasLtMatmulPreferenceDestroy(pref);
     if (s != HIPBLAS_STATUS_SUCCESS || n == 0)
         K3_FAIL(K3HIP_EUNSUPPORTED, "hipBLASLt has no algorithm for %dx%dx%d bf16 GEMM (%s)", M, N,
                 K, lt_status(s));
-    p.algo = res[0].algo;
-    p.ws = res[0].workspaceSize;
+    int best = 0;
+    if (n > 1) {
+        hipEvent_t e0, e1;
+        K3_HIP(hipEventCreate(&e0));
+        K3_HIP(hipEventCreate(&e1));
+        const float alpha = 1.0f, beta = 0.0f;
+        float best_ms = 1e30f;
+        for (int i = 0; i < n; i++) {
+            if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > GEMM_WS) continue;
+            auto run = [&]() {
+                return hipblasLtMatmul(d.h, p.op, &alpha, W, p.la, A, p.lb, &beta, Cm, p.lc, Cm, p.lc,
+                                       &res[i].algo, res[i].workspaceSize ? d.ws : nullptr,
+                                       res[i].workspaceSize, st);
+            };
+            if (run() != HIPBLAS_STATUS_SUCCESS) continue;   // warm-up; skip what fails
+            K3_HIP(hipEventRecord(e0, st));
+            for (int r = 0; r < 3; r++) (void)run();
+            K3_HIP(hipEventRecord(e1, st));
+            K3_HIP(hipEventSynchronize(e1));
+            float ms = 0.0f;
+            K3_HIP(hipEventElapsedTime(&ms, e0, e1));
+            if (ms < best_ms) {
+                best_ms = ms;
+                best = i;
+            }
+        }
+        (void)hipEventDestroy(e0);
+        (void)hipEventDestroy(e1);
+    }
+    p.algo = res[best].algo;
+    p.ws = res[best].workspaceSize;
     return K3HIP_OK;
 }
 
@@ -112,7 +148,7 @@ int gemm_bf16(int M, int N, int K, const void *A, const void *W, void *C, int c_
     auto it = d.plans.find(key);
     if (it == d.plans.end()) {
         Plan p;
-        int rc = make_plan(d, M, N, K, c_dtype, p);
+        int rc = make_plan(d, M, N, K, c_dtype, p, A, W, C, st);
         if (rc) return rc;
         it = d.plans.emplace(key, p).first;
     }
