@@ -224,6 +224,25 @@ int k3hip_kda_layer_dev(const k3hip_kda_weights *w, int T, float *out, const flo
 int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *out, int out_dtype,
                             const void *x, int x_dtype, float *state, void *stream);
 
+/* Device-resident state for a decode loop: the reference's kstate[L * kper] array
+ * (src/cli/k3_run.c:514-567), kper = H*D*D + 3*P*(conv_k-1) floats per layer
+ * (k3_state_geom, src/cli/k3_state.c:23-29), in the same layout on the device. */
+typedef struct k3hip_kda_states k3hip_kda_states;
+size_t k3hip_kda_state_floats(const K3Cfg *c);                       /* kper; 0 on bad cfg */
+int k3hip_kda_states_create(const K3Cfg *c, int n_layers, k3hip_kda_states **out);  /* zeroed */
+int k3hip_kda_states_release(k3hip_kda_states *s);
+/* Device pointer of layer L's slot: the `state` argument of k3hip_kda_layer_dev /
+ * k3hip_kda_layer_prefill. NULL when L is out of range. */
+float *k3hip_kda_states_layer(const k3hip_kda_states *s, int layer);
+int k3hip_kda_states_zero(k3hip_kda_states *s, void *stream);
+/* Spec-decode snapshot / restore (the memcpy of kstate at src/cli/k3_run.c:1969-1984) as a
+ * device-to-device copy between two pools of the same geometry. */
+int k3hip_kda_states_copy(k3hip_kda_states *dst, const k3hip_kda_states *src, void *stream);
+/* Whole array to / from host memory in the reference layout (the payload k3_state_save
+ * writes and k3_state_load fills); both synchronize `stream`. */
+int k3hip_kda_states_download(const k3hip_kda_states *s, float *host, void *stream);
+int k3hip_kda_states_upload(k3hip_kda_states *s, const float *host, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

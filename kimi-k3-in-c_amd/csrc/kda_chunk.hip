@@ -16,11 +16,15 @@
 // the sequential order "decay, delta write, read the UPDATED state".
 //
 // Exponent range. e^(G_t - G_s) for s < t is <= 1, but factoring it into a product of two
-// MFMA operands needs a pivot. Row block a (16 rows) uses the pivot p = 16a: the row
-// factor e^(G_t - G_p) <= 1, the column factor e^(G_p - G_s) is <= 1 for s < p and at
-// most e^(15 |gate_lb|) inside the block. The host only takes this path when
-// 15 |gate_lb| <= 80, so every factor is a normal fp32 / bf16 number. Exponentials are
-// v_exp_f32 (2^x) on G pre-multiplied by log2(e).
+// MFMA operands needs a pivot. Row block a (16 rows) uses the pivot p = 16a + 8, its middle
+// row: the row factor e^(G_t - G_p) and, inside the diagonal block, the column factor
+// e^(G_p - G_s) both lie in [e^(-8 |gate_lb|), e^(8 |gate_lb|)]; for s before the block the
+// column factor is <= 1 and only underflows where the true e^(G_t - G_s) does. Keeping both
+// factors near 1 keeps a factored operand (k or q times its factor) a normal bf16 number
+// for inputs as small as ~1e-20 -- with the pivot at the block's first row the row factor
+// reaches e^(-15 |gate_lb|), and tiny (eps-dominated, unnormalised) q and k then fell into
+// the denormal range, which the MFMA flushes. The host takes this path when
+// 15 |gate_lb| <= 80. Exponentials are v_exp_f32 (2^x) on G pre-multiplied by log2(e).
 //
 // Precision. Every product whose operands are not exact bf16 is a split-bf16 product:
 // x = hi + lo (both bf16), a.b ~ ah.bh + ah.bl + al.bh with fp32 accumulation, i.e. about
@@ -215,7 +219,7 @@ __device__ __forceinline__ void p1_item(float *lds, const float (&vreg)[2][8], c
             for (int e = 0; e < 4; e++) sT[(SB * a + 4 * kg + e) * PA + SB * b + m] = 0.0f;
             continue;
         }
-        const int p = SB * a;        // pivot row
+        const int p = SB * a + 8;    // pivot row: the middle of row block a
         const int t = SB * a + m;    // A-operand row (token t)
         const int s = SB * b + m;    // B-operand row (token s)
         f32x4 akk = 0.0f, aqk = 0.0f;

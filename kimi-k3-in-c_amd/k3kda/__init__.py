@@ -26,6 +26,9 @@ EXPORTS = (
     "k3hip_device_count", "k3hip_kda_decode", "k3hip_kda_prep", "k3hip_kda_chunk_workspace",
     "k3hip_kda_chunk", "k3hip_kda_prefill", "k3hip_kda_recurrent", "k3hip_kda_epilogue",
     "k3hip_kda_upload", "k3hip_kda_release", "k3hip_kda_layer_dev", "k3hip_kda_layer_prefill",
+    "k3hip_kda_state_floats", "k3hip_kda_states_create", "k3hip_kda_states_release",
+    "k3hip_kda_states_layer", "k3hip_kda_states_zero", "k3hip_kda_states_copy",
+    "k3hip_kda_states_download", "k3hip_kda_states_upload",
 )
 
 
@@ -103,6 +106,14 @@ def lib() -> C.CDLL:
         "k3hip_kda_release": (i, [_P]),
         "k3hip_kda_layer_dev": (i, [_P, i, _P, _P, _P, _P]),
         "k3hip_kda_layer_prefill": (i, [_P, i, _P, i, _P, i, _P, _P]),
+        "k3hip_kda_state_floats": (sz, [C.POINTER(K3Cfg)]),
+        "k3hip_kda_states_create": (i, [C.POINTER(K3Cfg), i, C.POINTER(_P)]),
+        "k3hip_kda_states_release": (i, [_P]),
+        "k3hip_kda_states_layer": (_P, [_P, i]),
+        "k3hip_kda_states_zero": (i, [_P, _P]),
+        "k3hip_kda_states_copy": (i, [_P, _P, _P]),
+        "k3hip_kda_states_download": (i, [_P, _P, _P]),
+        "k3hip_kda_states_upload": (i, [_P, _P, _P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -126,6 +137,8 @@ def _ptr(t):
     non-contiguous views: the kernels index dense row-major memory."""
     if t is None:
         return None
+    if isinstance(t, _DevPtr):
+        return C.c_void_p(t.addr)
     if not t.is_cuda:
         raise ValueError("k3kda: device tensor required")
     if not t.is_contiguous():
@@ -228,6 +241,58 @@ class DeviceWeights:
     def close(self) -> None:
         if self.handle:
             lib().k3hip_kda_release(self.handle)
+            self.handle = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class _DevPtr:
+    """A raw device address usable wherever a tensor pointer is expected."""
+
+    def __init__(self, addr: int):
+        self.addr = addr
+
+
+class States:
+    """k3hip_kda_states: per-layer device state slots in the reference kstate layout."""
+
+    def __init__(self, cfg: K3Cfg, n_layers: int):
+        self.handle = C.c_void_p()
+        self.n_layers = n_layers
+        self.kper = int(lib().k3hip_kda_state_floats(C.byref(cfg)))
+        _check(lib().k3hip_kda_states_create(C.byref(cfg), n_layers, C.byref(self.handle)))
+
+    def layer(self, L: int) -> "_DevPtr":
+        p = lib().k3hip_kda_states_layer(self.handle, L)
+        if not p:
+            raise K3HipError(EINVAL, f"layer {L} out of range")
+        return _DevPtr(p)
+
+    def zero(self, stream=None) -> None:
+        _check(lib().k3hip_kda_states_zero(self.handle, _stream(stream)))
+
+    def copy_from(self, other: "States", stream=None) -> None:
+        _check(lib().k3hip_kda_states_copy(self.handle, other.handle, _stream(stream)))
+
+    def download(self):
+        import numpy as np
+        out = np.empty(self.n_layers * self.kper, np.float32)
+        _check(lib().k3hip_kda_states_download(self.handle, out.ctypes.data_as(C.c_void_p), None))
+        return out
+
+    def upload(self, host) -> None:
+        import numpy as np
+        a = np.ascontiguousarray(host, np.float32)
+        assert a.size == self.n_layers * self.kper
+        _check(lib().k3hip_kda_states_upload(self.handle, a.ctypes.data_as(C.c_void_p), None))
+
+    def close(self) -> None:
+        if self.handle:
+            lib().k3hip_kda_states_release(self.handle)
             self.handle = C.c_void_p()
 
     def __del__(self):

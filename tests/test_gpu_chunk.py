@@ -62,6 +62,23 @@ def test_chunk_vs_sequential_oracle(gpu, T, D):
     check(got_o, got_S, want_o, want_S, f"T={T} D={D}")
 
 
+@pytest.mark.parametrize("D", [64, 128])
+def test_chunk_tiny_unnormalised_inputs(gpu, D):
+    """q, k of ~1e-6 (what the L2 norm leaves when eps dominates), v ~1e-9, zero S0, decays
+    at the bound: every factored operand of the intra-chunk products must stay a normal
+    bf16 number. With the pivot at a block's first row this case lost ~4% of the output."""
+    T, H = 200, 2
+    rng = np.random.default_rng(0x4B334441 + 30 + D)
+    q, k, v, g, beta, S0 = inputs(rng, T, H, D)
+    q, k, v = f32(q * 1e-6), f32(k * 1e-6), f32(v * 1e-9)
+    g = f32(np.full_like(g, -5.0) * rng.uniform(0.9, 1.0, g.shape))
+    S0[:] = 0.0
+    qs = float(np.float32(1) / np.sqrt(np.float32(D)))
+    want_o, want_S = sequential(q, k, v, g, beta, S0, qs)
+    got_o, got_S = run_chunk(gpu, q, k, v, g, beta, S0, qs)
+    check(got_o, got_S, want_o, want_S, f"tiny inputs D={D}")
+
+
 def test_chunk_library_workspace_and_zero_state(gpu):
     rng = np.random.default_rng(3)
     T, H, D = 300, 4, 128
