@@ -90,6 +90,16 @@ typedef struct {
     int          wdt;
 } K3KdaW;
 
+/* Field-for-field mirror of the reference K3MlaW (include/k3/k3.h:203-210): gated MLA,
+ * NoPE. Matrices tagged by wdt; the two layernorm weights are fp32; g may be NULL. */
+typedef struct {
+    const void  *q_a, *q_b;                 /* [q_lora][hidden], [H*(nope+rope)][q_lora] */
+    const void  *kv_a, *kv_b;               /* [kv_lora+rope][hidden], [H*(nope+v)][kv_lora] */
+    const void  *o, *g;                     /* [hidden][H*v], [H*v][hidden]  */
+    const float *q_a_norm, *kv_a_norm;      /* [q_lora], [kv_lora]           */
+    int          wdt;
+} K3MlaW;
+
 /* Replaces k3_kda_scratch, include/k3/k3.h:464 (src/core/k3_ops.c:853-862). Returns the
  * same float count, so a caller that sizes scratch from it is unchanged. The GPU path
  * keeps its intermediates in device memory and does not touch the host scratch. */

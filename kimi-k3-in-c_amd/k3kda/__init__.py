@@ -59,6 +59,13 @@ class K3KdaW(C.Structure):
     ]
 
 
+class K3MlaW(C.Structure):
+    """Mirror of the reference K3MlaW (include/k3/k3.h:203-210)."""
+    _fields_ = [("q_a", C.c_void_p), ("q_b", C.c_void_p), ("kv_a", C.c_void_p),
+                ("kv_b", C.c_void_p), ("o", C.c_void_p), ("g", C.c_void_p),
+                ("q_a_norm", C.c_void_p), ("kv_a_norm", C.c_void_p), ("wdt", C.c_int)]
+
+
 def make_cfg(hidden: int, heads: int, head_dim: int, conv_k: int = 4, gate_lb: float = -5.0,
              rms_eps: float = 1e-5) -> K3Cfg:
     c = K3Cfg()

@@ -21,6 +21,8 @@
  *   orc_l2norm         closed form (unit norm); kda_layer1/8.json
  *   orc_kda_layer      kda_layer1/8.json (out + recurrent state); bitwise vs reference
  *   orc_kda_core       equals orc_kda_layer minus the projections (tested by composing)
+ *   orc_mla_cached     mla.json (uncached path, T tokens); the cached path equals the
+ *                      uncached one token by token (tests/test_oracle_golden.py)
  *   orc_kda_decay_softplus  PARITY UNPINNED: the reference has no softplus gate; only
  *                      its closed form is checked. Selected by gate_lb == 0 in orc_kda_core
  *                      and orc_kda_layer (the reference itself would give g = 0 there: no
@@ -403,4 +405,85 @@ void orc_kda_decode_batch(int B, int H, int D, float *S, float *o,
                      beta[p], D, D);
     }
     (void)nthreads;
+}
+
+/* ---------------------------------------------------------------- MLA ---- */
+/* src/core/k3_ops.c:321-424 (k3_mla_cached): gated MLA, NoPE. Per token: q = q_b(rmsnorm(
+ * q_a x)) [H][nope+rope]; ONE projection c = kv_a x gives the latent (rmsnorm'd, the rope
+ * slot excluded) and the shared rope slot; the expanded per-head keys/values
+ * kv = kv_b(latent) [H][nope+v] are cached (kvc [cap][H*(nope+v)], ropec [cap][rope]) or,
+ * with kvc == NULL, kept for this call only. Attention per head, causal over positions
+ * 0..p: score = (float)(double dot over nope + rope) * (nope+rope)^-0.5 in fp32, max,
+ * expf, double sum z, weights (float)(e/z), fp32 weighted sum of values in position order.
+ * Then the gate (sigmoid(g x), multiplied BEFORE o_proj, no norm) and o_proj. */
+void orc_mla_cached(float *out, const float *x, const K3MlaW *w, const K3Cfg *c, int T,
+                    float *kvc, float *ropec, int cached, int cap)
+{
+    const int E = c->hidden, H = c->n_heads;
+    const int qn = c->qk_nope, qr = c->qk_rope, vh = c->v_head;
+    const int qh = qn + qr, kvw = c->kv_lora + qr, kvd = qn + vh;
+    const float scale = 1.0f / sqrtf((float)qh);
+    if (!kvc) cached = 0;
+    const int last = cached + T - 1;
+    if (kvc && last >= cap) {
+        fprintf(stderr, "k3_oracle: MLA cache position %d past capacity %d\n", last, cap);
+        abort();
+    }
+    float *q = (float *)orc_alloc(sizeof(float) * (size_t)T * H * qh, "mla q");
+    float *ct = (float *)orc_alloc(sizeof(float) * (size_t)kvw, "mla ct");
+    float *ql = (float *)orc_alloc(sizeof(float) * (size_t)c->q_lora, "mla ql");
+    float *acc = (float *)orc_alloc(sizeof(float) * (size_t)H * vh, "mla acc");
+    float *gb = (float *)orc_alloc(sizeof(float) * (size_t)H * vh, "mla gate");
+    float *sc = (float *)orc_alloc(sizeof(float) * (size_t)(last + 1), "mla scores");
+    float *kvs = kvc ? NULL : (float *)orc_alloc(sizeof(float) * (size_t)T * H * kvd, "mla kv");
+    float *rps = ropec ? NULL : (float *)orc_alloc(sizeof(float) * (size_t)T * qr + 1, "mla rope");
+#define KV_AT(p) (kvc ? kvc + (size_t)(p) * H * kvd : kvs + (size_t)(p) * H * kvd)
+#define ROPE_AT(p) (ropec ? ropec + (size_t)(p) * qr : rps + (size_t)(p) * qr)
+    for (int t = 0; t < T; t++) {
+        const int p = cached + t;
+        const float *xt = x + (size_t)t * E;
+        orc_mmw(ql, xt, w->q_a, w->wdt, E, c->q_lora);
+        orc_rmsnorm(ql, ql, w->q_a_norm, c->q_lora, c->rms_eps);
+        orc_mmw(q + (size_t)t * H * qh, ql, w->q_b, w->wdt, c->q_lora, H * qh);
+        orc_mmw(ct, xt, w->kv_a, w->wdt, E, kvw);
+        orc_rmsnorm(ct, ct, w->kv_a_norm, c->kv_lora, c->rms_eps);
+        memcpy(ROPE_AT(p), ct + c->kv_lora, (size_t)qr * sizeof(float));
+        orc_mmw(KV_AT(p), ct, w->kv_b, w->wdt, c->kv_lora, H * kvd);
+    }
+    for (int t = 0; t < T; t++) {
+        const int p = cached + t;
+        for (int h = 0; h < H; h++) {
+            const float *qt = q + ((size_t)t * H + h) * qh;
+            float m = -INFINITY;
+            for (int s = 0; s <= p; s++) {
+                const float *ks = KV_AT(s) + (size_t)h * kvd;
+                const float *kr = ROPE_AT(s);
+                double d = 0.0;
+                for (int i = 0; i < qn; i++) d += (double)qt[i] * (double)ks[i];
+                for (int i = 0; i < qr; i++) d += (double)qt[qn + i] * (double)kr[i];
+                sc[s] = (float)d * scale;
+                if (sc[s] > m) m = sc[s];
+            }
+            double z = 0.0;
+            for (int s = 0; s <= p; s++) {
+                sc[s] = expf(sc[s] - m);
+                z += sc[s];
+            }
+            float *o = acc + (size_t)h * vh;
+            for (int j = 0; j < vh; j++) o[j] = 0.0f;
+            for (int s = 0; s <= p; s++) {
+                const float pr = (float)(sc[s] / z);
+                const float *vs = KV_AT(s) + (size_t)h * kvd + qn;
+                for (int j = 0; j < vh; j++) o[j] += pr * vs[j];
+            }
+        }
+        if (w->g) {
+            orc_mmw(gb, x + (size_t)t * E, w->g, w->wdt, E, H * vh);
+            for (int i = 0; i < H * vh; i++) acc[i] *= 1.0f / (1.0f + expf(-gb[i]));
+        }
+        orc_mmw(out + (size_t)t * E, acc, w->o, w->wdt, H * vh, E);
+    }
+#undef KV_AT
+#undef ROPE_AT
+    free(q); free(ct); free(ql); free(acc); free(gb); free(sc); free(kvs); free(rps);
 }

@@ -66,6 +66,10 @@ void   orc_kda_recurrence(int T, int H, int D, float *S, float *o,
                           int nthreads);
 
 /* Round-to-nearest-even fp32 -> bf16 and the exact widening back. */
+/* Gated MLA with an optional expanded KV cache (src/core/k3_ops.c:321-424). */
+void   orc_mla_cached(float *out, const float *x, const K3MlaW *w, const K3Cfg *c, int T,
+                      float *kvc, float *ropec, int cached, int cap);
+
 uint16_t orc_f2bf(float f);
 float    orc_bf2f(uint16_t h);
 

@@ -22,7 +22,7 @@ REF_SO = HERE / "_ref" / "libk3ref.so"
 REF_SRC = Path("/root/reference/src/core/k3_ops.c")
 
 sys.path.insert(0, str(REPO / "kimi-k3-in-c_amd"))
-from k3kda import K3Cfg, K3KdaW, make_cfg  # noqa: E402  (ABI struct mirrors)
+from k3kda import K3Cfg, K3KdaW, K3MlaW, make_cfg  # noqa: E402  (ABI struct mirrors)
 
 _P = C.c_void_p
 
@@ -55,6 +55,12 @@ def _bind(L: C.CDLL, prefix: str) -> C.CDLL:
             "kda_recurrence": (None, [i, i, i, _P, _P, _P, _P, _P, _P, _P, f, i]),
             "l2norm": (None, [_P, i, f]),
             "sigmoid": (f, [f]),
+            "mla_cached": (None, [_P, _P, C.POINTER(K3MlaW), C.POINTER(K3Cfg), i, _P, _P, i, i]),
+        })
+    else:   # the reference's own MLA (src/core/k3_ops.c:321-424) takes a scratch buffer
+        sig.update({
+            "mla_cached": (None, [_P, _P, C.POINTER(K3MlaW), C.POINTER(K3Cfg), i, _P, _P, _P, i, i]),
+            "mla_scratch_cached": (C.c_size_t, [C.POINTER(K3Cfg), i, i, i]),
         })
     for name, (res, args) in sig.items():
         fn = getattr(L, prefix + name)
@@ -197,3 +203,49 @@ def prep(q_in, k_in, v_in, z, b_logit, W: Weights, cfg: K3Cfg, T: int, conv_stat
         else:   # no lower bound: the softplus gate
             L.orc_kda_decay_softplus(gp, ap, zp, ptr(W.arrays["A_log"]), ptr(W.arrays["dt_bias"]), H, D)
     return q, k, v, g, al, beta.reshape(T, H)
+
+
+class MlaWeights:
+    """Numpy arrays for a gated MLA layer and the K3MlaW of pointers into them. Matrices are
+    float32 (wdt 0) or uint16 bf16 bit patterns (wdt 1); the layernorm weights are fp32."""
+
+    MATS = ("q_a", "q_b", "kv_a", "kv_b", "o", "g")
+
+    def __init__(self, arrays: dict, wdt: int = 0):
+        self.arrays = {}
+        for n in self.MATS + ("q_a_norm", "kv_a_norm"):
+            a = arrays.get(n)
+            if a is None:
+                continue
+            self.arrays[n] = np.ascontiguousarray(a) if a.dtype == np.uint16 else f32(a)
+        self.w = K3MlaW()
+        C.memset(C.byref(self.w), 0, C.sizeof(self.w))
+        for n, a in self.arrays.items():
+            setattr(self.w, n, a.ctypes.data)
+        self.w.wdt = wdt
+
+
+def mla_cfg(hidden: int, n_heads: int, q_lora: int, kv_lora: int, qk_nope: int, qk_rope: int,
+            v_head: int, rms_eps: float = 1e-5, gate: int = 1) -> K3Cfg:
+    c = make_cfg(hidden, 1, 16, 1, -5.0, rms_eps)
+    c.n_heads, c.q_lora, c.kv_lora = n_heads, q_lora, kv_lora
+    c.qk_nope, c.qk_rope, c.v_head, c.mla_out_gate = qk_nope, qk_rope, v_head, gate
+    return c
+
+
+def mla(x: np.ndarray, W: MlaWeights, cfg: K3Cfg, T: int, kvc=None, ropec=None, cached: int = 0,
+        cap: int = 0, lib: str = "orc"):
+    """Gated MLA over T tokens (k3_mla_cached); kvc [cap][H*(nope+v)] and ropec [cap][rope]
+    are updated in place when given. lib = "orc" (this restatement) or "ref" (the
+    reference compiled from its own sources)."""
+    out = np.zeros((T, cfg.hidden), np.float32)
+    if lib == "orc":
+        orc().orc_mla_cached(ptr(out), ptr(f32(x)), C.byref(W.w), C.byref(cfg), T, ptr(kvc),
+                             ptr(ropec), cached, cap)
+    else:
+        L = ref()
+        n = L.k3_mla_scratch_cached(C.byref(cfg), T, cap, 1 if kvc is not None else 0)
+        scratch = np.zeros(max(1, n), np.float32)
+        L.k3_mla_cached(ptr(out), ptr(f32(x)), C.byref(W.w), C.byref(cfg), T, ptr(scratch),
+                        ptr(kvc), ptr(ropec), cached, cap)
+    return out

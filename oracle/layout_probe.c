@@ -1,4 +1,4 @@
-/* layout_probe.c - prints sizeof/offsetof of K3Cfg and K3KdaW. TEST INFRASTRUCTURE.
+/* layout_probe.c - prints sizeof/offsetof of K3Cfg, K3KdaW and K3MlaW. TEST INFRASTRUCTURE.
  * Built twice by oracle/Makefile: once against the reference include/k3/k3.h and once
  * (-DMIRROR) against include/k3kda.h; the two outputs must be identical. */
 #include <stddef.h>
@@ -22,5 +22,8 @@ int main(void)
     F(K3KdaW, v_conv); F(K3KdaW, f_a); F(K3KdaW, f_b); F(K3KdaW, A_log);
     F(K3KdaW, dt_bias); F(K3KdaW, b); F(K3KdaW, g); F(K3KdaW, o_norm); F(K3KdaW, o);
     F(K3KdaW, wdt);
+    printf("K3MlaW %zu\n", sizeof(K3MlaW));
+    F(K3MlaW, q_a); F(K3MlaW, q_b); F(K3MlaW, kv_a); F(K3MlaW, kv_b); F(K3MlaW, o);
+    F(K3MlaW, g); F(K3MlaW, q_a_norm); F(K3MlaW, kv_a_norm); F(K3MlaW, wdt);
     return 0;
 }

@@ -167,3 +167,41 @@ def test_oracle_equals_reference_on_fixtures():
         o2 = ko.kda_layer(R, f["in"].reshape(T, -1), W, cfg, T, s2)
         assert np.array_equal(o1.view(np.uint32), o2.view(np.uint32)), fname
         assert np.array_equal(s1.view(np.uint32), s2.view(np.uint32)), fname
+
+
+def mla_from_fixture():
+    r = load_fixture("mla")
+    T, hidden = r["in"].shape[1], r["in"].shape[2]
+    cfg = ko.mla_cfg(hidden, int(r["n_heads"]), int(r["q_lora"]), int(r["kv_lora"]),
+                     int(r["qk_nope"]), int(r["qk_rope"]), int(r["v_head"]), float(r["rms_eps"]))
+    names = {"q_a": "q_a_proj_weight", "q_a_norm": "q_a_layernorm_weight", "q_b": "q_b_proj_weight",
+             "kv_a": "kv_a_proj_with_mqa_weight", "kv_a_norm": "kv_a_layernorm_weight",
+             "kv_b": "kv_b_proj_weight", "o": "o_proj_weight", "g": "g_proj_weight"}
+    W = ko.MlaWeights({k: r[v] for k, v in names.items()}, 0)
+    return r, cfg, W, T
+
+
+def test_mla_fixture():
+    """t_mla (tests/unit/test_ops.c:410-470): the uncached gated MLA over the fixture's T
+    tokens, the softmax scale over the full head width (nope + rope)."""
+    r, cfg, W, T = mla_from_fixture()
+    assert abs(float(r["scale"]) - 1.0 / np.sqrt(cfg.qk_nope + cfg.qk_rope)) < 1e-7
+    x = r["in"].reshape(T, cfg.hidden)
+    libs = ["orc"] + (["ref"] if ko.ref() is not None else [])
+    for lib in libs:
+        y = ko.mla(x, W, cfg, T, lib=lib)
+        assert worst_ratio(y, r["out"].reshape(T, cfg.hidden), ATOL, RTOL) <= 1.0, lib
+
+
+def test_mla_cached_equals_uncached():
+    """The expanded-KV cache path token by token gives the uncached sequence's outputs
+    (the property tests/unit/k3_model.c gates between the two reference paths)."""
+    r, cfg, W, T = mla_from_fixture()
+    x = r["in"].reshape(T, cfg.hidden)
+    want = ko.mla(x, W, cfg, T)
+    H, kvd = cfg.n_heads, cfg.qk_nope + cfg.v_head
+    cap = T + 2
+    kvc = np.zeros((cap, H * kvd), np.float32)
+    ropec = np.zeros((cap, cfg.qk_rope), np.float32)
+    rows = [ko.mla(x[t:t + 1], W, cfg, 1, kvc, ropec, t, cap) for t in range(T)]
+    assert np.array_equal(np.concatenate(rows), want)

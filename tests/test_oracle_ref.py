@@ -126,3 +126,35 @@ def test_shortconv_short_sequence_carries_history():
         ko.orc().orc_shortconv(ptr(y1), ptr(x), ptr(w), ptr(st1), Cn, K, T)
         R.k3_shortconv(ptr(y2), ptr(x), ptr(w), ptr(st2), Cn, K, T)
         assert bits_equal(y1, y2) and bits_equal(st1, st2)
+
+
+@pytest.mark.parametrize("wdt", [0, 1])
+def test_mla_bitwise_vs_reference(wdt):
+    """orc_mla_cached against the reference's k3_mla_cached, built from its own sources:
+    uncached over T tokens, then cached decode steps, fp32 and bf16 weights."""
+    L = ko.ref()
+    if L is None:
+        pytest.skip("reference C not built in this container (no /root/reference)")
+    rng = np.random.default_rng(77 + wdt)
+    hidden, H, ql, kvl, qn, qr, vh = 96, 3, 48, 40, 24, 8, 16
+    cfg = ko.mla_cfg(hidden, H, ql, kvl, qn, qr, vh)
+    mats = {"q_a": (ql, hidden), "q_b": (H * (qn + qr), ql), "kv_a": (kvl + qr, hidden),
+            "kv_b": (H * (qn + vh), kvl), "o": (hidden, H * vh), "g": (H * vh, hidden)}
+    arrays = {n: rng.standard_normal(s).astype(np.float32) * 0.1 for n, s in mats.items()}
+    if wdt:
+        arrays = {n: bf16(a) for n, a in arrays.items()}
+    arrays["q_a_norm"] = (1 + 0.1 * rng.standard_normal(ql)).astype(np.float32)
+    arrays["kv_a_norm"] = (1 + 0.1 * rng.standard_normal(kvl)).astype(np.float32)
+    W = ko.MlaWeights(arrays, wdt)
+    T = 7
+    x = rng.standard_normal((T, hidden)).astype(np.float32)
+    assert np.array_equal(ko.mla(x, W, cfg, T, lib="orc"), ko.mla(x, W, cfg, T, lib="ref"))
+    cap = 12
+    caches = {lib: (np.zeros((cap, H * (qn + vh)), np.float32), np.zeros((cap, qr), np.float32))
+              for lib in ("orc", "ref")}
+    for t in range(5):
+        xt = rng.standard_normal((1, hidden)).astype(np.float32)
+        a = ko.mla(xt, W, cfg, 1, *caches["orc"], t, cap, lib="orc")
+        b = ko.mla(xt, W, cfg, 1, *caches["ref"], t, cap, lib="ref")
+        assert np.array_equal(a, b), t
+    assert np.array_equal(caches["orc"][0], caches["ref"][0])
