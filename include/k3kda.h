@@ -253,6 +253,22 @@ int k3hip_kda_states_copy(k3hip_kda_states *dst, const k3hip_kda_states *src, vo
 int k3hip_kda_states_download(const k3hip_kda_states *s, float *host, void *stream);
 int k3hip_kda_states_upload(k3hip_kda_states *s, const float *host, void *stream);
 
+/* Gated MLA (NoPE) decode with absorbed kv_b, for the hybrid KDA + MLA slice. Replaces the
+ * cached path of k3_mla_cached (src/core/k3_ops.c:321-424) for single-token steps of B
+ * sequences. The cache holds, per sequence and position, the rmsnorm'd compressed latent
+ * (kv_lora floats) followed by the shared rope slot (qk_rope floats) -- not the reference's
+ * expanded per-head keys and values (42x smaller); the attention is the same maths in
+ * another order (W_UK absorbed into q, W_UV applied after the weighted sum).
+ * bf16 weights (K3_WBF16) only. */
+typedef struct k3hip_mla_weights k3hip_mla_weights;
+int k3hip_mla_upload(const K3MlaW *w, const K3Cfg *c, k3hip_mla_weights **out);
+int k3hip_mla_release(k3hip_mla_weights *w);
+size_t k3hip_mla_cache_floats(const K3Cfg *c, int cap);   /* per sequence: cap*(kv_lora+rope) */
+/* x, out [B][hidden] fp32; cache [B][cap][kv_lora+rope] fp32; every sequence holds `pos`
+ * cached positions: the step writes position pos and attends over 0..pos (pos < cap). */
+int k3hip_mla_decode(const k3hip_mla_weights *w, int B, int pos, int cap, float *cache,
+                     const float *x, float *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

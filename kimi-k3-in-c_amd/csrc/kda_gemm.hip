@@ -35,10 +35,12 @@ struct Plan {
     size_t ws = 0;
 };
 
+typedef std::tuple<int, int, int, int, int, int, long, long, long, int, long, long, long> Key;
+
 struct DevGemm {
     hipblasLtHandle_t h = nullptr;
     void *ws = nullptr;
-    std::map<std::tuple<int, int, int, int>, Plan> plans;
+    std::map<Key, Plan> plans;
 };
 
 std::mutex g_mu;
@@ -66,21 +68,38 @@ const char *lt_status(hipblasStatus_t s)
                     __LINE__);                                                           \
     } while (0)
 
+int set_batch(hipblasLtMatrixLayout_t l, int batch, long stride)
+{
+    if (batch <= 1) return K3HIP_OK;
+    const int32_t n = batch;
+    const int64_t st = stride;
+    K3_LT(hipblasLtMatrixLayoutSetAttribute(l, HIPBLASLT_MATRIX_LAYOUT_BATCH_COUNT, &n, sizeof n));
+    K3_LT(hipblasLtMatrixLayoutSetAttribute(l, HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET, &st, sizeof st));
+    return K3HIP_OK;
+}
+
 // Candidates from the heuristic, each timed on the call's own buffers (first call of a
 // shape only; that call synchronizes the stream). The fastest is kept.
 constexpr int NCAND = 8;
 
-int make_plan(DevGemm &d, int M, int N, int K, int cdt, Plan &p, const void *A, const void *W,
-              void *Cm, hipStream_t st)
+int make_plan(DevGemm &d, const GemmDesc &g, Plan &p, const void *A, const void *B, void *Cm,
+              hipStream_t st)
 {
-    const hipDataType ct = cdt == K3HIP_BF16 ? HIP_R_16BF : HIP_R_32F;
+    const hipDataType abt = g.ab_dtype == K3HIP_BF16 ? HIP_R_16BF : HIP_R_32F;
+    const hipDataType ct = g.c_dtype == K3HIP_BF16 ? HIP_R_16BF : HIP_R_32F;
     K3_LT(hipblasLtMatmulDescCreate(&p.op, HIPBLAS_COMPUTE_32F, HIP_R_32F));
-    const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+    // column-major view: C^T (N x M) = op(B') . op(A'), B' = B, A' = A
+    const hipblasOperation_t ta = g.b_trans ? HIPBLAS_OP_T : HIPBLAS_OP_N, tb = HIPBLAS_OP_N;
     K3_LT(hipblasLtMatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof ta));
     K3_LT(hipblasLtMatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof tb));
-    K3_LT(hipblasLtMatrixLayoutCreate(&p.la, HIP_R_16BF, K, N, K));
-    K3_LT(hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_16BF, K, M, K));
-    K3_LT(hipblasLtMatrixLayoutCreate(&p.lc, ct, N, M, N));
+    if (g.b_trans) K3_LT(hipblasLtMatrixLayoutCreate(&p.la, abt, g.K, g.N, g.ldb));
+    else K3_LT(hipblasLtMatrixLayoutCreate(&p.la, abt, g.N, g.K, g.ldb));
+    K3_LT(hipblasLtMatrixLayoutCreate(&p.lb, abt, g.K, g.M, g.lda));
+    K3_LT(hipblasLtMatrixLayoutCreate(&p.lc, ct, g.N, g.M, g.ldc));
+    int rc;
+    if ((rc = set_batch(p.la, g.batch, g.sb)) || (rc = set_batch(p.lb, g.batch, g.sa)) ||
+        (rc = set_batch(p.lc, g.batch, g.sc)))
+        return rc;
     hipblasLtMatmulPreference_t pref = nullptr;
     K3_LT(hipblasLtMatmulPreferenceCreate(&pref));
     const uint64_t wmax = GEMM_WS;
@@ -92,10 +111,10 @@ int make_plan(DevGemm &d, int M, int N, int K, int cdt, Plan &p, const void *A, 
         s = hipblasLtMatmulAlgoGetHeuristic(d.h, p.op, p.la, p.lb, p.lc, p.lc, pref, NCAND, res, &n);
     (void)hipblasLtMatmulPreferenceDestroy(pref);
     if (s != HIPBLAS_STATUS_SUCCESS || n == 0)
-        K3_FAIL(K3HIP_EUNSUPPORTED, "hipBLASLt has no algorithm for %dx%dx%d bf16 GEMM (%s)", M, N,
-                K, lt_status(s));
+        K3_FAIL(K3HIP_EUNSUPPORTED, "hipBLASLt has no algorithm for a %dx%dx%d (batch %d) GEMM (%s)",
+                g.M, g.N, g.K, g.batch, lt_status(s));
     int best = 0;
-    if (n > 1) {
+    if (n > 1 && g.tune) {
         hipEvent_t e0, e1;
         K3_HIP(hipEventCreate(&e0));
         K3_HIP(hipEventCreate(&e1));
@@ -104,7 +123,7 @@ int make_plan(DevGemm &d, int M, int N, int K, int cdt, Plan &p, const void *A, 
         for (int i = 0; i < n; i++) {
             if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > GEMM_WS) continue;
             auto run = [&]() {
-                return hipblasLtMatmul(d.h, p.op, &alpha, W, p.la, A, p.lb, &beta, Cm, p.lc, Cm, p.lc,
+                return hipblasLtMatmul(d.h, p.op, &alpha, B, p.la, A, p.lb, &beta, Cm, p.lc, Cm, p.lc,
                                        &res[i].algo, res[i].workspaceSize ? d.ws : nullptr,
                                        res[i].workspaceSize, st);
             };
@@ -130,33 +149,44 @@ int make_plan(DevGemm &d, int M, int N, int K, int cdt, Plan &p, const void *A, 
 
 }  // namespace
 
-int gemm_bf16(int M, int N, int K, const void *A, const void *W, void *C, int c_dtype, hipStream_t st)
+int gemm(const GemmDesc &g, const void *A, const void *B, void *C, hipStream_t st)
 {
-    if (M <= 0 || N <= 0 || K <= 0) return K3HIP_OK;
-    if (c_dtype != K3HIP_BF16 && c_dtype != K3HIP_F32)
-        K3_FAIL(K3HIP_EINVAL, "gemm_bf16: output dtype %d", c_dtype);
+    if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.batch <= 0) return K3HIP_OK;
+    if ((g.c_dtype != K3HIP_BF16 && g.c_dtype != K3HIP_F32) ||
+        (g.ab_dtype != K3HIP_BF16 && g.ab_dtype != K3HIP_F32))
+        K3_FAIL(K3HIP_EINVAL, "gemm: dtypes %d/%d", g.ab_dtype, g.c_dtype);
     int dev = 0;
     K3_HIP(hipGetDevice(&dev));
-    if (dev < 0 || dev >= MAX_DEV) K3_FAIL(K3HIP_EUNSUPPORTED, "gemm_bf16: device %d", dev);
+    if (dev < 0 || dev >= MAX_DEV) K3_FAIL(K3HIP_EUNSUPPORTED, "gemm: device %d", dev);
     std::lock_guard<std::mutex> lock(g_mu);
     DevGemm &d = g_dev[dev];
     if (!d.h) {
         K3_LT(hipblasLtCreate(&d.h));
         K3_HIP(hipMalloc(&d.ws, GEMM_WS));
     }
-    const auto key = std::make_tuple(M, N, K, c_dtype);
+    const Key key{g.M, g.N, g.K, g.ab_dtype, g.c_dtype, (g.b_trans ? 1 : 0) | (g.tune ? 2 : 0), g.lda,
+                  g.ldb, g.ldc, g.batch, g.sa, g.sb, g.sc};
     auto it = d.plans.find(key);
     if (it == d.plans.end()) {
         Plan p;
-        int rc = make_plan(d, M, N, K, c_dtype, p, A, W, C, st);
+        int rc = make_plan(d, g, p, A, B, C, st);
         if (rc) return rc;
         it = d.plans.emplace(key, p).first;
     }
     const Plan &p = it->second;
     const float alpha = 1.0f, beta = 0.0f;
-    K3_LT(hipblasLtMatmul(d.h, p.op, &alpha, W, p.la, A, p.lb, &beta, C, p.lc, C, p.lc, &p.algo,
+    K3_LT(hipblasLtMatmul(d.h, p.op, &alpha, B, p.la, A, p.lb, &beta, C, p.lc, C, p.lc, &p.algo,
                           p.ws ? d.ws : nullptr, p.ws, st));
     return K3HIP_OK;
+}
+
+int gemm_bf16(int M, int N, int K, const void *A, const void *W, void *C, int c_dtype, hipStream_t st)
+{
+    GemmDesc g;
+    g.M = M; g.N = N; g.K = K;
+    g.ab_dtype = K3HIP_BF16; g.c_dtype = c_dtype; g.b_trans = true;
+    g.lda = K; g.ldb = K; g.ldc = N;
+    return gemm(g, A, W, C, st);
 }
 
 }  // namespace k3kda

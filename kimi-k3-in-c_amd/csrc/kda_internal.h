@@ -9,14 +9,33 @@ namespace k3kda {
 // y[T][out] = W[out][in] . x[T][in] with double accumulation; wdt = K3_WF32 | K3_WBF16.
 int proj(int T, int in, int out, const float *x, const void *W, int wdt, float *y, hipStream_t st);
 
-// C[M][N] = A[M][K] . W[N][K]^T on bf16 MFMA (hipBLASLt), fp32 accumulation; A, W bf16
-// row-major; C bf16 or fp32 (c_dtype) row-major.
+// Row-major C[M][N] = A[M][K] . op(B) with fp32 accumulation (hipBLASLt): op(B) = B^T for
+// B [N][K] (b_trans) or B for B [K][N]; A and B both bf16 or both fp32; C bf16 or fp32;
+// leading dimensions in elements; `batch` strided problems (strides in elements).
+struct GemmDesc {
+    int M = 0, N = 0, K = 0;
+    int ab_dtype = K3HIP_BF16, c_dtype = K3HIP_F32;
+    bool b_trans = true;
+    long lda = 0, ldb = 0, ldc = 0;
+    int batch = 1;
+    long sa = 0, sb = 0, sc = 0;
+    bool tune = true;   // time the heuristic's candidates on the first call of the shape
+};
+int gemm(const GemmDesc &g, const void *A, const void *B, void *C, hipStream_t st);
+
+// C[M][N] = A[M][K] . W[N][K]^T on bf16 MFMA, A, W bf16 row-major, C bf16 or fp32.
 int gemm_bf16(int M, int N, int K, const void *A, const void *W, void *C, int c_dtype, hipStream_t st);
 
 // K4 with y written as a bf16 hi/lo pair into y2 [T][2P] (hi columns 0..P-1, lo P..2P-1),
 // for an o_proj GEMM with K = 2P against [W_o | W_o]. D = 64 / 128, 16-byte aligned.
 int epilogue_split(int T, int H, int D, float eps, const float *o, const void *gate, int gate_dtype,
                    const float *o_norm, void *y2, hipStream_t st);
+
+// x [B][N] fp32 -> y [2B][N] bf16: rows 0..B-1 = hi, rows B..2B-1 = lo = bf16(x - hi), the
+// input of a GEMM that reads each weight once for both halves.
+int split_rows2(const float *x, uint16_t *y, int B, int N, hipStream_t st);
+// y[b][n] = C2[b][n] + C2[B+b][n] (the two halves of such a GEMM).
+int pair_add(const float *C2, float *y, int B, int N, hipStream_t st);
 
 // Stream-ordered scratch: hipMallocAsync on `st`, freed with hipFreeAsync on the same stream.
 struct StreamBuf {

@@ -253,6 +253,43 @@ static unsigned grid_for(size_t n)
     return (unsigned)(b > 8192 ? 8192 : (b ? b : 1));
 }
 
+__global__ void split_rows2_kernel(const float *__restrict__ x, uint16_t *__restrict__ y, size_t BN)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < BN;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const uint16_t hi = f2bf(x[i]);
+        y[i] = hi;
+        y[BN + i] = f2bf(x[i] - __uint_as_float((uint32_t)hi << 16));
+    }
+}
+
+__global__ void pair_add_kernel(const float *__restrict__ C2, float *__restrict__ y, size_t BN)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < BN;
+         i += (size_t)gridDim.x * blockDim.x)
+        y[i] = C2[i] + C2[BN + i];
+}
+
+namespace k3kda {
+int split_rows2(const float *x, uint16_t *y, int B, int N, hipStream_t st)
+{
+    const size_t n = (size_t)B * N;
+    if (!n) return K3HIP_OK;
+    hipLaunchKernelGGL(split_rows2_kernel, dim3(grid_for(n)), dim3(256), 0, st, x, y, n);
+    K3_LAUNCHED();
+    return K3HIP_OK;
+}
+
+int pair_add(const float *C2, float *y, int B, int N, hipStream_t st)
+{
+    const size_t n = (size_t)B * N;
+    if (!n) return K3HIP_OK;
+    hipLaunchKernelGGL(pair_add_kernel, dim3(grid_for(n)), dim3(256), 0, st, C2, y, n);
+    K3_LAUNCHED();
+    return K3HIP_OK;
+}
+}  // namespace k3kda
+
 extern "C" int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *out, int out_dtype,
                                        const void *x, int x_dtype, float *state, void *stream)
 {

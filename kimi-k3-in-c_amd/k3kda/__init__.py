@@ -29,6 +29,7 @@ EXPORTS = (
     "k3hip_kda_state_floats", "k3hip_kda_states_create", "k3hip_kda_states_release",
     "k3hip_kda_states_layer", "k3hip_kda_states_zero", "k3hip_kda_states_copy",
     "k3hip_kda_states_download", "k3hip_kda_states_upload",
+    "k3hip_mla_upload", "k3hip_mla_release", "k3hip_mla_cache_floats", "k3hip_mla_decode",
 )
 
 
@@ -121,6 +122,10 @@ def lib() -> C.CDLL:
         "k3hip_kda_states_copy": (i, [_P, _P, _P]),
         "k3hip_kda_states_download": (i, [_P, _P, _P]),
         "k3hip_kda_states_upload": (i, [_P, _P, _P]),
+        "k3hip_mla_upload": (i, [C.POINTER(K3MlaW), C.POINTER(K3Cfg), C.POINTER(_P)]),
+        "k3hip_mla_release": (i, [_P]),
+        "k3hip_mla_cache_floats": (sz, [C.POINTER(K3Cfg), i]),
+        "k3hip_mla_decode": (i, [_P, i, i, i, _P, _P, _P, _P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -300,6 +305,31 @@ class States:
     def close(self) -> None:
         if self.handle:
             lib().k3hip_kda_states_release(self.handle)
+            self.handle = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class MlaWeights:
+    """k3hip_mla_upload / k3hip_mla_release around a K3MlaW of host pointers."""
+
+    def __init__(self, w: "K3MlaW", cfg: K3Cfg):
+        self.handle = C.c_void_p()
+        _check(lib().k3hip_mla_upload(C.byref(w), C.byref(cfg), C.byref(self.handle)))
+
+    def decode(self, out, x, cache, pos: int, cap: int, stream=None) -> None:
+        """One step for B = x.shape[0] sequences: x, out [B, hidden] fp32, cache
+        [B, cap, kv_lora + rope] fp32 holding `pos` positions per sequence."""
+        _check(lib().k3hip_mla_decode(self.handle, x.shape[0], pos, cap, _ptr(cache), _ptr(x),
+                                      _ptr(out), _stream(stream)))
+
+    def close(self) -> None:
+        if self.handle:
+            lib().k3hip_mla_release(self.handle)
             self.handle = C.c_void_p()
 
     def __del__(self):

@@ -1,0 +1,80 @@
+# SPDX-License-Identifier: Apache-2.0
+"""Gated MLA decode with absorbed weights (k3hip_mla_decode) against the oracle's
+expanded-KV restatement of k3_mla_cached (src/core/k3_ops.c:321-424), which is itself
+pinned to the reference's mla.json fixture and to the reference C bit for bit.
+
+B sequences decode token by token from an empty cache: the GPU keeps the compressed latent
+per position, the oracle the expanded per-head keys and values, one cache per sequence.
+Every output of every step is compared at the decode bar (rtol 1e-4, atol 1e-4 * rms):
+the two orders of the same maths differ by fp32 rounding only."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import assert_close, worst_ratio
+from test_oracle_ref import bf16
+import k3_oracle as ko
+
+pytestmark = pytest.mark.gpu
+
+
+def rms(a):
+    return float(np.sqrt(np.mean(np.asarray(a, np.float64) ** 2)))
+
+
+def mla_case(rng, hidden, H, ql, kvl, qn, qr, vh, gate=1):
+    cfg = ko.mla_cfg(hidden, H, ql, kvl, qn, qr, vh, 1e-5, gate)
+    mats = {"q_a": (ql, hidden), "q_b": (H * (qn + qr), ql), "kv_a": (kvl + qr, hidden),
+            "kv_b": (H * (qn + vh), kvl), "o": (hidden, H * vh), "g": (H * vh, hidden)}
+    arrays = {n: bf16(rng.standard_normal(s) * (0.5 / np.sqrt(s[1]))) for n, s in mats.items()}
+    if not gate:
+        del arrays["g"]
+    arrays["q_a_norm"] = (1 + 0.1 * rng.standard_normal(ql)).astype(np.float32)
+    arrays["kv_a_norm"] = (1 + 0.1 * rng.standard_normal(kvl)).astype(np.float32)
+    return cfg, ko.MlaWeights(arrays, 1)
+
+
+@pytest.mark.parametrize("hidden,H,ql,kvl,qn,qr,vh,B,T,gate", [
+    (256, 4, 64, 64, 32, 16, 32, 3, 9, 1),
+    (384, 8, 96, 128, 64, 32, 64, 17, 6, 1),     # B above one absorb pass of 16
+    (128, 2, 32, 32, 16, 8, 16, 2, 40, 0),       # ungated, longer context
+])
+def test_mla_decode_vs_expanded_oracle(gpu, hidden, H, ql, kvl, qn, qr, vh, B, T, gate):
+    import torch
+    rng = np.random.default_rng(0x4B334441 + 4 + hidden + B + T)
+    cfg, W = mla_case(rng, hidden, H, ql, kvl, qn, qr, vh, gate)
+    cap = T + 3
+    kvcs = [np.zeros((cap, H * (qn + vh)), np.float32) for _ in range(B)]
+    ropecs = [np.zeros((cap, qr), np.float32) for _ in range(B)]
+    mw = gpu.MlaWeights(W.w, cfg)
+    cache = torch.zeros((B, cap, kvl + qr), device="cuda")
+    worst = 0.0
+    for t in range(T):
+        x = rng.standard_normal((B, hidden)).astype(np.float32)
+        want = np.concatenate([ko.mla(x[b:b + 1], W, cfg, 1, kvcs[b], ropecs[b], t, cap) for b in range(B)])
+        out = torch.full((B, hidden), float("nan"), device="cuda")
+        mw.decode(out, torch.from_numpy(x).cuda(), cache, t, cap)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        assert_close(got, want, 1e-4 * rms(want), 1e-4, f"MLA step {t}")
+        worst = max(worst, worst_ratio(got, want, 1e-4 * rms(want), 1e-4))
+    print(f"hidden={hidden} H={H} B={B} T={T} gate={gate}: worst {worst:.3f}x of the 1e-4 bar")
+    mw.close()
+
+
+def test_mla_refusals(gpu):
+    import torch
+    rng = np.random.default_rng(5)
+    cfg, W = mla_case(rng, 128, 2, 32, 32, 16, 8, 16)
+    mw = gpu.MlaWeights(W.w, cfg)
+    cache = torch.zeros((1, 4, 40), device="cuda")
+    x, out = torch.zeros((1, 128), device="cuda"), torch.zeros((1, 128), device="cuda")
+    with pytest.raises(gpu.K3HipError) as e:
+        mw.decode(out, x, cache, 4, 4)          # position past the cache
+    assert e.value.code == 1
+    mw.close()
+    W32 = ko.MlaWeights({n: a for n, a in W.arrays.items()}, 0)   # fp32 tag: not supported
+    with pytest.raises(gpu.K3HipError) as e:
+        gpu.MlaWeights(W32.w, cfg)
+    assert e.value.code == 3
