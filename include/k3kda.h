@@ -234,6 +234,15 @@ int k3hip_kda_layer_dev(const k3hip_kda_weights *w, int T, float *out, const flo
 int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *out, int out_dtype,
                             const void *x, int x_dtype, float *state, void *stream);
 
+/* One decode token for each of B sequences through the whole layer on bf16 weights: the
+ * per-token path of k3_kda_layer (src/core/k3_ops.c:864-951, T = 1) batched over
+ * sequences. The projections read each weight once for all B (bf16 MFMA, the fp32 input
+ * as a bf16 hi/lo pair); sequence b's state (S then conv history, the reference layout)
+ * starts at states + b * state_stride floats (>= H*D*D + 3*P*(conv_k-1), a multiple of 4).
+ * x, out [B][hidden] fp32. */
+int k3hip_kda_layer_decode(const k3hip_kda_weights *w, int B, float *out, const float *x,
+                           float *states, long state_stride, void *stream);
+
 /* Device-resident state for a decode loop: the reference's kstate[L * kper] array
  * (src/cli/k3_run.c:514-567), kper = H*D*D + 3*P*(conv_k-1) floats per layer
  * (k3_state_geom, src/cli/k3_state.c:23-29), in the same layout on the device. */

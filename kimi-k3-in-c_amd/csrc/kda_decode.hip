@@ -20,7 +20,7 @@
 // Element arithmetic is kept in the reference's order with contraction off (decay
 // multiply, then products added separately); only the summation order of the two row
 // reductions differs (per-thread partial sums, then across row slots).
-#include "k3kda_common.h"
+#include "kda_internal.h"
 
 namespace k3kda {
 
@@ -28,7 +28,7 @@ template <int D, int NT>
 __global__ __launch_bounds__(NT) void kda_decode_kernel(
     float *__restrict__ S, float *__restrict__ o, const float *__restrict__ q,
     const float *__restrict__ k, const float *__restrict__ v, const float *__restrict__ alpha,
-    const float *__restrict__ beta, float q_scale)
+    const float *__restrict__ beta, float q_scale, int H, long s_stride)
 {
 #pragma clang fp contract(off)
     constexpr int CPR = D / 4;      // float4 column groups per row
@@ -51,7 +51,8 @@ __global__ __launch_bounds__(NT) void kda_decode_kernel(
         s_q[tid] = q[vo + tid] * q_scale;
         s_a[tid] = alpha[vo + tid];
     }
-    f4 *Sp = reinterpret_cast<f4 *>(S + (size_t)pair * D * D);
+    // sequence pair / H's state starts s_stride floats after the previous one's
+    f4 *Sp = reinterpret_cast<f4 *>(S + (size_t)(pair / H) * s_stride + (size_t)(pair % H) * D * D);
     f4 s[NPASS];
 #pragma unroll
     for (int m = 0; m < NPASS; m++) s[m] = Sp[(rs + m * RPP) * CPR + cg];
@@ -102,12 +103,30 @@ __global__ __launch_bounds__(NT) void kda_decode_kernel(
 template <int D, int NT>
 static int launch_decode(int pairs, float *S, float *o, const float *q, const float *k,
                          const float *v, const float *alpha, const float *beta, float qs,
-                         hipStream_t st)
+                         int H, long s_stride, hipStream_t st)
 {
     hipLaunchKernelGGL((kda_decode_kernel<D, NT>), dim3(pairs), dim3(NT), 0, st, S, o, q, k,
-                       v, alpha, beta, qs);
+                       v, alpha, beta, qs, H, s_stride);
     K3_LAUNCHED();
     return K3HIP_OK;
+}
+
+int decode_strided(int B, int H, int D, float *S, long s_stride, float *o, const float *q,
+                   const float *k, const float *v, const float *alpha, const float *beta,
+                   float qs, hipStream_t st)
+{
+    const long pairs = (long)B * H;
+    if (pairs == 0) return K3HIP_OK;
+    if (pairs > 0x7fffffffL) K3_FAIL(K3HIP_EINVAL, "decode: B*H=%ld too large", pairs);
+    if (!is_pow2_head(D)) K3_FAIL(K3HIP_EUNSUPPORTED, "decode: D=%d not in {16,32,64,128}", D);
+    if (s_stride < (long)H * D * D || (s_stride & 3) || (((uintptr_t)S | (uintptr_t)o | (uintptr_t)v) & 15))
+        K3_FAIL(K3HIP_EINVAL, "decode: state stride %ld or alignment", s_stride);
+    switch (D) {
+    case 16: return launch_decode<16, 64>((int)pairs, S, o, q, k, v, alpha, beta, qs, H, s_stride, st);
+    case 32: return launch_decode<32, 128>((int)pairs, S, o, q, k, v, alpha, beta, qs, H, s_stride, st);
+    case 64: return launch_decode<64, 256>((int)pairs, S, o, q, k, v, alpha, beta, qs, H, s_stride, st);
+    default: return launch_decode<128, 256>((int)pairs, S, o, q, k, v, alpha, beta, qs, H, s_stride, st);
+    }
 }
 
 }  // namespace k3kda
@@ -128,11 +147,6 @@ extern "C" int k3hip_kda_decode(int B, int H, int D, float *S, float *o, const f
         K3_FAIL(K3HIP_EINVAL, "k3hip_kda_decode: NULL tensor");
     if (((uintptr_t)S | (uintptr_t)o | (uintptr_t)v) & 15)
         K3_FAIL(K3HIP_EINVAL, "k3hip_kda_decode: S, o and v must be 16-byte aligned");
-    hipStream_t st = as_stream(stream);
-    switch (D) {
-    case 16: return launch_decode<16, 64>((int)pairs, S, o, q, k, v, alpha, beta, q_scale, st);
-    case 32: return launch_decode<32, 128>((int)pairs, S, o, q, k, v, alpha, beta, q_scale, st);
-    case 64: return launch_decode<64, 256>((int)pairs, S, o, q, k, v, alpha, beta, q_scale, st);
-    default: return launch_decode<128, 256>((int)pairs, S, o, q, k, v, alpha, beta, q_scale, st);
-    }
+    return decode_strided(B, H, D, S, (long)H * D * D, o, q, k, v, alpha, beta, q_scale,
+                          as_stream(stream));
 }

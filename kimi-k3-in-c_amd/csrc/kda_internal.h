@@ -37,6 +37,11 @@ int split_rows2(const float *x, uint16_t *y, int B, int N, hipStream_t st);
 // y[b][n] = C2[b][n] + C2[B+b][n] (the two halves of such a GEMM).
 int pair_add(const float *C2, float *y, int B, int N, hipStream_t st);
 
+// K3 over B sequences whose [H][D][D] states start s_stride floats apart (decode slots).
+int decode_strided(int B, int H, int D, float *S, long s_stride, float *o, const float *q,
+                   const float *k, const float *v, const float *alpha, const float *beta,
+                   float qs, hipStream_t st);
+
 // Stream-ordered scratch: hipMallocAsync on `st`, freed with hipFreeAsync on the same stream.
 struct StreamBuf {
     void *p = nullptr;

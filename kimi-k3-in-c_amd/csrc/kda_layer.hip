@@ -16,6 +16,7 @@
 #include <string.h>
 
 #include "kda_internal.h"
+#include "kda_prep_math.h"
 
 namespace k3kda {
 
@@ -371,6 +372,177 @@ extern "C" int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *
     if ((rc = epilogue_split(T, H, D, w->rms_eps, o, gl, K3HIP_F32, w->o_norm, y2, st))) return rc;
     // 9 o_proj: K = 2P against [W_o | W_o]
     return gemm_bf16(T, E, 2 * (int)P, y2, w->o2, out, out_dtype, st);
+}
+
+// ------------------------------------------------------------- batched decode ----
+// K1 for one token of each of B sequences, reading the projections as the two halves of a
+// hi/lo row-split GEMM (C2 [2B][N]: rows b and B+b summed), with sequence b's conv history
+// in its state slot (states + b*stride + H*D*D, [3][P][K-1], oldest first; shifted in
+// place). One wave per (head, sequence); lanes own D/64 adjacent channels (D >= 64) or one.
+// Arithmetic of kda_prep_math.h; L2 sums fp32 per lane, double across the wave.
+template <int D, int K>
+__global__ __launch_bounds__(64) void kda_step_prep_kernel(
+    int B, int H, float lb, const float *__restrict__ Cq, const float *__restrict__ Ck,
+    const float *__restrict__ Cv, const float *__restrict__ Cz, const float *__restrict__ Cb,
+    const float *__restrict__ q_conv, const float *__restrict__ k_conv,
+    const float *__restrict__ v_conv, const float *__restrict__ A_log,
+    const float *__restrict__ dt_bias, float *__restrict__ states, long stride,
+    float *__restrict__ q, float *__restrict__ k, float *__restrict__ v,
+    float *__restrict__ alpha, float *__restrict__ beta)
+{
+#pragma clang fp contract(off)
+    constexpr int CPL = D >= 64 ? D / 64 : 1, NH = K - 1;
+    const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+    const bool active = lane * CPL < D;
+    const size_t P = (size_t)H * D;
+    const size_t c0 = (size_t)h * D + (active ? lane * CPL : 0);
+    float *hist = states + (size_t)b * stride + (size_t)H * D * D;
+    const float *C2[3] = {Cq, Ck, Cv};
+    const float *cw[3] = {q_conv, k_conv, v_conv};
+    float *outp[3] = {q, k, v};
+    float y[3][CPL];
+#pragma unroll
+    for (int t = 0; t < 3; t++)
+#pragma unroll
+        for (int e = 0; e < CPL; e++) {
+            const size_t ch = c0 + e;
+            const float x = C2[t][(size_t)b * P + ch] + C2[t][(size_t)(B + b) * P + ch];
+            float w[K], win[NH > 0 ? NH : 1];
+#pragma unroll
+            for (int j = 0; j < K; j++) w[j] = cw[t][ch * K + j];
+            float *hs = hist + ((size_t)t * P + ch) * NH;
+#pragma unroll
+            for (int j = 0; j < NH; j++) win[j] = hs[j];
+            y[t][e] = conv_silu<K>(w, win, x);
+            if (active) {
+#pragma unroll
+                for (int j = 0; j + 1 < NH; j++) hs[j] = win[j + 1];
+                if constexpr (NH > 0) hs[NH - 1] = x;
+            }
+        }
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        float part = 0.0f;
+#pragma unroll
+        for (int e = 0; e < CPL; e++) part = part + (active ? y[t][e] * y[t][e] : 0.0f);
+        double ss = (double)part;
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+        const float r = (float)(1.0 / sqrt(ss + 1e-6));
+#pragma unroll
+        for (int e = 0; e < CPL; e++) y[t][e] = y[t][e] * r;
+    }
+    const float a = expf(A_log[h]);
+    if (active) {
+#pragma unroll
+        for (int e = 0; e < CPL; e++) {
+            const size_t ch = c0 + e, at = (size_t)b * P + ch;
+            for (int t = 0; t < 3; t++) outp[t][at] = y[t][e];
+            const float z = Cz[(size_t)b * P + ch] + Cz[(size_t)(B + b) * P + ch];
+            const float g = lb != 0.0f ? gate_bounded(lb, a, z, dt_bias[ch])
+                                       : -a * softplus_ref(z + dt_bias[ch]);
+            alpha[at] = fast_exp(g);
+        }
+    }
+    if (lane == 0)
+        beta[(size_t)b * H + h] = fast_sigmoid(Cb[(size_t)b * H + h] + Cb[(size_t)(B + b) * H + h]);
+}
+
+template <int D>
+static int step_prep_k(int K, dim3 grid, hipStream_t st, int B, int H, float lb, const float *Cq,
+                       const float *Ck, const float *Cv, const float *Cz, const float *Cb,
+                       const k3hip_kda_weights *w, float *states, long stride, float *q, float *k,
+                       float *v, float *al, float *beta)
+{
+#define K3_STEP(KK) hipLaunchKernelGGL((kda_step_prep_kernel<D, KK>), grid, dim3(64), 0, st, B, H, lb, Cq, Ck, Cv, Cz, Cb, w->q_conv, w->k_conv, w->v_conv, w->A_log, w->dt_bias, states, stride, q, k, v, al, beta)
+    switch (K) {
+    case 1: K3_STEP(1); break;
+    case 2: K3_STEP(2); break;
+    case 3: K3_STEP(3); break;
+    case 4: K3_STEP(4); break;
+    default: K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_layer_decode: conv_k=%d not in 1..4", K);
+    }
+#undef K3_STEP
+    K3_LAUNCHED();
+    return K3HIP_OK;
+}
+
+extern "C" int k3hip_kda_layer_decode(const k3hip_kda_weights *w, int B, float *out, const float *x,
+                                      float *states, long state_stride, void *stream)
+{
+    clear_error();
+    if (!w || !out || !x || !states) K3_FAIL(K3HIP_EINVAL, "k3hip_kda_layer_decode: NULL argument");
+    if (B < 0) K3_FAIL(K3HIP_EINVAL, "k3hip_kda_layer_decode: B=%d", B);
+    if (B == 0) return K3HIP_OK;
+    if (w->wdt != K3_WBF16)
+        K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_layer_decode: bf16 weights only (use k3hip_kda_layer_dev)");
+    const int E = w->hidden, H = w->H, D = w->D, K = w->K;
+    const size_t P = (size_t)H * D;
+    const long kper = (long)(P * D + 3 * P * (size_t)(K - 1));
+    if (!is_pow2_head(D) || K < 1 || K > 4)
+        K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_layer_decode: D=%d conv_k=%d", D, K);
+    if (state_stride < kper || (state_stride & 3) || ((uintptr_t)states & 15))
+        K3_FAIL(K3HIP_EINVAL, "k3hip_kda_layer_decode: state stride %ld < %ld floats or misaligned",
+                state_stride, kper);
+    hipStream_t st = as_stream(stream);
+    const size_t BP = (size_t)B * P;
+    // scratch: x hi/lo | q k v g halves | b halves | f_a halves | f_a | f_a hi/lo | z halves |
+    //          q k v alpha | beta | gate logits | o | y | y hi/lo | out halves
+    size_t sizes[] = {(size_t)2 * B * E * 2, 4 * 2 * BP * 4, (size_t)2 * B * H * 4, (size_t)2 * B * D * 4,
+                      (size_t)B * D * 4, (size_t)2 * B * D * 2, 2 * BP * 4, 4 * BP * 4, (size_t)B * H * 4,
+                      BP * 4, BP * 4, BP * 4, 2 * BP * 2, (size_t)2 * B * E * 4};
+    constexpr int NB = sizeof sizes / sizeof sizes[0];
+    size_t off[NB], total = 0;
+    for (int i = 0; i < NB; i++) {
+        off[i] = total;
+        total += (sizes[i] + 255) & ~(size_t)255;
+    }
+    StreamBuf buf;
+    int rc = stream_alloc(buf, total, st);
+    if (rc) return rc;
+    char *bs = (char *)buf.p;
+    uint16_t *xs = (uint16_t *)(bs + off[0]);
+    float *Cq = (float *)(bs + off[1]), *Ck = Cq + 2 * BP, *Cv = Ck + 2 * BP, *Cg = Cv + 2 * BP;
+    float *Cb = (float *)(bs + off[2]), *Cfa = (float *)(bs + off[3]), *fa = (float *)(bs + off[4]);
+    uint16_t *fa2 = (uint16_t *)(bs + off[5]);
+    float *Cz = (float *)(bs + off[6]);
+    float *q = (float *)(bs + off[7]), *k = q + BP, *v = k + BP, *al = v + BP;
+    float *beta = (float *)(bs + off[8]), *gl = (float *)(bs + off[9]), *o = (float *)(bs + off[10]);
+    float *y = (float *)(bs + off[11]);
+    uint16_t *ys = (uint16_t *)(bs + off[12]);
+    float *out2 = (float *)(bs + off[13]);
+
+    // 1 projections, each weight read once for both halves of the split input
+    if ((rc = split_rows2(x, xs, B, E, st))) return rc;
+    if ((rc = gemm_bf16(2 * B, (int)P, E, xs, w->q, Cq, K3HIP_F32, st))) return rc;
+    if ((rc = gemm_bf16(2 * B, (int)P, E, xs, w->k, Ck, K3HIP_F32, st))) return rc;
+    if ((rc = gemm_bf16(2 * B, (int)P, E, xs, w->v, Cv, K3HIP_F32, st))) return rc;
+    if ((rc = gemm_bf16(2 * B, (int)P, E, xs, w->g, Cg, K3HIP_F32, st))) return rc;
+    if ((rc = gemm_bf16(2 * B, H, E, xs, w->b, Cb, K3HIP_F32, st))) return rc;
+    if ((rc = gemm_bf16(2 * B, D, E, xs, w->f_a, Cfa, K3HIP_F32, st))) return rc;
+    if ((rc = pair_add(Cfa, fa, B, D, st))) return rc;
+    if ((rc = split_rows2(fa, fa2, B, D, st))) return rc;
+    if ((rc = gemm_bf16(2 * B, (int)P, D, fa2, w->f_b, Cz, K3HIP_F32, st))) return rc;
+    // 2-5 K1 on one token per sequence, conv history carried in each slot
+    const dim3 grid(H, B);
+    switch (D) {
+    case 16: rc = step_prep_k<16>(K, grid, st, B, H, w->gate_lb, Cq, Ck, Cv, Cz, Cb, w, states, state_stride, q, k, v, al, beta); break;
+    case 32: rc = step_prep_k<32>(K, grid, st, B, H, w->gate_lb, Cq, Ck, Cv, Cz, Cb, w, states, state_stride, q, k, v, al, beta); break;
+    case 64: rc = step_prep_k<64>(K, grid, st, B, H, w->gate_lb, Cq, Ck, Cv, Cz, Cb, w, states, state_stride, q, k, v, al, beta); break;
+    default: rc = step_prep_k<128>(K, grid, st, B, H, w->gate_lb, Cq, Ck, Cv, Cz, Cb, w, states, state_stride, q, k, v, al, beta); break;
+    }
+    if (rc) return rc;
+    // 6 K3 on the B slots
+    if ((rc = decode_strided(B, H, D, states, state_stride, o, q, k, v, al, beta,
+                             1.0f / sqrtf((float)D), st)))
+        return rc;
+    // 7-8 K4, 9 o_proj
+    if ((rc = pair_add(Cg, gl, B, (int)P, st))) return rc;
+    if ((rc = k3hip_kda_epilogue(B, H, D, w->rms_eps, o, gl, K3HIP_F32, w->o_norm, y, K3HIP_F32, stream)))
+        return rc;
+    if ((rc = split_rows2(y, ys, B, (int)P, st))) return rc;
+    if ((rc = gemm_bf16(2 * B, E, (int)P, ys, w->o, out2, K3HIP_F32, st))) return rc;
+    return pair_add(out2, out, B, E, st);
 }
 
 // ------------------------------------------------------------------ drop-in ----

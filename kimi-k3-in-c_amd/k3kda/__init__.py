@@ -30,6 +30,7 @@ EXPORTS = (
     "k3hip_kda_states_layer", "k3hip_kda_states_zero", "k3hip_kda_states_copy",
     "k3hip_kda_states_download", "k3hip_kda_states_upload",
     "k3hip_mla_upload", "k3hip_mla_release", "k3hip_mla_cache_floats", "k3hip_mla_decode",
+    "k3hip_kda_layer_decode",
 )
 
 
@@ -126,6 +127,7 @@ def lib() -> C.CDLL:
         "k3hip_mla_release": (i, [_P]),
         "k3hip_mla_cache_floats": (sz, [C.POINTER(K3Cfg), i]),
         "k3hip_mla_decode": (i, [_P, i, i, i, _P, _P, _P, _P]),
+        "k3hip_kda_layer_decode": (i, [_P, i, _P, _P, _P, C.c_long, _P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -244,6 +246,11 @@ class DeviceWeights:
     def layer(self, out, x, state, T: int, stream=None) -> None:
         _check(lib().k3hip_kda_layer_dev(self.handle, T, _ptr(out), _ptr(x), _ptr(state),
                                          _stream(stream)))
+
+    def layer_decode(self, out, x, states, stride: int, stream=None) -> None:
+        """One token for each of B = x.shape[0] sequences; states: B slots `stride` floats apart."""
+        _check(lib().k3hip_kda_layer_decode(self.handle, x.shape[0], _ptr(out), _ptr(x),
+                                            _ptr(states), stride, _stream(stream)))
 
     def layer_prefill(self, out, x, state, T: int, stream=None) -> None:
         """bf16 full-layer prefill: x, out [T, hidden] float32 or bfloat16 tensors."""

@@ -14,6 +14,8 @@
 - Decode after a prefill of T equals a prefill of T+1 (last row).
 - A_log shipped as [128] with a non-zero tail: only the first H values are per-head
   (src/model/k3_bind.c:212-216, k3_bind.h:29-31); the tail must not change anything.
+- The batched decode layer (k3hip_kda_layer_decode): B sequences, one token each, states in
+  strided slots, against the oracle's k3_kda_layer per sequence at the decode bar.
 """
 from __future__ import annotations
 
@@ -176,3 +178,47 @@ def test_a_log_per_head_binding(gpu):
     assert torch.equal(outs[0], outs[1]), "A_log beyond the first H heads changed the output"
     want = ko.kda_layer(ko.orc(), x.cpu().numpy(), W128, cfg, 20, None)   # oracle reads A_log[h] too
     assert_close(outs[1].cpu().numpy(), want, 2e-3 * rms(want), 2e-3, "128-entry A_log vs oracle")
+
+
+@pytest.mark.parametrize("D,K,B,lb", [(64, 4, 5, -5.0), (128, 3, 3, -5.0), (32, 4, 2, 0.0)])
+def test_batched_layer_decode_vs_oracle(gpu, D, K, B, lb):
+    """k3hip_kda_layer_decode: B sequences, one token each per step, states in B slots of a
+    strided array (stride > kper), bf16 weights; each sequence against the oracle's
+    k3_kda_layer with T = 1 on its own state, at the decode bar (rtol 1e-4, atol 1e-4*rms).
+    The lb = 0 case runs the unbounded softplus gate (parity unpinned)."""
+    import torch
+    from test_oracle_ref import bf16
+    rng = np.random.default_rng(0x4B334441 + 25 + D + B)
+    Hh, hid = 3, 192
+    P = Hh * D
+    cfg = ko.make_cfg(hid, Hh, D, K, lb, 1e-5)
+    nrm = lambda *s: rng.standard_normal(s) * 0.05
+    arrays = {n: bf16(nrm(*s)) for n, s in {"q": (P, hid), "k": (P, hid), "v": (P, hid), "g": (P, hid),
+                                             "o": (hid, P), "f_a": (D, hid), "f_b": (P, D), "b": (Hh, hid)}.items()}
+    arrays.update({"q_conv": f32(rng.standard_normal((P, K)) * 0.5), "k_conv": f32(rng.standard_normal((P, K)) * 0.5),
+                   "v_conv": f32(rng.standard_normal((P, K)) * 0.5), "A_log": f32(rng.uniform(0, 1.5, Hh)),
+                   "dt_bias": f32(rng.standard_normal(P)), "o_norm": f32(1 + 0.1 * rng.standard_normal(D))})
+    W = ko.Weights(arrays, 1)
+    kper = P * D + 3 * P * (K - 1)
+    stride = kper + 8
+    host = [f32(rng.standard_normal(kper) * 0.05) for _ in range(B)]
+    dev = torch.zeros((B, stride), device="cuda")
+    for b in range(B):
+        dev[b, :kper] = torch.from_numpy(host[b])
+    dw = gpu.DeviceWeights(W.w, cfg)
+    worst = 0.0
+    for step in range(4):
+        x = f32(rng.standard_normal((B, hid)))
+        want = np.concatenate([ko.kda_layer(ko.orc(), x[b:b + 1], W, cfg, 1, host[b]) for b in range(B)])
+        out = torch.full((B, hid), float("nan"), device="cuda")
+        dw.layer_decode(out, torch.from_numpy(x).cuda(), dev, stride)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        assert_close(got, want, 1e-4 * rms(want), 1e-4, f"batched decode step {step}")
+        worst = max(worst, worst_ratio(got, want, 1e-4 * rms(want), 1e-4))
+    st = dev.cpu().numpy()
+    for b in range(B):
+        assert_close(st[b, :kper], host[b], 1e-4 * rms(host[b]), 1e-4, f"state of sequence {b}")
+        assert np.all(st[b, kper:] == 0.0), "padding between slots untouched"
+    print(f"D={D} K={K} B={B} lb={lb}: worst {worst:.3f}x of the 1e-4 bar")
+    dw.close()
