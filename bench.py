@@ -36,6 +36,9 @@ FP32_PEAK = 157.3e12       # flop/s, dense fp32 MFMA
 # c2 / c1 shapes
 PRE = dict(hidden=4096, H=32, D=128, T=8192, chunk=64, K=4, gate_lb=-5.0, rms_eps=1e-5)
 DEC = dict(B=64, H=32, D=128)
+# c4 hybrid slice: 3 KDA layers + 1 gated MLA layer, decode at batch 16 over an 8192 context
+HYB = dict(hidden=7168, B=16, ctx=8192, kda_layers=3, H=32, D=128, K=4, gate_lb=-5.0,
+           mla_heads=64, q_lora=1536, kv_lora=512, qk_nope=128, qk_rope=64, v_head=128)
 
 
 def decode_bytes_per_token(H: int, D: int) -> int:
@@ -339,6 +342,112 @@ def bench_layer(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
     return out_d
 
 
+def bench_hybrid(torch, k3, steps: int, warmup: int) -> dict:
+    """c4: one decode step of batch 16 through 3 KDA layers (k3hip_kda_layer_decode) and one
+    gated MLA layer with absorbed weights over an 8192-position latent cache
+    (k3hip_mla_decode), hidden 7168, bf16 weights N(0, 0.02). Each part is timed with HIP
+    events over `steps` back-to-back steps. Bytes: each layer's weights once + its
+    state / cache traffic."""
+    import ctypes as C
+    c = HYB
+    E, B, ctx = c["hidden"], c["B"], c["ctx"]
+    H, D, K = c["H"], c["D"], c["K"]
+    P = H * D
+    g = torch.Generator(device="cuda").manual_seed(0x4B334441 + 4)
+    bf = torch.bfloat16
+
+    def host_bf16(rows, cols):
+        return (torch.randn((rows, cols), device="cuda", generator=g) * 0.02).to(bf).view(torch.int16).cpu().numpy()
+
+    def host_f32(t):
+        return t.float().cpu().numpy().copy()
+
+    keep = []
+    kcfg = k3.make_cfg(E, H, D, K, c["gate_lb"], 1e-5)
+    kdas = []
+    for _ in range(c["kda_layers"]):
+        a = {n: host_bf16(r_, c_) for n, (r_, c_) in {"q": (P, E), "k": (P, E), "v": (P, E), "g": (P, E),
+                                                      "o": (E, P), "f_a": (D, E), "f_b": (P, D), "b": (H, E)}.items()}
+        a["q_conv"], a["k_conv"], a["v_conv"] = (host_f32(torch.randn((P, K), device="cuda", generator=g) * 0.5) for _ in range(3))
+        a["A_log"] = host_f32(torch.rand((H,), device="cuda", generator=g) * 1.5)
+        a["dt_bias"] = host_f32(torch.randn((P,), device="cuda", generator=g))
+        a["o_norm"] = host_f32(1 + 0.1 * torch.randn((D,), device="cuda", generator=g))
+        w = k3.K3KdaW()
+        C.memset(C.byref(w), 0, C.sizeof(w))
+        for n, arr in a.items():
+            setattr(w, n, arr.ctypes.data)
+        w.wdt = 1
+        kdas.append(k3.DeviceWeights(w, kcfg))
+        keep.append(a)
+    Hm, QL, KL, QN, QR, VH = c["mla_heads"], c["q_lora"], c["kv_lora"], c["qk_nope"], c["qk_rope"], c["v_head"]
+    mcfg = k3.make_cfg(E, 1, 16, 1, -5.0, 1e-5)
+    mcfg.n_heads, mcfg.q_lora, mcfg.kv_lora, mcfg.qk_nope, mcfg.qk_rope, mcfg.v_head, mcfg.mla_out_gate = \
+        Hm, QL, KL, QN, QR, VH, 1
+    ma = {n: host_bf16(r_, c_) for n, (r_, c_) in {"q_a": (QL, E), "q_b": (Hm * (QN + QR), QL), "kv_a": (KL + QR, E),
+                                                    "kv_b": (Hm * (QN + VH), KL), "o": (E, Hm * VH), "g": (Hm * VH, E)}.items()}
+    ma["q_a_norm"] = host_f32(1 + 0.1 * torch.randn((QL,), device="cuda", generator=g))
+    ma["kv_a_norm"] = host_f32(1 + 0.1 * torch.randn((KL,), device="cuda", generator=g))
+    mw_ = k3.K3MlaW()
+    C.memset(C.byref(mw_), 0, C.sizeof(mw_))
+    for n, arr in ma.items():
+        setattr(mw_, n, arr.ctypes.data)
+    mw_.wdt = 1
+    mla = k3.MlaWeights(mw_, mcfg)
+    keep.append(ma)
+    kper = P * D + 3 * P * (K - 1)
+    states = [torch.zeros((B, kper), device="cuda") for _ in kdas]
+    cache = torch.randn((B, ctx, KL + QR), device="cuda", generator=g)
+    x = torch.randn((B, E), device="cuda", generator=g)
+    hbuf = [torch.empty((B, E), device="cuda") for _ in range(len(kdas) + 1)]
+
+    def kda_part():
+        h = x
+        for i, dw in enumerate(kdas):
+            dw.layer_decode(hbuf[i], h, states[i], kper)
+            h = hbuf[i]
+        return h
+
+    def mla_part(h):
+        mla.decode(hbuf[-1], h, cache, ctx - 1, ctx)
+
+    h = kda_part()
+    mla_part(h)
+    torch.cuda.synchronize()
+    for _ in range(warmup):
+        mla_part(kda_part())
+    torch.cuda.synchronize()
+    evs = [ev_pair(torch) for _ in range(2)]
+    evs[0][0].record()
+    for _ in range(steps):
+        h = kda_part()
+    evs[0][1].record()
+    evs[1][0].record()
+    for _ in range(steps):
+        mla_part(h)
+    evs[1][1].record()
+    torch.cuda.synchronize()
+    kda_s = evs[0][0].elapsed_time(evs[0][1]) * 1e-3 / steps
+    mla_s = evs[1][0].elapsed_time(evs[1][1]) * 1e-3 / steps
+    kda_w = (4 * P * E + E * P + D * E + P * D + H * E) * 2
+    kda_bytes = len(kdas) * (kda_w + 2 * B * kper * 4)
+    mla_w = (QL * E + Hm * (QN + QR) * QL + (KL + QR) * E + Hm * (QN + VH) * KL + 2 * E * Hm * VH) * 2
+    mla_bytes = mla_w + B * ctx * (KL + QR) * 4
+    for dw in kdas:
+        dw.close()
+    mla.close()
+    return {
+        "config": {"workload": "hybrid_decode_slice", "hidden": E, "batch": B, "context": ctx,
+                   "kda_layers": len(kdas), "kda_heads": H, "kda_head_dim": D,
+                   "mla_heads": Hm, "kv_lora": KL, "qk_rope": QR, "qk_nope": QN, "v_head": VH, "q_lora": QL,
+                   "weights": "bf16 N(0,0.02)", "mla_cache": "compressed latent + rope slot, fp32"},
+        "kda_ms_per_step": kda_s * 1e3, "kda_ms_per_layer": kda_s * 1e3 / len(kdas),
+        "mla_ms_per_step": mla_s * 1e3, "mla_over_kda_layer": mla_s / (kda_s / len(kdas)),
+        "tokens_per_s": B / (kda_s + mla_s),
+        "kda_hbm_frac": kda_bytes / kda_s / HBM_PEAK, "mla_hbm_frac": mla_bytes / mla_s / HBM_PEAK,
+        "kda_bytes_per_step": kda_bytes, "mla_bytes_per_step": mla_bytes,
+    }
+
+
 def cpu_prefill(torch, q_in, k_in, v_in, z, b_logit, gate, conv, A_log, dt_bias, o_norm) -> dict:
     """orc_kda_core (conv .. gate, the same steps as the GPU step) on the first Ts tokens."""
     import numpy as np
@@ -397,7 +506,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["all", "prefill", "decode", "layer", "copy"], default="all",
+    ap.add_argument("--workload", choices=["all", "prefill", "decode", "layer", "hybrid", "copy"], default="all",
                     help="copy: the 1 GiB device copy used to calibrate HBM traffic counters")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     a = ap.parse_args()
@@ -420,11 +529,16 @@ def main() -> int:
         res["prefill"] = bench_prefill(torch, k3, a.steps, a.warmup, not a.no_cpu)
     if a.workload in ("all", "layer"):
         res["layer"] = bench_layer(torch, k3, max(3, a.steps // 2), a.warmup, not a.no_cpu)
+    if a.workload in ("all", "hybrid"):
+        res["hybrid"] = bench_hybrid(torch, k3, a.steps, a.warmup)
     for r in res.values():   # CPU baselines last, after all GPU timing
         f = r.pop("_cpu", None)
         if f is not None:
             r["cpu_baseline"] = f()
-    head = res.get("prefill") or res.get("layer") or res["decode"]
+    head = res.get("prefill") or res.get("layer") or res.get("decode")
+    if head is None:   # hybrid alone
+        print(json.dumps({"workload": "hybrid", **res["hybrid"]}))
+        return 0
     line = {
         "metric": "KDA prefill tokens/s (H=32,d=128,T=8k) + decode state-update GB/s, 1 GPU",
         "value": head["value"], "unit": head["unit"], "n_gpus": 1, "steps": a.steps,
@@ -439,6 +553,8 @@ def main() -> int:
         line["decode"] = res["decode"]
     if "layer" in res and head is not res["layer"]:
         line["layer"] = res["layer"]
+    if "hybrid" in res:
+        line["hybrid"] = res["hybrid"]
     print(json.dumps(line))
     return 0
 

@@ -15,8 +15,10 @@
 // latent goes to position pos and attends over 0..pos. Projections are bf16 MFMA GEMMs on
 // bf16 weights with the fp32 activation split into a bf16 hi/lo pair stacked as 2B rows
 // (each weight is read once; the two halves are summed after), so activations keep fp32
-// accuracy. The attention is two strided-batched fp32 GEMMs (scores, then P . cache) around
-// the reference's softmax (fp32 scores times (nope+rope)^-0.5, max, expf, double sum).
+// accuracy. The absorption (W_UK_h^T q) and the final W_UV_h are bf16 GEMMs batched over
+// heads on the same hi/lo row pairs. The attention is two strided-batched fp32 GEMMs
+// (scores, then P . cache) around the reference's softmax (fp32 scores times
+// (nope+rope)^-0.5, max, expf, double sum).
 #include <math.h>
 #include <stdlib.h>
 
@@ -30,8 +32,6 @@ struct k3hip_mla_weights {
 };
 
 namespace k3kda {
-
-constexpr int MLA_MAXB = 16;   // sequences per absorb / un-absorb pass
 
 __device__ __forceinline__ double block_sum(double v, double *red)
 {
@@ -75,40 +75,18 @@ __global__ void mla_norm_kernel(const float *__restrict__ C2, int B, int N, int 
     }
 }
 
-// qcat[b][h] = [ W_UK_h^T q_nope(b,h) | q_rope(b,h) ], q = q2[b] + q2[B+b]. Block = head h,
-// threads over latent columns c; each W_UK element is read once for all sequences.
-__global__ void mla_absorb_kernel(const float *__restrict__ q2, int B, int H, int QN, int QR,
-                                  int KL, int VH, const uint16_t *__restrict__ kvb,
-                                  float *__restrict__ qcat)
+// qcat[b][h] = [ A2[b][h] + A2[B+b][h] (the absorbed W_UK_h^T q_nope, kv_lora floats) |
+// q_rope(b,h) ], from the hi/lo halves of the batched absorb GEMM and the fp32 q.
+__global__ void mla_qcat_kernel(const float *__restrict__ A2, const float *__restrict__ q, int B,
+                                int H, int QN, int QR, int KL, float *__restrict__ qcat)
 {
-    extern __shared__ float sq[];   // [MLA_MAXB][QN + QR]
-    const int h = blockIdx.x, QH = QN + QR, W = KL + QR;
-    for (int b0 = 0; b0 < B; b0 += MLA_MAXB) {
-        const int nb = min(MLA_MAXB, B - b0);
-        __syncthreads();
-        for (int i = threadIdx.x; i < nb * QH; i += blockDim.x) {
-            const int bb = i / QH, e = i % QH;
-            const size_t at = (size_t)h * QH + e;
-            sq[i] = q2[(size_t)(b0 + bb) * H * QH + at] + q2[(size_t)(B + b0 + bb) * H * QH + at];
-        }
-        __syncthreads();
-        for (int c = threadIdx.x; c < KL; c += blockDim.x) {
-            float acc[MLA_MAXB];
-#pragma unroll
-            for (int bb = 0; bb < MLA_MAXB; bb++) acc[bb] = 0.0f;
-            const uint16_t *col = kvb + (size_t)h * (QN + VH) * KL + c;
-            for (int i = 0; i < QN; i++) {
-                const float wv = bf2f(col[(size_t)i * KL]);
-#pragma unroll
-                for (int bb = 0; bb < MLA_MAXB; bb++)
-                    if (bb < nb) acc[bb] = __builtin_fmaf(sq[bb * QH + i], wv, acc[bb]);
-            }
-            for (int bb = 0; bb < nb; bb++) qcat[((size_t)(b0 + bb) * H + h) * W + c] = acc[bb];
-        }
-        for (int i = threadIdx.x; i < nb * QR; i += blockDim.x) {
-            const int bb = i / QR, r = i % QR;
-            qcat[((size_t)(b0 + bb) * H + h) * W + KL + r] = sq[bb * QH + QN + r];
-        }
+    const int W = KL + QR, QH = QN + QR;
+    const size_t n = (size_t)B * H * W;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const size_t bh = i / W;
+        const int c = (int)(i % W);
+        qcat[i] = c < KL ? A2[i] + A2[n + i] : q[bh * QH + QN + (c - KL)];
     }
 }
 
@@ -137,42 +115,26 @@ __global__ void mla_softmax_kernel(float *__restrict__ S, int n, int ld, float s
     for (int t = threadIdx.x; t < ld; t += blockDim.x) row[t] = t < n ? (float)((double)row[t] / z) : 0.0f;
 }
 
-// o(b,h)[j] = W_UV_h[j] . chat(b,h), times sigmoid(g) when gated (g = g2[b] + g2[B+b]);
-// written as hi/lo bf16 rows of o2 [2B][H*VH]. Block = head h, threads over j.
-__global__ void mla_unabsorb_kernel(const float *__restrict__ chat, int B, int H, int QN, int KL,
-                                    int VH, const uint16_t *__restrict__ kvb,
-                                    const float *__restrict__ g2, uint16_t *__restrict__ o2)
+// o = O2[b] + O2[B+b] (the halves of the batched W_UV GEMM), times sigmoid(g2[b] + g2[B+b])
+// when gated, written as hi/lo bf16 rows of o2 [2B][H*VH] for o_proj.
+__global__ void mla_gate_split_kernel(const float *__restrict__ O2, const float *__restrict__ g2,
+                                      int B, size_t HV, uint16_t *__restrict__ o2)
 {
-    extern __shared__ float sc[];   // [MLA_MAXB][KL]
-    const int h = blockIdx.x;
-    const size_t HV = (size_t)H * VH;
-    for (int b0 = 0; b0 < B; b0 += MLA_MAXB) {
-        const int nb = min(MLA_MAXB, B - b0);
-        __syncthreads();
-        for (int i = threadIdx.x; i < nb * KL; i += blockDim.x)
-            sc[i] = chat[((size_t)(b0 + i / KL) * H + h) * KL + i % KL];
-        __syncthreads();
-        for (int j = threadIdx.x; j < VH; j += blockDim.x) {
-            float acc[MLA_MAXB];
-#pragma unroll
-            for (int bb = 0; bb < MLA_MAXB; bb++) acc[bb] = 0.0f;
-            const uint16_t *row = kvb + ((size_t)h * (QN + VH) + QN + j) * KL;
-            for (int c = 0; c < KL; c++) {
-                const float wv = bf2f(row[c]);
-#pragma unroll
-                for (int bb = 0; bb < MLA_MAXB; bb++)
-                    if (bb < nb) acc[bb] = __builtin_fmaf(sc[bb * KL + c], wv, acc[bb]);
-            }
-            for (int bb = 0; bb < nb; bb++) {
-                const size_t b = b0 + bb, at = (size_t)h * VH + j;
-                float v = acc[bb];
-                if (g2) v *= 1.0f / (1.0f + expf(-(g2[b * HV + at] + g2[(B + b) * HV + at])));
-                const uint16_t hi = f2bf(v);
-                o2[b * HV + at] = hi;
-                o2[(B + b) * HV + at] = f2bf(v - __uint_as_float((uint32_t)hi << 16));
-            }
-        }
+    const size_t n = (size_t)B * HV;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x) {
+        float v = O2[i] + O2[n + i];
+        if (g2) v *= 1.0f / (1.0f + expf(-(g2[i] + g2[n + i])));
+        const uint16_t hi = f2bf(v);
+        o2[i] = hi;
+        o2[n + i] = f2bf(v - __uint_as_float((uint32_t)hi << 16));
     }
+}
+
+static unsigned mla_grid(size_t n)
+{
+    size_t b = (n + 255) / 256;
+    return (unsigned)(b > 4096 ? 4096 : (b ? b : 1));
 }
 
 }  // namespace k3kda
@@ -247,10 +209,15 @@ extern "C" int k3hip_mla_decode(const k3hip_mla_weights *w, int B, int pos, int 
     const int E = w->E, H = w->H, QL = w->QL, KL = w->KL, QN = w->QN, QR = w->QR, VH = w->VH;
     const int QH = QN + QR, CW = KL + QR, Tn = pos + 1;
     const int HV = H * VH;
+    // scratch: x hi/lo | q_a halves | q_a normed hi/lo | q_b halves | kv_a halves | g halves |
+    //          q fp32 | q hi/lo | absorb halves | qcat | scores | chat | chat hi/lo |
+    //          W_UV halves | o hi/lo | out halves
     size_t sizes[] = {(size_t)2 * B * E * 2, (size_t)2 * B * QL * 4, (size_t)2 * B * QL * 2,
                       (size_t)2 * B * H * QH * 4, (size_t)2 * B * CW * 4, (size_t)2 * B * HV * 4,
+                      (size_t)B * H * QH * 4, (size_t)2 * B * H * QH * 2, (size_t)2 * B * H * CW * 4,
                       (size_t)B * H * CW * 4, (size_t)B * H * Tn * 4, (size_t)B * H * KL * 4,
-                      (size_t)2 * B * HV * 2, (size_t)2 * B * E * 4};
+                      (size_t)2 * B * H * KL * 2, (size_t)2 * B * HV * 4, (size_t)2 * B * HV * 2,
+                      (size_t)2 * B * E * 4};
     constexpr int NB = sizeof sizes / sizeof sizes[0];
     size_t off[NB], total = 0;
     for (int i = 0; i < NB; i++) {
@@ -265,9 +232,15 @@ extern "C" int k3hip_mla_decode(const k3hip_mla_weights *w, int B, int pos, int 
     float *ql2 = (float *)(base + off[1]);
     uint16_t *qls = (uint16_t *)(base + off[2]);
     float *q2 = (float *)(base + off[3]), *c2 = (float *)(base + off[4]), *g2 = (float *)(base + off[5]);
-    float *qcat = (float *)(base + off[6]), *S = (float *)(base + off[7]), *chat = (float *)(base + off[8]);
-    uint16_t *o2 = (uint16_t *)(base + off[9]);
-    float *out2 = (float *)(base + off[10]);
+    float *q = (float *)(base + off[6]);
+    uint16_t *qs2 = (uint16_t *)(base + off[7]);
+    float *A2 = (float *)(base + off[8]), *qcat = (float *)(base + off[9]), *S = (float *)(base + off[10]);
+    float *chat = (float *)(base + off[11]);
+    uint16_t *ch2 = (uint16_t *)(base + off[12]);
+    float *O2 = (float *)(base + off[13]);
+    uint16_t *o2 = (uint16_t *)(base + off[14]);
+    float *out2 = (float *)(base + off[15]);
+    const uint16_t *kvb = (const uint16_t *)w->kv_b;
 
     if ((rc = split_rows2(x, xs, B, E, st))) return rc;
     // q = q_b(rmsnorm(q_a x)), latent + rope = kv_a x (latent rmsnorm'd into the cache), g x
@@ -281,9 +254,16 @@ extern "C" int k3hip_mla_decode(const k3hip_mla_weights *w, int B, int pos, int 
                        (uint16_t *)nullptr, cache, (long)cap, pos);
     K3_LAUNCHED();
     if (w->gate && (rc = gemm_bf16(2 * B, HV, E, xs, w->g, g2, K3HIP_F32, st))) return rc;
-    // absorb W_UK into q
-    hipLaunchKernelGGL(mla_absorb_kernel, dim3(H), dim3(256), (size_t)MLA_MAXB * QH * 4, st, q2, B, H,
-                       QN, QR, KL, VH, (const uint16_t *)w->kv_b, qcat);
+    // absorb: per head h, [q hi; lo] (2B x QN) . W_UK_h (QN x KL), batched over heads
+    if ((rc = pair_add(q2, q, B, H * QH, st))) return rc;
+    if ((rc = split_rows2(q, qs2, B, H * QH, st))) return rc;
+    GemmDesc ga;
+    ga.M = 2 * B; ga.N = KL; ga.K = QN; ga.ab_dtype = K3HIP_BF16; ga.c_dtype = K3HIP_F32; ga.b_trans = false;
+    ga.lda = (long)H * QH; ga.ldb = KL; ga.ldc = (long)H * CW; ga.batch = H;
+    ga.sa = QH; ga.sb = (long)(QN + VH) * KL; ga.sc = CW;
+    if ((rc = gemm(ga, qs2, kvb, A2, st))) return rc;
+    hipLaunchKernelGGL(mla_qcat_kernel, dim3(mla_grid((size_t)B * H * CW)), dim3(256), 0, st, A2, q, B, H,
+                       QN, QR, KL, qcat);
     K3_LAUNCHED();
     // scores S_b [H][Tn] = qcat_b [H][CW] . cache_b[0..Tn)^T, per sequence
     GemmDesc gs;
@@ -302,9 +282,15 @@ extern "C" int k3hip_mla_decode(const k3hip_mla_weights *w, int B, int pos, int 
     gp.sa = (long)H * Tn; gp.sb = (long)cap * CW; gp.sc = (long)H * KL;
     gp.tune = false;
     if ((rc = gemm(gp, S, cache, chat, st))) return rc;
-    // W_UV, the gate, o_proj
-    hipLaunchKernelGGL(mla_unabsorb_kernel, dim3(H), dim3(128), (size_t)MLA_MAXB * KL * 4, st, chat, B,
-                       H, QN, KL, VH, (const uint16_t *)w->kv_b, w->gate ? g2 : nullptr, o2);
+    // W_UV: per head h, [chat hi; lo] (2B x KL) . W_UV_h^T (KL x VH), batched over heads; gate
+    if ((rc = split_rows2(chat, ch2, B, H * KL, st))) return rc;
+    GemmDesc gu;
+    gu.M = 2 * B; gu.N = VH; gu.K = KL; gu.ab_dtype = K3HIP_BF16; gu.c_dtype = K3HIP_F32; gu.b_trans = true;
+    gu.lda = (long)H * KL; gu.ldb = KL; gu.ldc = HV; gu.batch = H;
+    gu.sa = KL; gu.sb = (long)(QN + VH) * KL; gu.sc = VH;
+    if ((rc = gemm(gu, ch2, kvb + (size_t)QN * KL, O2, st))) return rc;
+    hipLaunchKernelGGL(mla_gate_split_kernel, dim3(mla_grid((size_t)B * HV)), dim3(256), 0, st, O2,
+                       w->gate ? g2 : nullptr, B, (size_t)HV, o2);
     K3_LAUNCHED();
     if ((rc = gemm_bf16(2 * B, E, HV, o2, w->o, out2, K3HIP_F32, st))) return rc;
     return pair_add(out2, out, B, E, st);
