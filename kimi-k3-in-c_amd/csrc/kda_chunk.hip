@@ -170,8 +170,11 @@ __device__ __forceinline__ char *blk_addr(char *ws, int c, int H, int h)
 // q * q_scale in sX (rows past the end of the sequence zero), beta in sB, sA zero, and this
 // wave's column tile of v in vreg. Writes the item's workspace block. Every LDS read of the
 // item is complete when it returns.
-template <int D>
-__device__ __forceinline__ void p1_item(float *lds, const float (&vreg)[2][8], char *blk)
+// hook(0) .. hook(6) are called between the stages; the fused kernel issues its prefetch of
+// the next item's inputs in parts there, so that the loads of all workgroups spread over the
+// item instead of reaching HBM as one burst.
+template <int D, typename Hook>
+__device__ __forceinline__ void p1_item(float *lds, const float (&vreg)[2][8], char *blk, Hook &&hook)
 {
     using L = P1Lds<D>;
     using WL = Ws<D>;
@@ -210,15 +213,14 @@ __device__ __forceinline__ void p1_item(float *lds, const float (&vreg)[2][8], c
     }
     __syncthreads();
 
+    hook(0);
     // (3) A_kk (times beta_t, strictly lower) into sA; A_qk (lower with the diagonal) staged
-    //     in sT. Each 16x16 block (a, b); blocks above the diagonal are zero.
-    for (int job = w; job < 16; job += NW) {
-        const int a = job >> 2, b = job & 3;
-        if (b > a) {
-#pragma unroll
-            for (int e = 0; e < 4; e++) sT[(SB * a + 4 * kg + e) * PA + SB * b + m] = 0.0f;
-            continue;
-        }
+    //     in sT (both zeroed beforehand). The 10 blocks (a, b), b <= a, of 16x16 are dealt
+    //     as jobs w and w + 8 to wave w: waves w and w + 4 share a SIMD, so the SIMDs take
+    //     3, 3, 2 and 2 blocks.
+    for (int j = w; j < 10; j += NW) {
+        const int a = j < 1 ? 0 : j < 3 ? 1 : j < 6 ? 2 : 3;
+        const int b = j - a * (a + 1) / 2;
         const int p = SB * a + 8;    // pivot row: the middle of row block a
         const int t = SB * a + m;    // A-operand row (token t)
         const int s = SB * b + m;    // B-operand row (token s)
@@ -256,6 +258,7 @@ __device__ __forceinline__ void p1_item(float *lds, const float (&vreg)[2][8], c
     }
     __syncthreads();
 
+    hook(1);
     // (3b) A_qk as A-fragments [rt 4][ks 2], one fragment lane per thread; q e^G (q scaled)
     //      as A-fragments [rt 4][KSI] from the staged q.
     {
@@ -278,6 +281,7 @@ __device__ __forceinline__ void p1_item(float *lds, const float (&vreg)[2][8], c
     for (int e = tid; e < CH * PA; e += P1_THREADS) sT[e] = 0.0f;
     __syncthreads();
 
+    hook(2);
     // (4a) diagonal blocks of Tm = (I + A)^-1. A 16x16 strictly lower block N is nilpotent
     //      (N^16 = 0), so (I + N)^-1 = (I - N)(I + N^2)(I + N^4)(I + N^8) exactly: three
     //      squarings and three products, each a 16x16x16 fp32 MFMA product (4 x 16x16x4).
@@ -339,6 +343,7 @@ __device__ __forceinline__ void p1_item(float *lds, const float (&vreg)[2][8], c
     }
     __syncthreads();
 
+    hook(3);
     // (4b) off-diagonal blocks, by distance d = a - b:
     //      Tm_ab = -Tm_aa * sum_{c=b}^{a-1} A_ac Tm_cb   (fp32 MFMA)
     for (int d = 1; d < 4; d++) {
@@ -372,6 +377,7 @@ __device__ __forceinline__ void p1_item(float *lds, const float (&vreg)[2][8], c
         __syncthreads();
     }
 
+    hook(4);
     // (5) W = Tm (beta K e^G) staged in sX, U = Tm (beta V) written as C blocks;
     //     wave w takes column tiles w, w+NW, ...
     static_assert(NCT <= NW, "one column tile per wave (v is prefetched for tile w)");
@@ -413,6 +419,7 @@ __device__ __forceinline__ void p1_item(float *lds, const float (&vreg)[2][8], c
     }
     __syncthreads();
 
+    hook(5);
     // (5b) W as A-fragments [rt 4][KSI]
     for (int f = tid; f < 4 * KSI * 64; f += P1_THREADS) {
         const int fb = f >> 6, rt = fb / KSI, ks = fb % KSI;
@@ -421,6 +428,7 @@ __device__ __forceinline__ void p1_item(float *lds, const float (&vreg)[2][8], c
         store_frag(blk + WL::WF + (size_t)fb * 2048, lane, x);
     }
 
+    hook(6);
     // (6) (k e^(G_last - G))^T as A-fragments [D/16][2]; e^G_last.
     for (int f = tid; f < NCT * 2 * 64; f += P1_THREADS) {
         const int fb = f >> 6, rt = fb >> 1, ks = fb & 1;
@@ -509,11 +517,11 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra(int T, int H, floa
             *reinterpret_cast<f4 *>(&sK[t * PD + i4]) = live ? pk[j] : f4(0.0f);
             *reinterpret_cast<f4 *>(&sX[t * PD + i4]) = live ? pq[j] * qs : f4(0.0f);
         }
-        for (int e = tid; e < CH * PA; e += P1_THREADS) sA[e] = 0.0f;
+        for (int e = tid; e < 2 * CH * PA; e += P1_THREADS) sA[e] = 0.0f;   // A and Tm
         if (tid < CH) sB[tid] = tid < Tc ? pb : 0.0f;
         __syncthreads();
         fetch(min(item + (int)gridDim.x, nitems - 1));
-        p1_item<D>(lds, vreg, blk_addr<D>(ws, c, H, h));
+        p1_item<D>(lds, vreg, blk_addr<D>(ws, c, H, h), [](int) {});
     }
 }
 
@@ -569,25 +577,31 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra_act(
 
     Raw raw[3][NR];
     float zr[RL][CPL], pbl;
-    auto fetch = [&](int item) {
+    // the inputs of one item in five parts: raw q, k, v rows (with the K-1 rows before the
+    // run), z, the beta logit; issued at the first five stage boundaries of the item before
+    auto fetch = [&](int item, int part) {
         const int fh = item / nch, ft0 = (item % nch) * CH;
+        if (part < 3) {
 #pragma unroll
-        for (int j = 0; j < NR; j++) {
-            const int p = min(max(ft0 + r0 - NH + j, 0), T - 1);
+            for (int j = 0; j < NR; j++) {
+                const int p = min(max(ft0 + r0 - NH + j, 0), T - 1);
+                raw[part][j] = *reinterpret_cast<const Raw *>(xin[part] + (size_t)p * P + (size_t)fh * D + c0);
+            }
+        } else if (part == 3) {
 #pragma unroll
-            for (int b = 0; b < 3; b++)
-                raw[b][j] = *reinterpret_cast<const Raw *>(xin[b] + (size_t)p * P + (size_t)fh * D + c0);
+            for (int r = 0; r < RL; r++) {
+                float x[CPL];
+                RowIO<CPL, K3HIP_F32>::load(x, z, (size_t)min(ft0 + r0 + r, T - 1) * P + (size_t)fh * D + c0);
+#pragma unroll
+                for (int e = 0; e < CPL; e++) zr[r][e] = x[e];
+            }
+        } else if (part == 4) {
+            pbl = b_logit[(size_t)min(ft0 + (tid & (CH - 1)), T - 1) * H + fh];
         }
-#pragma unroll
-        for (int r = 0; r < RL; r++) {
-            float x[CPL];
-            RowIO<CPL, K3HIP_F32>::load(x, z, (size_t)min(ft0 + r0 + r, T - 1) * P + (size_t)fh * D + c0);
-#pragma unroll
-            for (int e = 0; e < CPL; e++) zr[r][e] = x[e];
-        }
-        pbl = b_logit[(size_t)min(ft0 + (tid & (CH - 1)), T - 1) * H + fh];
     };
-    if (lo < hi) fetch(lo);
+    if (lo < hi)
+#pragma unroll
+        for (int part = 0; part < 5; part++) fetch(lo, part);
 
     int head = -1;
     float a = 0.0f;
@@ -674,9 +688,9 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra_act(
                 }
         }
         __syncthreads();   // v staging read before A is cleared
-        for (int e = tid; e < CH * PA; e += P1_THREADS) sA[e] = 0.0f;
-        fetch(min(item + 1, hi - 1));
-        p1_item<D>(lds, vreg, blk_addr<D>(ws, c, H, h));
+        for (int e = tid; e < 2 * CH * PA; e += P1_THREADS) sA[e] = 0.0f;   // A and Tm
+        const int next = min(item + 1, hi - 1);
+        p1_item<D>(lds, vreg, blk_addr<D>(ws, c, H, h), [&](int part) { fetch(next, part); });
     }
 }
 
@@ -689,10 +703,10 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra_act(
 // Per chunk: state waves publish S to LDS -> barrier -> row waves publish Vn -> barrier
 // -> row waves finish O while state waves update S. Each role prefetches the next chunk's
 // operands into a second register set (used alternately, no copies).
-template <int D> struct RowOps {
+template <int D, int NW> struct RowOps {
     static constexpr int KSI = D / 32;
     Frag wf[KSI], qf[KSI], af[2];
-    f32x4 u;
+    f32x4 u[NW];
 };
 template <int D> struct StateOps {
     static constexpr int RTW = D / 64;   // 16-row tiles per state wave
@@ -700,8 +714,10 @@ template <int D> struct StateOps {
     f32x4 gl[RTW];
 };
 
-template <int D>
-__device__ __forceinline__ void load_row_ops(RowOps<D> &op, const char *blk, int w, int lane, int ct)
+// Row wave w's operands of one chunk: W, Q e^G and A_qk fragments of its 16 token rows
+// (shared by all of the workgroup's column tiles) and U for each tile ct0 .. ct0+NW-1.
+template <int D, int NW>
+__device__ __forceinline__ void load_row_ops(RowOps<D, NW> &op, const char *blk, int w, int lane, int ct0)
 {
     using WL = Ws<D>;
     constexpr int KSI = WL::KSI;
@@ -713,7 +729,9 @@ __device__ __forceinline__ void load_row_ops(RowOps<D> &op, const char *blk, int
 #pragma unroll
     for (int ks = 0; ks < 2; ks++)   // af[1] of waves 0-1 is all zero and unused
         op.af[ks] = load_frag(blk + WL::AF + (size_t)(w * 2 + ks) * 2048, lane);
-    op.u = *reinterpret_cast<const f32x4 *>(blk + WL::UC + ((size_t)(w * WL::NCT + ct) * 64 + lane) * 16);
+#pragma unroll
+    for (int j = 0; j < NW; j++)
+        op.u[j] = *reinterpret_cast<const f32x4 *>(blk + WL::UC + ((size_t)(w * WL::NCT + ct0 + j) * 64 + lane) * 16);
 }
 
 // sw = state-wave index 0..3; its tiles are rows 16*(RTW*sw + r) .. +15
@@ -765,78 +783,102 @@ __device__ __forceinline__ Frag read_frag(const char *buf, int ks, int lane)
     return f;
 }
 
-template <int D>
-__device__ __forceinline__ void row_step(const RowOps<D> &op, const char *sSF, char *sVF, int w,
+// LDS of one column tile: S fragments (D/32 K-steps) then Vn fragments (2 K-steps).
+template <int D> struct P2Lds {
+    static constexpr size_t SF = (size_t)(D / 32) * 2 * 1024;
+    static constexpr size_t VF = (size_t)2 * 2 * 1024;
+};
+
+template <int D, int NW>
+__device__ __forceinline__ void row_step(const RowOps<D, NW> &op, const char *sSF, char *sVF, int w,
                                          int lane, int nrows, float *ob, size_t P)
 {
     constexpr int KSI = D / 32;
     const int m = lane & 15, kg = lane >> 4;
-    // Vn = U - W S and O = Q S; two accumulators per product shorten the MFMA chains
-    f32x4 aw0 = 0.0f, aw1 = 0.0f, ao0 = 0.0f, ao1 = 0.0f;
+    f32x4 ao[NW];
 #pragma unroll
-    for (int ks = 0; ks < KSI; ks++) {
-        const Frag sf = read_frag(sSF, ks, lane);
-        if (ks & 1) {
-            aw1 = mma3(aw1, op.wf[ks].hi, op.wf[ks].lo, sf.hi, sf.lo);
-            ao1 = mma3(ao1, op.qf[ks].hi, op.qf[ks].lo, sf.hi, sf.lo);
-        } else {
-            aw0 = mma3(aw0, op.wf[ks].hi, op.wf[ks].lo, sf.hi, sf.lo);
-            ao0 = mma3(ao0, op.qf[ks].hi, op.qf[ks].lo, sf.hi, sf.lo);
+    for (int j = 0; j < NW; j++) {
+        // Vn = U - W S and O = Q S; two accumulators per product shorten the MFMA chains
+        const char *sf_j = sSF + (size_t)j * P2Lds<D>::SF;
+        f32x4 aw0 = 0.0f, aw1 = 0.0f, ao0 = 0.0f, ao1 = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < KSI; ks++) {
+            const Frag sf = read_frag(sf_j, ks, lane);
+            if (ks & 1) {
+                aw1 = mma3(aw1, op.wf[ks].hi, op.wf[ks].lo, sf.hi, sf.lo);
+                ao1 = mma3(ao1, op.qf[ks].hi, op.qf[ks].lo, sf.hi, sf.lo);
+            } else {
+                aw0 = mma3(aw0, op.wf[ks].hi, op.wf[ks].lo, sf.hi, sf.lo);
+                ao0 = mma3(ao0, op.qf[ks].hi, op.qf[ks].lo, sf.hi, sf.lo);
+            }
         }
+        publish_frag4(sVF + (size_t)j * P2Lds<D>::VF, w, lane, op.u[j] - (aw0 + aw1));
+        ao[j] = ao0 + ao1;
     }
-    publish_frag4(sVF, w, lane, op.u - (aw0 + aw1));
     __syncthreads();   // (2) Vn published
-    const Frag v0 = read_frag(sVF, 0, lane);
-    f32x4 ao = mma3(ao0 + ao1, op.af[0].hi, op.af[0].lo, v0.hi, v0.lo);
-    if (w >= 2) {
-        const Frag v1 = read_frag(sVF, 1, lane);
-        ao = mma3(ao, op.af[1].hi, op.af[1].lo, v1.hi, v1.lo);
-    }
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-        const int t = 16 * w + 4 * kg + e;
-        if (t < nrows) ob[(size_t)t * P + m] = ao[e];
+    for (int j = 0; j < NW; j++) {
+        const char *vf_j = sVF + (size_t)j * P2Lds<D>::VF;
+        const Frag v0 = read_frag(vf_j, 0, lane);
+        f32x4 a = mma3(ao[j], op.af[0].hi, op.af[0].lo, v0.hi, v0.lo);
+        if (w >= 2) {
+            const Frag v1 = read_frag(vf_j, 1, lane);
+            a = mma3(a, op.af[1].hi, op.af[1].lo, v1.hi, v1.lo);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int t = 16 * w + 4 * kg + e;
+            if (t < nrows) ob[(size_t)t * P + 16 * j + m] = a[e];
+        }
     }
 }
 
-template <int D>
-__device__ __forceinline__ void state_publish(const f32x4 (&accS)[D / 64], char *sSF, int sw, int lane)
+template <int D, int NW>
+__device__ __forceinline__ void state_publish(const f32x4 (&accS)[D / 64][NW], char *sSF, int sw, int lane)
 {
     constexpr int RTW = D / 64;
 #pragma unroll
-    for (int r = 0; r < RTW; r++) publish_frag4(sSF, RTW * sw + r, lane, accS[r]);
+    for (int j = 0; j < NW; j++)
+#pragma unroll
+        for (int r = 0; r < RTW; r++) publish_frag4(sSF + (size_t)j * P2Lds<D>::SF, RTW * sw + r, lane, accS[r][j]);
 }
 
-template <int D>
-__device__ __forceinline__ void state_update(const StateOps<D> &op, f32x4 (&accS)[D / 64],
+template <int D, int NW>
+__device__ __forceinline__ void state_update(const StateOps<D> &op, f32x4 (&accS)[D / 64][NW],
                                              const char *sVF, int lane)
 {
     constexpr int RTW = D / 64;
-    const Frag v0 = read_frag(sVF, 0, lane), v1 = read_frag(sVF, 1, lane);
 #pragma unroll
-    for (int r = 0; r < RTW; r++) {
-        accS[r] = accS[r] * op.gl[r];
-        accS[r] = mma3(accS[r], op.kf[r][0].hi, op.kf[r][0].lo, v0.hi, v0.lo);
-        accS[r] = mma3(accS[r], op.kf[r][1].hi, op.kf[r][1].lo, v1.hi, v1.lo);
+    for (int j = 0; j < NW; j++) {
+        const char *vf_j = sVF + (size_t)j * P2Lds<D>::VF;
+        const Frag v0 = read_frag(vf_j, 0, lane), v1 = read_frag(vf_j, 1, lane);
+#pragma unroll
+        for (int r = 0; r < RTW; r++) {
+            accS[r][j] = accS[r][j] * op.gl[r];
+            accS[r][j] = mma3(accS[r][j], op.kf[r][0].hi, op.kf[r][0].lo, v0.hi, v0.lo);
+            accS[r][j] = mma3(accS[r][j], op.kf[r][1].hi, op.kf[r][1].lo, v1.hi, v1.lo);
+        }
     }
 }
 
-template <int D>
+// --- phase 2 kernel: one workgroup per (head, NW consecutive 16-column tiles of S) ---
+template <int D, int NW>
 __global__ __launch_bounds__(512) void kda_chunk_state(int T, int H, const char *__restrict__ ws,
                                                        float *__restrict__ S,
                                                        float *__restrict__ o)
 {
     using WL = Ws<D>;
-    constexpr int NTILE = D / 16;        // workgroups per head
+    constexpr int NG = D / 16 / NW;      // workgroups per head
     constexpr int RTW = D / 64;
-    __shared__ __attribute__((aligned(16))) char sSF[(D / 32) * 2 * 1024];   // S fragments
-    __shared__ __attribute__((aligned(16))) char sVF[2 * 2 * 1024];          // Vn fragments
+    extern __shared__ __attribute__((aligned(16))) char p2lds[];
+    char *sSF = p2lds;                               // [NW] S fragments
+    char *sVF = p2lds + (size_t)NW * P2Lds<D>::SF;   // [NW] Vn fragments
 
     // XCD-aware: block b runs on XCD b % 8; give each XCD whole heads.
     const int nb = gridDim.x, b = blockIdx.x;
     int idx = b;
     if (nb % 8 == 0) idx = (b % 8) * (nb / 8) + b / 8;
-    const int h = idx / NTILE, ct = idx % NTILE, j0 = ct * 16;
+    const int h = idx / NG, ct0 = (idx % NG) * NW, j0 = ct0 * 16;
 
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int kg = lane >> 4, m = lane & 15;
@@ -848,51 +890,81 @@ __global__ __launch_bounds__(512) void kda_chunk_state(int T, int H, const char 
     auto blk_of = [&](int c) { return ws + ((size_t)min(c, nch - 1) * H + h) * WL::SIZE; };
 
     if (w < 4) {
-        RowOps<D> opA, opB;
+        RowOps<D, NW> opA, opB;
         float *ob = o + (size_t)h * D + j0;
-        load_row_ops<D>(opA, blk_of(0), w, lane, ct);
+        load_row_ops<D, NW>(opA, blk_of(0), w, lane, ct0);
         for (int c = 0; c < nch; c += 2) {
-            load_row_ops<D>(opB, blk_of(c + 1), w, lane, ct);
+            load_row_ops<D, NW>(opB, blk_of(c + 1), w, lane, ct0);
             __builtin_amdgcn_sched_barrier(0);   // keep the prefetch ahead of the step
             __syncthreads();   // (1) S published
-            row_step<D>(opA, sSF, sVF, w, lane, T - c * CH, ob + (size_t)c * CH * P, P);
+            row_step<D, NW>(opA, sSF, sVF, w, lane, T - c * CH, ob + (size_t)c * CH * P, P);
             if (c + 1 >= nch) break;
-            load_row_ops<D>(opA, blk_of(c + 2), w, lane, ct);
+            load_row_ops<D, NW>(opA, blk_of(c + 2), w, lane, ct0);
             __builtin_amdgcn_sched_barrier(0);
             __syncthreads();
-            row_step<D>(opB, sSF, sVF, w, lane, T - (c + 1) * CH, ob + (size_t)(c + 1) * CH * P, P);
+            row_step<D, NW>(opB, sSF, sVF, w, lane, T - (c + 1) * CH, ob + (size_t)(c + 1) * CH * P, P);
         }
     } else {
         const int sw = w - 4;
-        f32x4 accS[RTW];
+        // L2 warm-up. The workgroups of one head together touch every 64-byte line of the
+        // item PF chunks ahead (one dword each); when the operand loads of that chunk come,
+        // they hit L2 instead of waiting on HBM once per step. A touch is consumed (waited
+        // for) two steps after it is issued, just before its register is reused.
+        constexpr int PF = 4;
+        constexpr int LINES = (int)((WL::SIZE + 63) / 64);
+        constexpr int PER_WG = (LINES + NG - 1) / NG;
+        constexpr int TPL = (PER_WG + 255) / 256;
+        const int line0 = (idx % NG) * PER_WG + sw * 64 + lane;
+        auto touch = [&](int (&t)[TPL], int c) {
+            const char *bk = blk_of(c);
 #pragma unroll
-        for (int r = 0; r < RTW; r++)
+            for (int i = 0; i < TPL; i++)
+                t[i] = *reinterpret_cast<const int *>(bk + (size_t)min(line0 + 256 * i, LINES - 1) * 64);
+        };
+        auto consume = [](const int (&t)[TPL]) {
 #pragma unroll
-            for (int e = 0; e < 4; e++)
-                accS[r][e] = Sh[(size_t)(16 * (RTW * sw + r) + 4 * kg + e) * D + j0 + m];
+            for (int i = 0; i < TPL; i++) asm volatile("" ::"v"(t[i]));
+        };
+        int tA[TPL], tB[TPL];
+        f32x4 accS[RTW][NW];
+#pragma unroll
+        for (int j = 0; j < NW; j++)
+#pragma unroll
+            for (int r = 0; r < RTW; r++)
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    accS[r][j][e] = Sh[(size_t)(16 * (RTW * sw + r) + 4 * kg + e) * D + j0 + 16 * j + m];
         StateOps<D> opA, opB;
         load_state_ops<D>(opA, blk_of(0), sw, lane);
-        state_publish<D>(accS, sSF, sw, lane);
+        touch(tA, PF - 2);
+        touch(tB, PF - 1);
+        state_publish<D, NW>(accS, sSF, sw, lane);
         for (int c = 0; c < nch; c += 2) {
             load_state_ops<D>(opB, blk_of(c + 1), sw, lane);
+            consume(tA);
+            touch(tA, c + PF);
             __builtin_amdgcn_sched_barrier(0);
             __syncthreads();   // (1)
             __syncthreads();   // (2) Vn published
-            state_update<D>(opA, accS, sVF, lane);
-            state_publish<D>(accS, sSF, sw, lane);   // row waves read sSF before (2)
+            state_update<D, NW>(opA, accS, sVF, lane);
+            state_publish<D, NW>(accS, sSF, sw, lane);   // row waves read sSF before (2)
             if (c + 1 >= nch) break;
             load_state_ops<D>(opA, blk_of(c + 2), sw, lane);
+            consume(tB);
+            touch(tB, c + 1 + PF);
             __builtin_amdgcn_sched_barrier(0);
             __syncthreads();
             __syncthreads();
-            state_update<D>(opB, accS, sVF, lane);
-            state_publish<D>(accS, sSF, sw, lane);
+            state_update<D, NW>(opB, accS, sVF, lane);
+            state_publish<D, NW>(accS, sSF, sw, lane);
         }
 #pragma unroll
-        for (int r = 0; r < RTW; r++)
+        for (int j = 0; j < NW; j++)
 #pragma unroll
-            for (int e = 0; e < 4; e++)
-                Sh[(size_t)(16 * (RTW * sw + r) + 4 * kg + e) * D + j0 + m] = accS[r][e];
+            for (int r = 0; r < RTW; r++)
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    Sh[(size_t)(16 * (RTW * sw + r) + 4 * kg + e) * D + j0 + 16 * j + m] = accS[r][j][e];
     }
 }
 
@@ -927,12 +999,26 @@ static int allow_lds(const void *fn, size_t bytes, bool &done)
     return K3HIP_OK;
 }
 
+template <int D, int NW>
+static int launch_state_nw(int T, int H, const char *ws, float *S, float *o, hipStream_t st)
+{
+    const size_t lds = (size_t)NW * (P2Lds<D>::SF + P2Lds<D>::VF);
+    static bool lds_ok = false;
+    int rc;
+    if ((rc = allow_lds((const void *)kda_chunk_state<D, NW>, lds, lds_ok))) return rc;
+    hipLaunchKernelGGL((kda_chunk_state<D, NW>), dim3(H * (D / 16 / NW)), dim3(512), lds, st, T, H, ws, S, o);
+    K3_LAUNCHED();
+    return K3HIP_OK;
+}
+
+// One 16-column tile per workgroup. Wider workgroups (NW = 2, 4) give the same bits but run
+// slower at H = 32, D = 128: a step's time is set by each CU's own operand loads (the row
+// operands of the whole head are needed by every tile), not by the redundant copies that
+// the head's other workgroups load from the same L2.
 template <int D>
 static int launch_state(int T, int H, const char *ws, float *S, float *o, hipStream_t st)
 {
-    hipLaunchKernelGGL((kda_chunk_state<D>), dim3(H * (D / 16)), dim3(512), 0, st, T, H, ws, S, o);
-    K3_LAUNCHED();
-    return K3HIP_OK;
+    return launch_state_nw<D, 1>(T, H, ws, S, o, st);
 }
 
 template <int D>

@@ -4,7 +4,8 @@
 // Replaces steps 2-5 of the reference k3_kda_layer (src/core/k3_ops.c:888-906):
 //   k3_shortconv (:133-165) on q, k, v     acc = w[K-1]*x_t, then += w[j]*x_{t-K+1+j}
 //                                           oldest first; y = acc * sigmoid(acc)
-//   l2norm_ (:845-851) on q and k          v *= (float)(1/sqrt(sum v^2 + 1e-6)), double sum
+//   l2norm_ (:845-851) on q and k          v *= 1/sqrt(sum v^2 + 1e-6); the reference sums
+//                                           in double, kda_prep2_kernel in fp32
 //   beta = sigmoid(b_logit) (:903)         one scalar per (token, head)
 //   k3_kda_decay (:168-183)                g = lb*sigmoid(expf(A_log[h])*(z+dt_bias)),
 //                                           alpha = expf(g)
@@ -130,8 +131,8 @@ __global__ __launch_bounds__(64 * PREP_WAVES) void kda_prep_kernel(
 // Wide form for D = 64 / 128 (the throughput path). A wave holds two independent runs of
 // PREP2_TT tokens, one per half-wave; each of the 32 lanes of a half owns CPL = D/32
 // adjacent channels of the head, so rows are read and written with 8- or 16-byte accesses.
-// The arithmetic is that of kda_prep_math.h (hardware 2^x and reciprocal; L2 sums fp32 per
-// lane and double across lanes), shared with the fused prefill kernel.
+// The arithmetic is that of kda_prep_math.h (hardware 2^x, reciprocal and reciprocal square
+// root; fp32 L2 sums), shared with the fused prefill kernel.
 constexpr int PREP2_TT = 16;   // tokens per half-wave run
 
 template <int CPL>

@@ -28,8 +28,30 @@ __device__ __forceinline__ float conv_silu(const float (&w)[K], const float *win
     return acc * fast_sigmoid(acc);
 }
 
+// Sum over the 32 lanes of a half-wave, the same bits in every lane: swaps of lane pairs
+// (xor 1, xor 2 inside quads), the mirror inside each 8-lane half-row and inside each 16-lane
+// row (DPP), then the other row of the half-wave (swizzle, xor 16). Every step adds the
+// same two values in both lanes of a pair, so all 32 lanes end equal.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float half_wave_sum(float x)
+{
+#pragma clang fp contract(off)
+    x = x + dpp_f<0xB1>(x);    // quad_perm [1,0,3,2]
+    x = x + dpp_f<0x4E>(x);    // quad_perm [2,3,0,1]
+    x = x + dpp_f<0x141>(x);   // row_half_mirror
+    x = x + dpp_f<0x140>(x);   // row_mirror
+    return x + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x401F));   // lane ^ 16
+}
+
 // L2 normalisation of one head row held by a 32-lane half-wave, CPL adjacent channels per
-// lane: fp32 sum of squares per lane, double across the 32 lanes, scale 1/sqrt(ss + 1e-6).
+// lane: y *= 1/sqrt(sum y^2 + 1e-6), the sum in fp32 (per lane, then across the half-wave)
+// and the scale from the hardware reciprocal square root. The reference sums in double
+// (k3_ops.c:845-851); for a row of up to 128 squares the fp32 tree differs from it by a
+// few 1e-7 relative.
 template <int CPL>
 __device__ __forceinline__ void l2norm_half(float (&y)[CPL])
 {
@@ -37,10 +59,7 @@ __device__ __forceinline__ void l2norm_half(float (&y)[CPL])
     float part = 0.0f;
 #pragma unroll
     for (int e = 0; e < CPL; e++) part = part + y[e] * y[e];
-    double ss = (double)part;
-#pragma unroll
-    for (int m = 16; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
-    const float r = (float)(1.0 / sqrt(ss + 1e-6));
+    const float r = __builtin_amdgcn_rsqf(half_wave_sum(part) + 1e-6f);
 #pragma unroll
     for (int e = 0; e < CPL; e++) y[e] = y[e] * r;
 }
