@@ -178,11 +178,11 @@ int k3hip_kda_chunk(int T, int H, int D, int chunk,
                     float *S, float *o, void *workspace, size_t workspace_bytes,
                     void *stream);
 
-/* K1 + K2 fused for bf16 conv inputs: the same arguments as k3hip_kda_prep followed by
- * k3hip_kda_chunk, and bit-identical results (o, S and the outgoing conv_state), without
- * the prepared fp32 q, k, v, g ever being written to memory. Replaces steps 2-6 of
+/* K1 + K2 fused: the same arguments as k3hip_kda_prep followed by k3hip_kda_chunk, and
+ * bit-identical results (o, S and the outgoing conv_state), without the prepared fp32
+ * q, k, v, g ever being written to memory. Replaces steps 2-6 of
  * src/core/k3_ops.c:888-938 for a T-token prefill.
- *   in_dtype = K3HIP_BF16 only; D = 128 or 64; conv_k 1..4; -80/15 <= gate_lb < 0 (the
+ *   in_dtype = K3HIP_BF16 or K3HIP_F32; D = 128 or 64; conv_k 1..4; -80/15 <= gate_lb < 0 (the
  *   bounded gate of k3_kda_decay); q_in, k_in, v_in, z 16-byte aligned; workspace as for
  *   k3hip_kda_chunk (chunk 64). Other shapes return K3HIP_EUNSUPPORTED: use prep + chunk. */
 int k3hip_kda_prefill(int T, int H, int D, int K, float gate_lb, int in_dtype,

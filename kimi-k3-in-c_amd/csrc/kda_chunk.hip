@@ -525,8 +525,8 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra(int T, int H, floa
     }
 }
 
-// Phase 1 fused with the input preparation, from the raw bf16 conv inputs q_in, k_in,
-// v_in [T][H*D], the fp32 gate pre-activation z [T][H*D] and the beta logits [T][H]:
+// Phase 1 fused with the input preparation, from the raw conv inputs q_in, k_in, v_in
+// [T][H*D] (bf16 or fp32, DT), the fp32 gate pre-activation z [T][H*D] and the beta logits [T][H]:
 // per token, short conv + SiLU (taps in order), L2 norm of q and k, the bounded decay gate
 // and beta, with the arithmetic of the stand-alone prep kernel (kda_prep_math.h), so the
 // staged values -- and hence the workspace -- are bit-identical to prep followed by
@@ -541,10 +541,10 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra(int T, int H, floa
 // Persistent over a contiguous range of items in head-major order (item = head * nch +
 // chunk), so a workgroup keeps one head -- its conv taps and dt_bias sit in LDS -- for many
 // consecutive chunks. The next item's raw rows are prefetched into registers.
-template <int D, int K>
+template <int D, int K, int DT>
 __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra_act(
-    int T, int H, float qs, float lb, const uint16_t *__restrict__ q_in,
-    const uint16_t *__restrict__ k_in, const uint16_t *__restrict__ v_in,
+    int T, int H, float qs, float lb, const void *__restrict__ q_in,
+    const void *__restrict__ k_in, const void *__restrict__ v_in,
     const float *__restrict__ z, const float *__restrict__ b_logit,
     const float *__restrict__ q_conv, const float *__restrict__ k_conv,
     const float *__restrict__ v_conv, const float *__restrict__ A_log,
@@ -557,7 +557,10 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra_act(
     constexpr int CPL = D / 32, NH = K - 1, RL = CH / 16, NR = RL + NH;
     static_assert(RL >= NH, "only the first run of a chunk reaches before the chunk");
     static_assert(3 * D * NH <= 4 * 3 * 16 * 17, "conv history fits the inverse scratch area");
-    typedef typename std::conditional<CPL == 4, uint2, uint32_t>::type Raw;
+    // raw conv inputs of CPL adjacent channels: bf16 (8 or 4 bytes) or fp32 (16 or 8 bytes)
+    typedef typename std::conditional<DT == K3HIP_BF16, typename std::conditional<CPL == 4, uint2, uint32_t>::type,
+                                      typename std::conditional<CPL == 4, uint4, uint2>::type>::type Raw;
+    constexpr int ESZ = DT == K3HIP_BF16 ? 2 : 4;
     extern __shared__ __attribute__((aligned(16))) float lds[];
     float *sG = lds + L::G, *sK = lds + L::K, *sX = lds + L::X, *sA = lds + L::A, *sB = lds + L::B;
     float *sV = lds + L::A;                    // v staging [CH][PD], aliases A and Tm
@@ -572,7 +575,7 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra_act(
     const long nitems = (long)nch * H;
     const int lo = (int)((long)blockIdx.x * nitems / gridDim.x);
     const int hi = (int)((long)(blockIdx.x + 1) * nitems / gridDim.x);
-    const uint16_t *xin[3] = {q_in, k_in, v_in};
+    const char *xin[3] = {(const char *)q_in, (const char *)k_in, (const char *)v_in};
     const float *convw[3] = {q_conv, k_conv, v_conv};
 
     Raw raw[3][NR];
@@ -585,7 +588,7 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra_act(
 #pragma unroll
             for (int j = 0; j < NR; j++) {
                 const int p = min(max(ft0 + r0 - NH + j, 0), T - 1);
-                raw[part][j] = *reinterpret_cast<const Raw *>(xin[part] + (size_t)p * P + (size_t)fh * D + c0);
+                raw[part][j] = *reinterpret_cast<const Raw *>(xin[part] + ((size_t)p * P + (size_t)fh * D + c0) * ESZ);
             }
         } else if (part == 3) {
 #pragma unroll
@@ -644,10 +647,16 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra_act(
                 for (int j = 0; j < K; j++) wt[j] = sW[(b * D + c0 + e) * 4 + j];
 #pragma unroll
                 for (int j = 0; j < NR; j++) {
-                    uint32_t u;
-                    if constexpr (CPL == 4) u = (e < 2) ? raw[b][j].x : raw[b][j].y;
-                    else u = raw[b][j];
-                    xs[j] = __uint_as_float((e & 1) ? (u & 0xffff0000u) : (u << 16));
+                    if constexpr (DT == K3HIP_BF16) {
+                        uint32_t u;
+                        if constexpr (CPL == 4) u = (e < 2) ? raw[b][j].x : raw[b][j].y;
+                        else u = raw[b][j];
+                        xs[j] = __uint_as_float((e & 1) ? (u & 0xffff0000u) : (u << 16));
+                    } else {
+                        xs[j] = __uint_as_float(e == 0 ? raw[b][j].x : e == 1 ? raw[b][j].y
+                                                : e == 2 ? ((const uint32_t *)&raw[b][j])[2]
+                                                         : ((const uint32_t *)&raw[b][j])[3]);
+                    }
                 }
                 if (t0 + r0 < NH) {   // first tokens of the sequence: incoming history
 #pragma unroll
@@ -1042,39 +1051,40 @@ static int launch_chunk(int T, int H, const float *q, const float *k, const floa
 struct PrefillArgs {
     int T, H;
     float lb, qs;
-    const uint16_t *qi, *ki, *vi;
+    int dt_in;
+    const void *qi, *ki, *vi;
     const float *z, *bl, *qc, *kc, *vc, *A, *dt;
     float *cs, *S, *o;
     char *ws;
 };
 
-template <int D, int K>
+template <int D, int K, int DT>
 static int launch_prefill(const PrefillArgs &a, hipStream_t st)
 {
     const long nitems = (long)((a.T + CH - 1) / CH) * a.H;
     const size_t lds = (P1Lds<D>::FLOATS + 3 * D * 4 + D) * sizeof(float);
     static bool lds_ok = false;
     int ncu = 0, rc;
-    if ((rc = allow_lds((const void *)kda_chunk_intra_act<D, K>, lds, lds_ok))) return rc;
+    if ((rc = allow_lds((const void *)kda_chunk_intra_act<D, K, DT>, lds, lds_ok))) return rc;
     if ((rc = cu_count(ncu))) return rc;
     const int grid = (int)(nitems < ncu ? nitems : ncu);
-    hipLaunchKernelGGL((kda_chunk_intra_act<D, K>), dim3(grid), dim3(P1_THREADS), lds, st, a.T, a.H,
-                       a.qs, a.lb, a.qi, a.ki, a.vi, a.z, a.bl, a.qc, a.kc, a.vc, a.A, a.dt, a.cs,
-                       a.ws);
+    hipLaunchKernelGGL((kda_chunk_intra_act<D, K, DT>), dim3(grid), dim3(P1_THREADS), lds, st, a.T,
+                       a.H, a.qs, a.lb, a.qi, a.ki, a.vi, a.z, a.bl, a.qc, a.kc, a.vc, a.A, a.dt,
+                       a.cs, a.ws);
     K3_LAUNCHED();
     // the outgoing conv history, after the kernel above has read the incoming one
-    if ((rc = conv_state_update(a.T, a.H * D, K, K3HIP_BF16, a.qi, a.ki, a.vi, a.cs, st))) return rc;
+    if ((rc = conv_state_update(a.T, a.H * D, K, DT, a.qi, a.ki, a.vi, a.cs, st))) return rc;
     return launch_state<D>(a.T, a.H, a.ws, a.S, a.o, st);
 }
 
-template <int D>
+template <int D, int DT>
 static int prefill_k(int K, const PrefillArgs &a, hipStream_t st)
 {
     switch (K) {
-    case 1: return launch_prefill<D, 1>(a, st);
-    case 2: return launch_prefill<D, 2>(a, st);
-    case 3: return launch_prefill<D, 3>(a, st);
-    case 4: return launch_prefill<D, 4>(a, st);
+    case 1: return launch_prefill<D, 1, DT>(a, st);
+    case 2: return launch_prefill<D, 2, DT>(a, st);
+    case 3: return launch_prefill<D, 3, DT>(a, st);
+    case 4: return launch_prefill<D, 4, DT>(a, st);
     default: K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_prefill: conv_k=%d not in 1..4", K);
     }
 }
@@ -1134,8 +1144,8 @@ extern "C" int k3hip_kda_prefill(int T, int H, int D, int K, float gate_lb, int 
 {
     clear_error();
     if (T < 0 || H < 0) K3_FAIL(K3HIP_EINVAL, "k3hip_kda_prefill: T=%d H=%d", T, H);
-    if (in_dtype != K3HIP_BF16)
-        K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_prefill: in_dtype=%d (bf16 only; use prep + chunk)", in_dtype);
+    if (in_dtype != K3HIP_BF16 && in_dtype != K3HIP_F32)
+        K3_FAIL(K3HIP_EINVAL, "k3hip_kda_prefill: in_dtype=%d", in_dtype);
     if (D != 64 && D != 128) K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_prefill: D=%d (64 or 128)", D);
     if (K < 1 || K > 4) K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_prefill: conv_k=%d not in 1..4", K);
     if (!(gate_lb < 0.0f && 15.0f * -gate_lb <= 80.0f))
@@ -1162,9 +1172,8 @@ extern "C" int k3hip_kda_prefill(int T, int H, int D, int K, float gate_lb, int 
         if (rc) return rc;
         ws = (char *)own.p;
     }
-    const PrefillArgs a{T, H, gate_lb, q_scale, (const uint16_t *)q_in, (const uint16_t *)k_in,
-                        (const uint16_t *)v_in, z, b_logit, q_conv, k_conv, v_conv, A_log, dt_bias,
-                        conv_state, S, o, ws};
-    if (D == 128) return prefill_k<128>(K, a, st);
-    return prefill_k<64>(K, a, st);
+    const PrefillArgs a{T, H, gate_lb, q_scale, in_dtype, q_in, k_in, v_in, z, b_logit, q_conv,
+                        k_conv, v_conv, A_log, dt_bias, conv_state, S, o, ws};
+    if (in_dtype == K3HIP_BF16) return D == 128 ? prefill_k<128, K3HIP_BF16>(K, a, st) : prefill_k<64, K3HIP_BF16>(K, a, st);
+    return D == 128 ? prefill_k<128, K3HIP_F32>(K, a, st) : prefill_k<64, K3HIP_F32>(K, a, st);
 }

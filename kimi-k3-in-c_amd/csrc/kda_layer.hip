@@ -311,11 +311,10 @@ extern "C" int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *
     const size_t wsb = k3hip_kda_chunk_workspace(T, H, D, 64);
     // scratch, 256-byte aligned pieces:
     //   0 x bf16 | 1 q k v gate projections fp32 | 2 f_a fp32 | 3 f_a hi/lo bf16 | 4 z fp32 |
-    //   5 b logits | 6 prepared q k v g fp32 | 7 beta | 8 o fp32 | 9 y hi/lo bf16 |
-    //   10 zero state | 11 chunk workspace
+    //   5 b logits | 6 o fp32 | 7 y hi/lo bf16 | 8 zero state | 9 chunk workspace
     size_t sizes[] = {x_dtype == K3HIP_F32 ? (size_t)T * E * 2 : 0, 4 * TP * 4, (size_t)T * D * 4,
-                      (size_t)T * D * 4, TP * 4, (size_t)T * H * 4, 4 * TP * 4, (size_t)T * H * 4,
-                      TP * 4, TP * 4, state ? 0 : (size_t)H * D * D * 4, wsb};
+                      (size_t)T * D * 4, TP * 4, (size_t)T * H * 4, TP * 4, TP * 4,
+                      state ? 0 : (size_t)H * D * D * 4, wsb};
     constexpr int NB = sizeof sizes / sizeof sizes[0];
     size_t off[NB], total = 0;
     for (int i = 0; i < NB; i++) {
@@ -338,12 +337,11 @@ extern "C" int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *
     float *fa = (float *)(base + off[2]);
     uint16_t *fa2 = (uint16_t *)(base + off[3]);
     float *z = (float *)(base + off[4]), *bl = (float *)(base + off[5]);
-    float *q = (float *)(base + off[6]), *k = q + TP, *v = k + TP, *g = v + TP;
-    float *beta = (float *)(base + off[7]), *o = (float *)(base + off[8]);
-    uint16_t *y2 = (uint16_t *)(base + off[9]);
+    float *o = (float *)(base + off[6]);
+    uint16_t *y2 = (uint16_t *)(base + off[7]);
     float *S = state;
     if (!S) {
-        S = (float *)(base + off[10]);
+        S = (float *)(base + off[8]);
         if ((rc = zero_fill(S, (size_t)H * D * D, st))) return rc;
     }
     float *cs = state ? state + (size_t)H * D * D : nullptr;
@@ -360,13 +358,10 @@ extern "C" int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *
                        (size_t)T * D);
     K3_LAUNCHED();
     if ((rc = gemm_bf16(T, (int)P, 2 * D, fa2, w->f_b2, z, K3HIP_F32, st))) return rc;
-    // 2-5 K1, 6 K2 (chunked)
-    if ((rc = k3hip_kda_prep(T, H, D, K, w->gate_lb, K3HIP_F32, qp, kp, vp, z, bl, w->q_conv,
-                             w->k_conv, w->v_conv, w->A_log, w->dt_bias, cs, q, k, v, g, nullptr,
-                             beta, stream)))
-        return rc;
-    if ((rc = k3hip_kda_chunk(T, H, D, 64, q, k, v, g, beta, 1.0f / sqrtf((float)D), S, o,
-                              base + off[11], wsb, stream)))
+    // 2-5 K1 fused into 6 K2 (chunked): the prepared q, k, v, g never reach HBM
+    if ((rc = k3hip_kda_prefill(T, H, D, K, w->gate_lb, K3HIP_F32, qp, kp, vp, z, bl, w->q_conv,
+                                w->k_conv, w->v_conv, w->A_log, w->dt_bias, cs,
+                                1.0f / sqrtf((float)D), S, o, base + off[9], wsb, stream)))
         return rc;
     // 7-8 head RMSNorm, then the gate; y as a bf16 hi/lo pair
     if ((rc = epilogue_split(T, H, D, w->rms_eps, o, gl, K3HIP_F32, w->o_norm, y2, st))) return rc;

@@ -207,7 +207,7 @@ def kda_chunk(q, k, v, g, beta, S, o, H: int, D: int, q_scale: float, chunk: int
 def kda_prefill(q_in, k_in, v_in, z, b_logit, q_conv, k_conv, v_conv, A_log, dt_bias,
                 conv_state, S, o, H: int, D: int, K: int, gate_lb: float, q_scale: float,
                 workspace=None, stream=None) -> None:
-    """K1 + K2 fused: bf16 inputs [T,P], z [T,P] fp32, b_logit [T,H]; S [H,D,D] in/out."""
+    """K1 + K2 fused: bf16 or fp32 inputs [T,P], z [T,P] fp32, b_logit [T,H]; S [H,D,D] in/out."""
     T = q_in.shape[0]
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     _check(lib().k3hip_kda_prefill(T, H, D, K, gate_lb, _dt(q_in), _ptr(q_in), _ptr(k_in),

@@ -1,12 +1,12 @@
 # SPDX-License-Identifier: Apache-2.0
-"""K1 + K2 fused (k3hip_kda_prefill) for bf16 conv inputs, through the C ABI.
+"""K1 + K2 fused (k3hip_kda_prefill) for bf16 and fp32 conv inputs, through the C ABI.
 
 1. Bit-identical to k3hip_kda_prep followed by k3hip_kda_chunk on the same device inputs:
    the output, the final state and the outgoing conv history, over ragged T, every conv
    size, with and without incoming history, and with workgroups whose item ranges cross
-   heads (H * chunks not a multiple of the workgroup count).
-2. Against the CPU oracle (prep, then the sequential recurrence, on the bf16-rounded
-   inputs) at the chunked bar: |got - want| <= 2e-3 * rms(want) + 2e-3 |want|.
+   heads (H * chunks not a multiple of the workgroup count); both input dtypes.
+2. Against the CPU oracle (prep, then the sequential recurrence, on the inputs the GPU
+   sees) at the chunked bar: |got - want| <= 2e-3 * rms(want) + 2e-3 |want|.
 3. Shapes outside the fused kernel are refused with K3HIP_EUNSUPPORTED / K3HIP_EINVAL.
 """
 from __future__ import annotations
@@ -29,13 +29,13 @@ def rms(a):
     return float(np.sqrt(np.mean(np.asarray(a, np.float64) ** 2)))
 
 
-def setup(rng, T, H, D, K, with_history):
+def setup(rng, T, H, D, K, with_history, fp32=False):
     import torch
     P = H * D
     W, ins, z, bl = prep_case(rng, T, H, D, K)
     a = W.arrays
     d = {
-        "ins": [dev(x, torch.bfloat16) for x in ins], "z": dev(z), "bl": dev(bl),
+        "ins": [dev(x, torch.float32 if fp32 else torch.bfloat16) for x in ins], "z": dev(z), "bl": dev(bl),
         "conv": [dev(a["q_conv"]), dev(a["k_conv"]), dev(a["v_conv"])],
         "A_log": dev(a["A_log"]), "dt": dev(a["dt_bias"]),
     }
@@ -74,18 +74,21 @@ def run_fused(gpu, d, cs, S0, T, H, D, K, qs, workspace=True):
     return o, S, dcs
 
 
-@pytest.mark.parametrize("T,H,D,K,hist", [
-    (1, 2, 128, 4, True), (2, 1, 64, 4, True), (3, 2, 128, 3, True), (64, 2, 128, 4, False),
-    (65, 3, 128, 2, True), (130, 2, 64, 1, False), (200, 2, 64, 3, True), (1000, 3, 128, 4, True),
-    (1000, 20, 64, 4, True), (4096 + 17, 5, 128, 4, True), (16384, 4, 128, 4, False)])
-def test_prefill_bitwise_vs_prep_then_chunk(gpu, T, H, D, K, hist):
+@pytest.mark.parametrize("T,H,D,K,hist,fp32", [
+    (1, 2, 128, 4, True, False), (2, 1, 64, 4, True, False), (3, 2, 128, 3, True, False),
+    (64, 2, 128, 4, False, False), (65, 3, 128, 2, True, False), (130, 2, 64, 1, False, False),
+    (200, 2, 64, 3, True, False), (1000, 3, 128, 4, True, False), (1000, 20, 64, 4, True, False),
+    (4096 + 17, 5, 128, 4, True, False), (16384, 4, 128, 4, False, False),
+    (1, 2, 128, 4, True, True), (3, 2, 64, 3, True, True), (200, 2, 64, 4, True, True),
+    (1000, 3, 128, 4, True, True), (4096 + 17, 5, 128, 2, False, True)])
+def test_prefill_bitwise_vs_prep_then_chunk(gpu, T, H, D, K, hist, fp32):
     import torch
     rng = np.random.default_rng(0x4B334441 + 7 + T + H + D + K)
     qs = float(np.float32(1) / np.sqrt(np.float32(D)))
-    _, _, _, _, d, cs, S0 = setup(rng, T, H, D, K, hist)
+    _, _, _, _, d, cs, S0 = setup(rng, T, H, D, K, hist, fp32)
     oa, Sa, csa = run_two_step(gpu, d, cs, S0, T, H, D, K, qs)
     ob, Sb, csb = run_fused(gpu, d, cs, S0, T, H, D, K, qs)
-    print(f"T={T} H={H} D={D} K={K} history={hist}: max |do| "
+    print(f"T={T} H={H} D={D} K={K} history={hist} fp32={fp32}: max |do| "
           f"{(oa - ob).abs().max().item():.3g}, max |dS| {(Sa - Sb).abs().max().item():.3g}")
     assert torch.equal(oa, ob), "fused output differs from prep + chunk"
     assert torch.equal(Sa, Sb), "fused final state differs from prep + chunk"
@@ -93,12 +96,14 @@ def test_prefill_bitwise_vs_prep_then_chunk(gpu, T, H, D, K, hist):
         assert torch.equal(csa, csb), "fused outgoing conv history differs"
 
 
-@pytest.mark.parametrize("T,H,D,K", [(1, 2, 128, 4), (70, 2, 64, 2), (300, 3, 128, 4), (1000, 2, 64, 3)])
-def test_prefill_vs_oracle(gpu, T, H, D, K):
+@pytest.mark.parametrize("T,H,D,K,fp32", [(1, 2, 128, 4, False), (70, 2, 64, 2, False),
+                                         (300, 3, 128, 4, False), (1000, 2, 64, 3, False),
+                                         (70, 2, 128, 4, True), (1000, 2, 64, 3, True)])
+def test_prefill_vs_oracle(gpu, T, H, D, K, fp32):
     rng = np.random.default_rng(0x4B334441 + 8 + T + D + K)
     qs = float(np.float32(1) / np.sqrt(np.float32(D)))
     cfg = ko.make_cfg(8, H, D, K, LB, 1e-5)
-    W, ins, z, bl, d, cs, S0 = setup(rng, T, H, D, K, True)
+    W, ins, z, bl, d, cs, S0 = setup(rng, T, H, D, K, True, fp32)
     ins_bf = [host(x) for x in d["ins"]]              # the values the GPU sees
     cs_ref = cs.copy() if cs is not None else None
     q, k, v, g, al, beta = ko.prep(*ins_bf, z, bl, W, cfg, T, cs_ref)
@@ -122,9 +127,6 @@ def test_prefill_refuses_other_shapes(gpu):
     S, o = dev(S0), torch.zeros((T, H * D), device="cuda")
     args = lambda ins, lb=LB, Dx=D: (*ins, d["z"], d["bl"], *d["conv"], d["A_log"], d["dt"], None,
                                      S, o, H, Dx, K, lb, 0.125)
-    with pytest.raises(gpu.K3HipError) as e:          # fp32 inputs: prep + chunk instead
-        gpu.kda_prefill(*args([x.float() for x in d["ins"]]))
-    assert e.value.code == 3
     with pytest.raises(gpu.K3HipError) as e:          # unbounded (softplus) gate
         gpu.kda_prefill(*args(d["ins"], lb=0.0))
     assert e.value.code == 3
