@@ -250,12 +250,12 @@ def bench_prefill(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
     step_s = wall / steps
     flops_launch = prefill_core_flops_per_token(H, D, 64) * T
     bytes_launch = prefill_core_bytes_per_token(H, D) * T
-    kname = {"fused": "kda_prefill (K1+K2: kda_chunk_intra_act<128,4> + kda_chunk_state<128>)",
+    kname = {"fused": "kda_prefill (K1+K2: kda_chunk_intra_act<128,4,bf16> + kda_chunk_state<128,1>)",
              "chunk": "kda_prep2 + kda_chunk (K1, K2)",
              "recurrent": "kda_prep2 + kda_recurrent_kernel<128> (sequential)"}[mode]
     traffic = None
     if mode == "fused":
-        traffic = measured_traffic("kda_chunk_intra_act<128, 4>", "kda_chunk_state<128>")
+        traffic = measured_traffic("kda_chunk_intra_act<128, 4, 1>", "kda_chunk_state<128, 1>")
     out = {
         "value": T / step_s, "unit": "tokens/s", "ms_per_step": step_s * 1e3,
         "core_ms_avg": kavg * 1e3, "core_ms_median": ks[len(ks) // 2] * 1e3,
