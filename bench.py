@@ -140,10 +140,10 @@ def bench_decode(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
         "kernel_ms_min_of_3": ks[0] * 1e3, "kernel_ms_max_of_3": ks[-1] * 1e3,
         "config": {"workload": "kda_decode", "batch": B, "heads": H, "head_dim": D,
                    "state_sets_rotated": nsets, "bytes_per_step": bytes_step},
-        "roofline": {"kernel": "kda_decode_kernel<128,256>", "bound": "hbm",
+        "roofline": {"kernel": "kda_decode_kernel<128,512>", "bound": "hbm",
                      "achieved": bytes_step / kavg / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                      "frac": bytes_step / kavg / HBM_PEAK,
-                     "traffic": measured_traffic("kda_decode_kernel<128,256>")},
+                     "traffic": measured_traffic("kda_decode_kernel<128, 512>")},
         "tolerance": "rtol 1e-4, atol 1e-4*rms (tests/test_gpu_kernels.py)",
     }
     if cpu:   # timed after every GPU workload (its OpenMP threads would load the host)

@@ -16,6 +16,9 @@
 // segments. The two reductions over rows (u, then o) go through LDS. The state write-back
 // is a nontemporal store: it streams out without being kept in the caches, which measured
 // 54.5 -> 45.5 us per B=64, H=32, D=128 step (5.0 -> 6.0 TB/s) on MI355X.
+// D = 128 uses 512 threads (8 float4s each, 60 VGPRs, 8 waves per SIMD): the 2,048 states
+// of a B=64 step then run as two full rounds of 1,024 workgroups; with 256 threads
+// (16 float4s, 90 VGPRs, 5 waves per SIMD) they ran as 1,280 + 768, about 1.5% slower.
 //
 // Element arithmetic is kept in the reference's order with contraction off (decay
 // multiply, then products added separately); only the summation order of the two row
@@ -125,7 +128,7 @@ int decode_strided(int B, int H, int D, float *S, long s_stride, float *o, const
     case 16: return launch_decode<16, 64>((int)pairs, S, o, q, k, v, alpha, beta, qs, H, s_stride, st);
     case 32: return launch_decode<32, 128>((int)pairs, S, o, q, k, v, alpha, beta, qs, H, s_stride, st);
     case 64: return launch_decode<64, 256>((int)pairs, S, o, q, k, v, alpha, beta, qs, H, s_stride, st);
-    default: return launch_decode<128, 256>((int)pairs, S, o, q, k, v, alpha, beta, qs, H, s_stride, st);
+    default: return launch_decode<128, 512>((int)pairs, S, o, q, k, v, alpha, beta, qs, H, s_stride, st);
     }
 }
 

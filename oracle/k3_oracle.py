@@ -131,6 +131,7 @@ class Weights:
         for n in self.NAMES:
             setattr(self.w, n, self.arrays[n].ctypes.data)
         self.w.wdt = wdt
+        self.w._arrays = self.arrays   # the struct holds raw addresses: keep their owners alive
 
 
 def kda_layer(L, x: np.ndarray, W: Weights, cfg: K3Cfg, T: int, state: np.ndarray | None):
@@ -223,6 +224,7 @@ class MlaWeights:
         for n, a in self.arrays.items():
             setattr(self.w, n, a.ctypes.data)
         self.w.wdt = wdt
+        self.w._arrays = self.arrays   # the struct holds raw addresses: keep their owners alive
 
 
 def mla_cfg(hidden: int, n_heads: int, q_lora: int, kv_lora: int, qk_nope: int, qk_rope: int,

@@ -138,7 +138,8 @@ def test_decode_after_prefill_equals_longer_prefill(gpu):
     import torch
     rng = np.random.default_rng(0x4B334441 + 23)
     cfg = ko.make_cfg(HID, H, D, K, -5.0, 1e-5)
-    dw = gpu.DeviceWeights(weights(rng).w, cfg)
+    W = weights(rng)
+    dw = gpu.DeviceWeights(W.w, cfg)
     T = 37
     x = torch.from_numpy(f32(rng.standard_normal((T + 1, HID)))).cuda()
     a, b = gpu.States(cfg, 1), gpu.States(cfg, 1)
