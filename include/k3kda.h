@@ -236,8 +236,9 @@ int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *out, int ou
 
 /* One decode token for each of B sequences through the whole layer on bf16 weights: the
  * per-token path of k3_kda_layer (src/core/k3_ops.c:864-951, T = 1) batched over
- * sequences. The projections read each weight once for all B (bf16 MFMA, the fp32 input
- * as a bf16 hi/lo pair); sequence b's state (S then conv history, the reference layout)
+ * sequences. The projections read each weight once for all B (bf16 MFMA, each fp32 input
+ * element split into bf16 hi + lo in registers); needs hidden % 8 == 0 and x 16-byte
+ * aligned. Sequence b's state (S then conv history, the reference layout)
  * starts at states + b * state_stride floats (>= H*D*D + 3*P*(conv_k-1), a multiple of 4).
  * x, out [B][hidden] fp32. */
 int k3hip_kda_layer_decode(const k3hip_kda_weights *w, int B, float *out, const float *x,

@@ -53,6 +53,16 @@ struct StreamBuf {
 };
 int stream_alloc(StreamBuf &b, size_t bytes, hipStream_t st);
 
+// C[B][N] (row stride ldc) = x[B][K] (fp32, row stride ldx) . W[N][K]^T (bf16), each x
+// element split into bf16 hi + lo in registers so products keep fp32 accuracy; built for
+// few rows (decode batches), bound by reading W once. K % 8 == 0, ldx % 4 == 0, x and W
+// 16-byte aligned. Stream-ordered. Split-K partials go to ws (16-byte aligned, at least
+// gemm_rows_ws_floats(B, N, K) floats); with ws == nullptr or too small they are allocated
+// on `st` for the call.
+size_t gemm_rows_ws_floats(int B, int N, int K);
+int gemm_rows(int B, int N, int K, const float *x, long ldx, const uint16_t *W, float *C, long ldc,
+              hipStream_t st, float *ws = nullptr, size_t ws_floats = 0);
+
 // p[0..n) = 0 on `st` with a kernel (never a memset node).
 int zero_fill(float *p, size_t n, hipStream_t st);
 

@@ -9,6 +9,7 @@
 //     (the sequential GPU recurrence when the gate bound is outside K2's range)
 //   7-8 K4: head RMSNorm then sigmoid gate              (:940-947)
 //   9 o_proj                                            (:948)
+#include <algorithm>
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
@@ -70,6 +71,9 @@ using namespace k3kda;
 struct k3hip_kda_weights {
     int hidden, H, D, K, wdt;
     float gate_lb, rms_eps;
+    // q, k, v, f_a, b are row blocks of one allocation xin ([3P + D + H][hidden], in that
+    // order), so a decode step projects into all five with one pass over the weights
+    void *xin;
     void *q, *k, *v, *f_a, *f_b, *b, *g, *o;        // matrices, wdt storage
     float *q_conv, *k_conv, *v_conv, *A_log, *dt_bias, *o_norm;
     void *f_b2, *o2;   // bf16 only: [W | W] along K, for GEMMs on hi/lo-split inputs
@@ -105,8 +109,8 @@ extern "C" int k3hip_kda_release(k3hip_kda_weights *w)
 {
     clear_error();
     if (!w) return K3HIP_OK;
-    void *ptrs[] = {w->q, w->k, w->v, w->f_a, w->f_b, w->b, w->g, w->o,
-                    w->q_conv, w->k_conv, w->v_conv, w->A_log, w->dt_bias, w->o_norm, w->f_b2, w->o2};
+    void *ptrs[] = {w->xin, w->f_b, w->g, w->o, w->q_conv, w->k_conv, w->v_conv, w->A_log,
+                    w->dt_bias, w->o_norm, w->f_b2, w->o2};   // q k v f_a b live inside xin
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
     free(w);
@@ -129,13 +133,34 @@ extern "C" int k3hip_kda_upload(const K3KdaW *w, const K3Cfg *c, k3hip_kda_weigh
     d->gate_lb = c->gate_lb; d->rms_eps = c->rms_eps;
     const size_t P = (size_t)H * D, es = w->wdt == K3_WBF16 ? 2 : 4;
     int rc = K3HIP_OK;
+    {
+        const size_t rowb = (size_t)E * es, nin = 3 * P + D + H;
+        const void *src[5] = {w->q, w->k, w->v, w->f_a, w->b};
+        const size_t rows[5] = {P, P, P, (size_t)D, (size_t)H};
+        void **dst[5] = {&d->q, &d->k, &d->v, &d->f_a, &d->b};
+        for (int i = 0; i < 5 && rc == K3HIP_OK; i++)
+            if (!src[i]) {
+                set_error("k3hip_kda_upload: NULL weight");
+                rc = K3HIP_EINVAL;
+            }
+        if (rc == K3HIP_OK && hipMalloc(&d->xin, nin * rowb) != hipSuccess) {
+            (void)hipGetLastError();
+            d->xin = nullptr;
+            set_error("k3hip_kda_upload: hipMalloc(%zu bytes)", nin * rowb);
+            rc = K3HIP_ENOMEM;
+        }
+        size_t at = 0;
+        for (int i = 0; i < 5 && rc == K3HIP_OK; i++) {
+            *dst[i] = (char *)d->xin + at * rowb;
+            if (hipMemcpy(*dst[i], src[i], rows[i] * rowb, hipMemcpyHostToDevice) != hipSuccess) {
+                set_error("k3hip_kda_upload: weight copy failed");
+                rc = K3HIP_EHIP;
+            }
+            at += rows[i];
+        }
+    }
 #define UP(field, src, bytes) if (rc == K3HIP_OK) rc = upload((void **)&d->field, src, bytes)
-    UP(q, w->q, P * E * es);
-    UP(k, w->k, P * E * es);
-    UP(v, w->v, P * E * es);
-    UP(f_a, w->f_a, (size_t)D * E * es);
     UP(f_b, w->f_b, P * D * es);
-    UP(b, w->b, (size_t)H * E * es);
     UP(g, w->g, P * E * es);
     UP(o, w->o, (size_t)E * P * es);
     UP(q_conv, w->q_conv, P * K * 4);
@@ -370,14 +395,14 @@ extern "C" int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *
 }
 
 // ------------------------------------------------------------- batched decode ----
-// K1 for one token of each of B sequences, reading the projections as the two halves of a
-// hi/lo row-split GEMM (C2 [2B][N]: rows b and B+b summed), with sequence b's conv history
+// K1 for one token of each of B sequences from the fp32 projections (q, k, v and the beta
+// logits in rows of stride ldc, z in rows of P), with sequence b's conv history
 // in its state slot (states + b*stride + H*D*D, [3][P][K-1], oldest first; shifted in
 // place). One wave per (head, sequence); lanes own D/64 adjacent channels (D >= 64) or one.
 // Arithmetic of kda_prep_math.h; L2 sums fp32 per lane, double across the wave.
 template <int D, int K>
 __global__ __launch_bounds__(64) void kda_step_prep_kernel(
-    int B, int H, float lb, const float *__restrict__ Cq, const float *__restrict__ Ck,
+    int B, int H, float lb, long ldc, const float *__restrict__ Cq, const float *__restrict__ Ck,
     const float *__restrict__ Cv, const float *__restrict__ Cz, const float *__restrict__ Cb,
     const float *__restrict__ q_conv, const float *__restrict__ k_conv,
     const float *__restrict__ v_conv, const float *__restrict__ A_log,
@@ -401,7 +426,7 @@ __global__ __launch_bounds__(64) void kda_step_prep_kernel(
 #pragma unroll
         for (int e = 0; e < CPL; e++) {
             const size_t ch = c0 + e;
-            const float x = C2[t][(size_t)b * P + ch] + C2[t][(size_t)(B + b) * P + ch];
+            const float x = C2[t][(size_t)b * ldc + ch];
             float w[K], win[NH > 0 ? NH : 1];
 #pragma unroll
             for (int j = 0; j < K; j++) w[j] = cw[t][ch * K + j];
@@ -433,23 +458,23 @@ __global__ __launch_bounds__(64) void kda_step_prep_kernel(
         for (int e = 0; e < CPL; e++) {
             const size_t ch = c0 + e, at = (size_t)b * P + ch;
             for (int t = 0; t < 3; t++) outp[t][at] = y[t][e];
-            const float z = Cz[(size_t)b * P + ch] + Cz[(size_t)(B + b) * P + ch];
+            const float z = Cz[(size_t)b * P + ch];
             const float g = lb != 0.0f ? gate_bounded(lb, a, z, dt_bias[ch])
                                        : -a * softplus_ref(z + dt_bias[ch]);
             alpha[at] = fast_exp(g);
         }
     }
     if (lane == 0)
-        beta[(size_t)b * H + h] = fast_sigmoid(Cb[(size_t)b * H + h] + Cb[(size_t)(B + b) * H + h]);
+        beta[(size_t)b * H + h] = fast_sigmoid(Cb[(size_t)b * ldc + h]);
 }
 
 template <int D>
-static int step_prep_k(int K, dim3 grid, hipStream_t st, int B, int H, float lb, const float *Cq,
+static int step_prep_k(int K, dim3 grid, hipStream_t st, int B, int H, float lb, long ldc, const float *Cq,
                        const float *Ck, const float *Cv, const float *Cz, const float *Cb,
                        const k3hip_kda_weights *w, float *states, long stride, float *q, float *k,
                        float *v, float *al, float *beta)
 {
-#define K3_STEP(KK) hipLaunchKernelGGL((kda_step_prep_kernel<D, KK>), grid, dim3(64), 0, st, B, H, lb, Cq, Ck, Cv, Cz, Cb, w->q_conv, w->k_conv, w->v_conv, w->A_log, w->dt_bias, states, stride, q, k, v, al, beta)
+#define K3_STEP(KK) hipLaunchKernelGGL((kda_step_prep_kernel<D, KK>), grid, dim3(64), 0, st, B, H, lb, ldc, Cq, Ck, Cv, Cz, Cb, w->q_conv, w->k_conv, w->v_conv, w->A_log, w->dt_bias, states, stride, q, k, v, al, beta)
     switch (K) {
     case 1: K3_STEP(1); break;
     case 2: K3_STEP(2); break;
@@ -481,11 +506,16 @@ extern "C" int k3hip_kda_layer_decode(const k3hip_kda_weights *w, int B, float *
                 state_stride, kper);
     hipStream_t st = as_stream(stream);
     const size_t BP = (size_t)B * P;
-    // scratch: x hi/lo | q k v g halves | b halves | f_a halves | f_a | f_a hi/lo | z halves |
-    //          q k v alpha | beta | gate logits | o | y | y hi/lo | out halves
-    size_t sizes[] = {(size_t)2 * B * E * 2, 4 * 2 * BP * 4, (size_t)2 * B * H * 4, (size_t)2 * B * D * 4,
-                      (size_t)B * D * 4, (size_t)2 * B * D * 2, 2 * BP * 4, 4 * BP * 4, (size_t)B * H * 4,
-                      BP * 4, BP * 4, BP * 4, 2 * BP * 2, (size_t)2 * B * E * 4};
+    if ((E & 7) || (D & 7) || (P & 7) || ((uintptr_t)x & 15))
+        K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_layer_decode: hidden=%d D=%d need multiples of 8, x 16-byte aligned", E, D);
+    // scratch: q k v f_a b projections [B][NI] | gate | z | q k v alpha | beta | o | y |
+    //          split-K partials (shared by the projections, which run one after another)
+    const int NI = 3 * (int)P + D + H;
+    const long ldi = (NI + 3) & ~3;   // a multiple of 4: f_a is read in place as an x operand
+    const size_t wsf = std::max({gemm_rows_ws_floats(B, NI, E), gemm_rows_ws_floats(B, (int)P, E),
+                                 gemm_rows_ws_floats(B, (int)P, D), gemm_rows_ws_floats(B, E, (int)P)});
+    size_t sizes[] = {(size_t)B * ldi * 4, BP * 4, BP * 4, 4 * BP * 4, (size_t)B * H * 4, BP * 4,
+                      BP * 4, wsf * 4};
     constexpr int NB = sizeof sizes / sizeof sizes[0];
     size_t off[NB], total = 0;
     for (int i = 0; i < NB; i++) {
@@ -496,35 +526,28 @@ extern "C" int k3hip_kda_layer_decode(const k3hip_kda_weights *w, int B, float *
     int rc = stream_alloc(buf, total, st);
     if (rc) return rc;
     char *bs = (char *)buf.p;
-    uint16_t *xs = (uint16_t *)(bs + off[0]);
-    float *Cq = (float *)(bs + off[1]), *Ck = Cq + 2 * BP, *Cv = Ck + 2 * BP, *Cg = Cv + 2 * BP;
-    float *Cb = (float *)(bs + off[2]), *Cfa = (float *)(bs + off[3]), *fa = (float *)(bs + off[4]);
-    uint16_t *fa2 = (uint16_t *)(bs + off[5]);
-    float *Cz = (float *)(bs + off[6]);
-    float *q = (float *)(bs + off[7]), *k = q + BP, *v = k + BP, *al = v + BP;
-    float *beta = (float *)(bs + off[8]), *gl = (float *)(bs + off[9]), *o = (float *)(bs + off[10]);
-    float *y = (float *)(bs + off[11]);
-    uint16_t *ys = (uint16_t *)(bs + off[12]);
-    float *out2 = (float *)(bs + off[13]);
+    float *Cin = (float *)(bs + off[0]);
+    float *Cq = Cin, *Ck = Cin + P, *Cv = Cin + 2 * P, *fa = Cin + 3 * P, *Cb = fa + D;
+    float *gl = (float *)(bs + off[1]), *Cz = (float *)(bs + off[2]);
+    float *q = (float *)(bs + off[3]), *k = q + BP, *v = k + BP, *al = v + BP;
+    float *beta = (float *)(bs + off[4]), *o = (float *)(bs + off[5]), *y = (float *)(bs + off[6]);
+    float *ws = (float *)(bs + off[7]);
+    const uint16_t *Win = (const uint16_t *)w->xin, *Wg = (const uint16_t *)w->g,
+                   *Wfb = (const uint16_t *)w->f_b, *Wo = (const uint16_t *)w->o;
 
-    // 1 projections, each weight read once for both halves of the split input
-    if ((rc = split_rows2(x, xs, B, E, st))) return rc;
-    if ((rc = gemm_bf16(2 * B, (int)P, E, xs, w->q, Cq, K3HIP_F32, st))) return rc;
-    if ((rc = gemm_bf16(2 * B, (int)P, E, xs, w->k, Ck, K3HIP_F32, st))) return rc;
-    if ((rc = gemm_bf16(2 * B, (int)P, E, xs, w->v, Cv, K3HIP_F32, st))) return rc;
-    if ((rc = gemm_bf16(2 * B, (int)P, E, xs, w->g, Cg, K3HIP_F32, st))) return rc;
-    if ((rc = gemm_bf16(2 * B, H, E, xs, w->b, Cb, K3HIP_F32, st))) return rc;
-    if ((rc = gemm_bf16(2 * B, D, E, xs, w->f_a, Cfa, K3HIP_F32, st))) return rc;
-    if ((rc = pair_add(Cfa, fa, B, D, st))) return rc;
-    if ((rc = split_rows2(fa, fa2, B, D, st))) return rc;
-    if ((rc = gemm_bf16(2 * B, (int)P, D, fa2, w->f_b, Cz, K3HIP_F32, st))) return rc;
+    // 1 projections: the fp32 rows against bf16 weights, each weight read once for all B
+    //   (kda_rows.hip: x split into bf16 hi + lo in registers); q, k, v, f_a and the beta
+    //   logits in one pass over their concatenated weights
+    if ((rc = gemm_rows(B, NI, E, x, E, Win, Cin, ldi, st, ws, wsf))) return rc;
+    if ((rc = gemm_rows(B, (int)P, E, x, E, Wg, gl, (long)P, st, ws, wsf))) return rc;
+    if ((rc = gemm_rows(B, (int)P, D, fa, ldi, Wfb, Cz, (long)P, st, ws, wsf))) return rc;
     // 2-5 K1 on one token per sequence, conv history carried in each slot
     const dim3 grid(H, B);
     switch (D) {
-    case 16: rc = step_prep_k<16>(K, grid, st, B, H, w->gate_lb, Cq, Ck, Cv, Cz, Cb, w, states, state_stride, q, k, v, al, beta); break;
-    case 32: rc = step_prep_k<32>(K, grid, st, B, H, w->gate_lb, Cq, Ck, Cv, Cz, Cb, w, states, state_stride, q, k, v, al, beta); break;
-    case 64: rc = step_prep_k<64>(K, grid, st, B, H, w->gate_lb, Cq, Ck, Cv, Cz, Cb, w, states, state_stride, q, k, v, al, beta); break;
-    default: rc = step_prep_k<128>(K, grid, st, B, H, w->gate_lb, Cq, Ck, Cv, Cz, Cb, w, states, state_stride, q, k, v, al, beta); break;
+    case 16: rc = step_prep_k<16>(K, grid, st, B, H, w->gate_lb, ldi, Cq, Ck, Cv, Cz, Cb, w, states, state_stride, q, k, v, al, beta); break;
+    case 32: rc = step_prep_k<32>(K, grid, st, B, H, w->gate_lb, ldi, Cq, Ck, Cv, Cz, Cb, w, states, state_stride, q, k, v, al, beta); break;
+    case 64: rc = step_prep_k<64>(K, grid, st, B, H, w->gate_lb, ldi, Cq, Ck, Cv, Cz, Cb, w, states, state_stride, q, k, v, al, beta); break;
+    default: rc = step_prep_k<128>(K, grid, st, B, H, w->gate_lb, ldi, Cq, Ck, Cv, Cz, Cb, w, states, state_stride, q, k, v, al, beta); break;
     }
     if (rc) return rc;
     // 6 K3 on the B slots
@@ -532,12 +555,9 @@ extern "C" int k3hip_kda_layer_decode(const k3hip_kda_weights *w, int B, float *
                              1.0f / sqrtf((float)D), st)))
         return rc;
     // 7-8 K4, 9 o_proj
-    if ((rc = pair_add(Cg, gl, B, (int)P, st))) return rc;
     if ((rc = k3hip_kda_epilogue(B, H, D, w->rms_eps, o, gl, K3HIP_F32, w->o_norm, y, K3HIP_F32, stream)))
         return rc;
-    if ((rc = split_rows2(y, ys, B, (int)P, st))) return rc;
-    if ((rc = gemm_bf16(2 * B, E, (int)P, ys, w->o, out2, K3HIP_F32, st))) return rc;
-    return pair_add(out2, out, B, E, st);
+    return gemm_rows(B, E, (int)P, y, (long)P, Wo, out, E, st, ws, wsf);
 }
 
 // ------------------------------------------------------------------ drop-in ----

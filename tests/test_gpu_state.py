@@ -181,12 +181,14 @@ def test_a_log_per_head_binding(gpu):
     assert_close(outs[1].cpu().numpy(), want, 2e-3 * rms(want), 2e-3, "128-entry A_log vs oracle")
 
 
-@pytest.mark.parametrize("D,K,B,lb", [(64, 4, 5, -5.0), (128, 3, 3, -5.0), (32, 4, 2, 0.0)])
+@pytest.mark.parametrize("D,K,B,lb", [(64, 4, 5, -5.0), (128, 3, 3, -5.0), (32, 4, 2, 0.0),
+                                      (128, 4, 17, -5.0), (16, 2, 70, -5.0)])
 def test_batched_layer_decode_vs_oracle(gpu, D, K, B, lb):
     """k3hip_kda_layer_decode: B sequences, one token each per step, states in B slots of a
     strided array (stride > kper), bf16 weights; each sequence against the oracle's
     k3_kda_layer with T = 1 on its own state, at the decode bar (rtol 1e-4, atol 1e-4*rms).
-    The lb = 0 case runs the unbounded softplus gate (parity unpinned)."""
+    B = 17 and 70 take two 16-row tiles and two 64-row passes of the projection kernel; D = 16
+    gives K = 16 for f_b. The lb = 0 case runs the unbounded softplus gate (parity unpinned)."""
     import torch
     from test_oracle_ref import bf16
     rng = np.random.default_rng(0x4B334441 + 25 + D + B)
