@@ -12,21 +12,26 @@
 // order: equal to the reference up to fp32 rounding, and 42x fewer cached bytes.
 //
 // One decode step for B sequences that each hold `pos` cached positions: the new token's
-// latent goes to position pos and attends over 0..pos. Projections are bf16 MFMA GEMMs on
-// bf16 weights with the fp32 activation split into a bf16 hi/lo pair stacked as 2B rows
-// (each weight is read once; the two halves are summed after), so activations keep fp32
-// accuracy. The absorption (W_UK_h^T q) and the final W_UV_h are bf16 GEMMs batched over
-// heads on the same hi/lo row pairs. The attention is two strided-batched fp32 GEMMs
+// latent goes to position pos and attends over 0..pos. The dense projections run on the
+// few-rows bf16 GEMM of kda_rows.hip (fp32 activations split into bf16 hi + lo in registers,
+// each weight read once for all B; q_a, kv_a and g in one pass over their concatenated
+// weights), so activations keep fp32 accuracy. The absorption (W_UK_h^T q) and the final
+// W_UV_h are bf16 GEMMs batched over heads on hi/lo row pairs (2B rows). The attention is two strided-batched fp32 GEMMs
 // (scores, then P . cache) around the reference's softmax (fp32 scores times
 // (nope+rope)^-0.5, max, expf, double sum).
 #include <math.h>
 #include <stdlib.h>
+
+#include <algorithm>
 
 #include "kda_internal.h"
 
 struct k3hip_mla_weights {
     int E, H, QL, KL, QN, QR, VH, gate;
     float eps;
+    // q_a, kv_a and g (when gated) are row blocks of one allocation xin ([QL + KL + QR + H*VH]
+    // [hidden], in that order): one pass over them projects a decode step's input
+    void *xin;
     void *q_a, *q_b, *kv_a, *kv_b, *o, *g;   // bf16
     float *q_a_norm, *kv_a_norm;
 };
@@ -45,33 +50,28 @@ __device__ __forceinline__ double block_sum(double v, double *red)
     return t;
 }
 
-// rows b of C2 [2B][N] summed with rows B+b; rmsnorm over the first nn entries (weight w,
-// src/core/k3_ops.c:94-102); then either split into hi/lo bf16 rows of y2 [2B][N]
-// (cache == nullptr) or written to cache row b at position pos (cache [B][cap][N]).
-__global__ void mla_norm_kernel(const float *__restrict__ C2, int B, int N, int nn,
-                                const float *__restrict__ w, float eps, uint16_t *__restrict__ y2,
+// Row b of C (row stride ldc): rmsnorm over the first nn of its N entries (weight w,
+// src/core/k3_ops.c:94-102; double mean of squares, eps inside), the rest copied; written
+// as fp32 row b of y [B][N] (y != nullptr) or to cache row b at position pos
+// (cache [B][cap][N]).
+__global__ void mla_norm_kernel(const float *__restrict__ C, long ldc, int N, int nn,
+                                const float *__restrict__ w, float eps, float *__restrict__ y,
                                 float *__restrict__ cache, long cap, int pos)
 {
     __shared__ double red[16];
     const int b = blockIdx.x;
-    const float *r0 = C2 + (size_t)b * N, *r1 = C2 + (size_t)(B + b) * N;
+    const float *r0 = C + (size_t)b * ldc;
     double ss = 0.0;
     for (int n = threadIdx.x; n < nn; n += blockDim.x) {
-        const double v = (double)(r0[n] + r1[n]);
+        const double v = (double)r0[n];
         ss += v * v;
     }
     ss = block_sum(ss, red);
     const float inv = (float)(1.0 / sqrt(ss / (double)nn + (double)eps));
+    float *dst = y ? y + (size_t)b * N : cache + ((size_t)b * cap + pos) * N;
     for (int n = threadIdx.x; n < N; n += blockDim.x) {
-        const float v = r0[n] + r1[n];
-        const float y = n < nn ? (w[n] * v) * inv : v;
-        if (cache) {
-            cache[((size_t)b * cap + pos) * N + n] = y;
-        } else {
-            const uint16_t hi = f2bf(y);
-            y2[(size_t)b * N + n] = hi;
-            y2[(size_t)(B + b) * N + n] = f2bf(y - __uint_as_float((uint32_t)hi << 16));
-        }
+        const float v = r0[n];
+        dst[n] = n < nn ? (w[n] * v) * inv : v;
     }
 }
 
@@ -115,19 +115,17 @@ __global__ void mla_softmax_kernel(float *__restrict__ S, int n, int ld, float s
     for (int t = threadIdx.x; t < ld; t += blockDim.x) row[t] = t < n ? (float)((double)row[t] / z) : 0.0f;
 }
 
-// o = O2[b] + O2[B+b] (the halves of the batched W_UV GEMM), times sigmoid(g2[b] + g2[B+b])
-// when gated, written as hi/lo bf16 rows of o2 [2B][H*VH] for o_proj.
-__global__ void mla_gate_split_kernel(const float *__restrict__ O2, const float *__restrict__ g2,
-                                      int B, size_t HV, uint16_t *__restrict__ o2)
+// o = O2[b] + O2[B+b] (the halves of the batched W_UV GEMM), times sigmoid(g) when gated
+// (g row b at stride ldg), as fp32 rows of o [B][H*VH] for o_proj.
+__global__ void mla_gate_kernel(const float *__restrict__ O2, const float *__restrict__ g, long ldg,
+                                int B, size_t HV, float *__restrict__ o)
 {
     const size_t n = (size_t)B * HV;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (size_t)gridDim.x * blockDim.x) {
         float v = O2[i] + O2[n + i];
-        if (g2) v *= 1.0f / (1.0f + expf(-(g2[i] + g2[n + i])));
-        const uint16_t hi = f2bf(v);
-        o2[i] = hi;
-        o2[n + i] = f2bf(v - __uint_as_float((uint32_t)hi << 16));
+        if (g) v *= 1.0f / (1.0f + expf(-g[(i / HV) * ldg + i % HV]));
+        o[i] = v;
     }
 }
 
@@ -145,7 +143,7 @@ extern "C" int k3hip_mla_release(k3hip_mla_weights *w)
 {
     clear_error();
     if (!w) return K3HIP_OK;
-    void *ptrs[] = {w->q_a, w->q_b, w->kv_a, w->kv_b, w->o, w->g, w->q_a_norm, w->kv_a_norm};
+    void *ptrs[] = {w->xin, w->q_b, w->kv_b, w->o, w->q_a_norm, w->kv_a_norm};   // q_a kv_a g in xin
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
     free(w);
@@ -170,13 +168,34 @@ extern "C" int k3hip_mla_upload(const K3MlaW *w, const K3Cfg *c, k3hip_mla_weigh
     d->QN = c->qk_nope; d->QR = c->qk_rope; d->VH = c->v_head; d->gate = c->mla_out_gate && w->g;
     d->eps = c->rms_eps;
     const size_t E = d->E, H = d->H, QH = d->QN + d->QR;
+    if (E % 8)
+        K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_mla_upload: hidden=%zu not a multiple of 8", E);
+    {
+        const size_t rows[3] = {(size_t)d->QL, (size_t)(d->KL + d->QR), d->gate ? H * d->VH : 0};
+        const void *src[3] = {w->q_a, w->kv_a, d->gate ? w->g : nullptr};
+        void **dst[3] = {&d->q_a, &d->kv_a, &d->g};
+        if (hipMalloc(&d->xin, (rows[0] + rows[1] + rows[2]) * E * 2) != hipSuccess) {
+            (void)hipGetLastError();
+            d->xin = nullptr;
+            k3hip_mla_release(d);
+            K3_FAIL(K3HIP_ENOMEM, "k3hip_mla_upload: device allocation");
+        }
+        size_t at = 0;
+        for (int i = 0; i < 3; i++) {
+            if (!rows[i]) continue;
+            *dst[i] = (char *)d->xin + at * E * 2;
+            if (hipMemcpy(*dst[i], src[i], rows[i] * E * 2, hipMemcpyHostToDevice) != hipSuccess) {
+                (void)hipGetLastError();
+                k3hip_mla_release(d);
+                K3_FAIL(K3HIP_EHIP, "k3hip_mla_upload: weight copy");
+            }
+            at += rows[i];
+        }
+    }
     struct { void **dst; const void *src; size_t bytes; } up[] = {
-        {&d->q_a, w->q_a, (size_t)d->QL * E * 2},
         {&d->q_b, w->q_b, H * QH * d->QL * 2},
-        {&d->kv_a, w->kv_a, (size_t)(d->KL + d->QR) * E * 2},
         {&d->kv_b, w->kv_b, H * (d->QN + d->VH) * d->KL * 2},
         {&d->o, w->o, E * H * d->VH * 2},
-        {&d->g, d->gate ? w->g : nullptr, H * d->VH * E * 2},
         {(void **)&d->q_a_norm, w->q_a_norm, (size_t)d->QL * 4},
         {(void **)&d->kv_a_norm, w->kv_a_norm, (size_t)d->KL * 4},
     };
@@ -209,15 +228,18 @@ extern "C" int k3hip_mla_decode(const k3hip_mla_weights *w, int B, int pos, int 
     const int E = w->E, H = w->H, QL = w->QL, KL = w->KL, QN = w->QN, QR = w->QR, VH = w->VH;
     const int QH = QN + QR, CW = KL + QR, Tn = pos + 1;
     const int HV = H * VH;
-    // scratch: x hi/lo | q_a halves | q_a normed hi/lo | q_b halves | kv_a halves | g halves |
-    //          q fp32 | q hi/lo | absorb halves | qcat | scores | chat | chat hi/lo |
-    //          W_UV halves | o hi/lo | out halves
-    size_t sizes[] = {(size_t)2 * B * E * 2, (size_t)2 * B * QL * 4, (size_t)2 * B * QL * 2,
-                      (size_t)2 * B * H * QH * 4, (size_t)2 * B * CW * 4, (size_t)2 * B * HV * 4,
-                      (size_t)B * H * QH * 4, (size_t)2 * B * H * QH * 2, (size_t)2 * B * H * CW * 4,
-                      (size_t)B * H * CW * 4, (size_t)B * H * Tn * 4, (size_t)B * H * KL * 4,
-                      (size_t)2 * B * H * KL * 2, (size_t)2 * B * HV * 4, (size_t)2 * B * HV * 2,
-                      (size_t)2 * B * E * 4};
+    if ((QL & 7) || (HV & 7))
+        K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_mla_decode: q_lora=%d, heads*v_head=%d not multiples of 8", QL, HV);
+    // scratch: q_a kv_a g projections [B][ld1] | q_a normed | q | q hi/lo | absorb halves | qcat |
+    //          scores | chat | chat hi/lo | W_UV halves | o | split-K partials
+    const int N1 = QL + CW + (w->gate ? HV : 0);
+    const long ld1 = (N1 + 3) & ~3;
+    const size_t wsf = std::max({gemm_rows_ws_floats(B, N1, E), gemm_rows_ws_floats(B, H * QH, QL),
+                                 gemm_rows_ws_floats(B, E, HV)});
+    size_t sizes[] = {(size_t)B * ld1 * 4, (size_t)B * QL * 4, (size_t)B * H * QH * 4,
+                      (size_t)2 * B * H * QH * 2, (size_t)2 * B * H * CW * 4, (size_t)B * H * CW * 4,
+                      (size_t)B * H * Tn * 4, (size_t)B * H * KL * 4, (size_t)2 * B * H * KL * 2,
+                      (size_t)2 * B * HV * 4, (size_t)B * HV * 4, wsf * 4};
     constexpr int NB = sizeof sizes / sizeof sizes[0];
     size_t off[NB], total = 0;
     for (int i = 0; i < NB; i++) {
@@ -228,34 +250,26 @@ extern "C" int k3hip_mla_decode(const k3hip_mla_weights *w, int B, int pos, int 
     int rc = stream_alloc(buf, total, st);
     if (rc) return rc;
     char *base = (char *)buf.p;
-    uint16_t *xs = (uint16_t *)(base + off[0]);
-    float *ql2 = (float *)(base + off[1]);
-    uint16_t *qls = (uint16_t *)(base + off[2]);
-    float *q2 = (float *)(base + off[3]), *c2 = (float *)(base + off[4]), *g2 = (float *)(base + off[5]);
-    float *q = (float *)(base + off[6]);
-    uint16_t *qs2 = (uint16_t *)(base + off[7]);
-    float *A2 = (float *)(base + off[8]), *qcat = (float *)(base + off[9]), *S = (float *)(base + off[10]);
-    float *chat = (float *)(base + off[11]);
-    uint16_t *ch2 = (uint16_t *)(base + off[12]);
-    float *O2 = (float *)(base + off[13]);
-    uint16_t *o2 = (uint16_t *)(base + off[14]);
-    float *out2 = (float *)(base + off[15]);
+    float *C1 = (float *)(base + off[0]), *qn = (float *)(base + off[1]), *q = (float *)(base + off[2]);
+    uint16_t *qs2 = (uint16_t *)(base + off[3]);
+    float *A2 = (float *)(base + off[4]), *qcat = (float *)(base + off[5]), *S = (float *)(base + off[6]);
+    float *chat = (float *)(base + off[7]);
+    uint16_t *ch2 = (uint16_t *)(base + off[8]);
+    float *O2 = (float *)(base + off[9]), *o = (float *)(base + off[10]), *ws = (float *)(base + off[11]);
     const uint16_t *kvb = (const uint16_t *)w->kv_b;
 
-    if ((rc = split_rows2(x, xs, B, E, st))) return rc;
-    // q = q_b(rmsnorm(q_a x)), latent + rope = kv_a x (latent rmsnorm'd into the cache), g x
-    if ((rc = gemm_bf16(2 * B, QL, E, xs, w->q_a, ql2, K3HIP_F32, st))) return rc;
-    hipLaunchKernelGGL(mla_norm_kernel, dim3(B), dim3(256), 0, st, ql2, B, QL, QL, w->q_a_norm, w->eps,
-                       qls, (float *)nullptr, 0L, 0);
+    // q_a, kv_a and g in one pass over their weights (fp32 x split hi/lo in registers);
+    // q = q_b(rmsnorm(q_a x)); latent + rope = kv_a x, the latent rmsnorm'd into the cache
+    if ((rc = gemm_rows(B, N1, E, x, E, (const uint16_t *)w->xin, C1, ld1, st, ws, wsf))) return rc;
+    hipLaunchKernelGGL(mla_norm_kernel, dim3(B), dim3(256), 0, st, C1, ld1, QL, QL, w->q_a_norm, w->eps,
+                       qn, (float *)nullptr, 0L, 0);
     K3_LAUNCHED();
-    if ((rc = gemm_bf16(2 * B, H * QH, QL, qls, w->q_b, q2, K3HIP_F32, st))) return rc;
-    if ((rc = gemm_bf16(2 * B, CW, E, xs, w->kv_a, c2, K3HIP_F32, st))) return rc;
-    hipLaunchKernelGGL(mla_norm_kernel, dim3(B), dim3(256), 0, st, c2, B, CW, KL, w->kv_a_norm, w->eps,
-                       (uint16_t *)nullptr, cache, (long)cap, pos);
+    if ((rc = gemm_rows(B, H * QH, QL, qn, QL, (const uint16_t *)w->q_b, q, (long)H * QH, st, ws, wsf)))
+        return rc;
+    hipLaunchKernelGGL(mla_norm_kernel, dim3(B), dim3(256), 0, st, C1 + QL, ld1, CW, KL, w->kv_a_norm,
+                       w->eps, (float *)nullptr, cache, (long)cap, pos);
     K3_LAUNCHED();
-    if (w->gate && (rc = gemm_bf16(2 * B, HV, E, xs, w->g, g2, K3HIP_F32, st))) return rc;
     // absorb: per head h, [q hi; lo] (2B x QN) . W_UK_h (QN x KL), batched over heads
-    if ((rc = pair_add(q2, q, B, H * QH, st))) return rc;
     if ((rc = split_rows2(q, qs2, B, H * QH, st))) return rc;
     GemmDesc ga;
     ga.M = 2 * B; ga.N = KL; ga.K = QN; ga.ab_dtype = K3HIP_BF16; ga.c_dtype = K3HIP_F32; ga.b_trans = false;
@@ -289,9 +303,8 @@ extern "C" int k3hip_mla_decode(const k3hip_mla_weights *w, int B, int pos, int 
     gu.lda = (long)H * KL; gu.ldb = KL; gu.ldc = HV; gu.batch = H;
     gu.sa = KL; gu.sb = (long)(QN + VH) * KL; gu.sc = VH;
     if ((rc = gemm(gu, ch2, kvb + (size_t)QN * KL, O2, st))) return rc;
-    hipLaunchKernelGGL(mla_gate_split_kernel, dim3(mla_grid((size_t)B * HV)), dim3(256), 0, st, O2,
-                       w->gate ? g2 : nullptr, B, (size_t)HV, o2);
+    hipLaunchKernelGGL(mla_gate_kernel, dim3(mla_grid((size_t)B * HV)), dim3(256), 0, st, O2,
+                       w->gate ? C1 + QL + CW : nullptr, ld1, B, (size_t)HV, o);
     K3_LAUNCHED();
-    if ((rc = gemm_bf16(2 * B, E, HV, o2, w->o, out2, K3HIP_F32, st))) return rc;
-    return pair_add(out2, out, B, E, st);
+    return gemm_rows(B, E, HV, o, HV, (const uint16_t *)w->o, out, E, st, ws, wsf);
 }
