@@ -129,6 +129,44 @@ __global__ void mla_gate_kernel(const float *__restrict__ O2, const float *__res
     }
 }
 
+// mla_softmax_kernel for rows of n <= 256 * RPT scores held in registers: one read and one
+// write of the row instead of three passes; the same arithmetic (fp32 score * scale, max,
+// expf(s - m), double sum over the block, (float)(e / z)).
+template <int RPT>
+__global__ __launch_bounds__(256) void mla_softmax_reg_kernel(float *__restrict__ S, int n, int ld, float scale)
+{
+    __shared__ double red[16];
+    __shared__ float smax[16];
+    float *row = S + (size_t)blockIdx.x * ld;
+    float v[RPT];
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < RPT; i++) {
+        const int t = threadIdx.x + 256 * i;
+        v[i] = t < n ? row[t] * scale : -INFINITY;
+        m = fmaxf(m, v[i]);
+    }
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    if (lane == 0) smax[w] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3]));
+    double z = 0.0;
+#pragma unroll
+    for (int i = 0; i < RPT; i++) {
+        const int t = threadIdx.x + 256 * i;
+        v[i] = t < n ? expf(v[i] - m) : 0.0f;
+        z += (double)v[i];
+    }
+    z = block_sum(z, red);
+#pragma unroll
+    for (int i = 0; i < RPT; i++) {
+        const int t = threadIdx.x + 256 * i;
+        if (t < n) row[t] = (float)((double)v[i] / z);
+    }
+    for (int t = n + threadIdx.x; t < ld; t += 256) row[t] = 0.0f;
+}
+
 static unsigned mla_grid(size_t n)
 {
     size_t b = (n + 255) / 256;
@@ -286,9 +324,16 @@ extern "C" int k3hip_mla_decode(const k3hip_mla_weights *w, int B, int pos, int 
     gs.sa = (long)H * CW; gs.sb = (long)cap * CW; gs.sc = (long)H * Tn;
     gs.tune = false;   // a new length every step: take the heuristic's first choice
     if ((rc = gemm(gs, qcat, cache, S, st))) return rc;
-    hipLaunchKernelGGL(mla_softmax_kernel, dim3(B * H), dim3(256), 0, st, S, Tn, Tn,
-                       1.0f / sqrtf((float)QH));
-    K3_LAUNCHED();
+    {
+        const float scale = 1.0f / sqrtf((float)QH);
+        if (Tn <= 256 * 8)
+            hipLaunchKernelGGL((mla_softmax_reg_kernel<8>), dim3(B * H), dim3(256), 0, st, S, Tn, Tn, scale);
+        else if (Tn <= 256 * 32)
+            hipLaunchKernelGGL((mla_softmax_reg_kernel<32>), dim3(B * H), dim3(256), 0, st, S, Tn, Tn, scale);
+        else
+            hipLaunchKernelGGL(mla_softmax_kernel, dim3(B * H), dim3(256), 0, st, S, Tn, Tn, scale);
+        K3_LAUNCHED();
+    }
     // chat_b [H][KL] = P_b [H][Tn] . cache_b[0..Tn)[0..KL)
     GemmDesc gp;
     gp.M = H; gp.N = KL; gp.K = Tn; gp.ab_dtype = K3HIP_F32; gp.c_dtype = K3HIP_F32; gp.b_trans = false;
