@@ -53,14 +53,20 @@ struct StreamBuf {
 };
 int stream_alloc(StreamBuf &b, size_t bytes, hipStream_t st);
 
-// C[B][N] (row stride ldc) = x[B][K] (fp32, row stride ldx) . W[N][K]^T (bf16), each x
-// element split into bf16 hi + lo in registers so products keep fp32 accuracy; built for
-// few rows (decode batches), bound by reading W once. K % 8 == 0, ldx % 4 == 0, x and W
-// 16-byte aligned. Stream-ordered. Split-K partials go to ws (16-byte aligned, at least
-// gemm_rows_ws_floats(B, N, K) floats); with ws == nullptr or too small they are allocated
-// on `st` for the call.
+// Decode copy of a row-major bf16 weight W[N][K] in MFMA fragment order, for gemm_rows:
+// rows_frag_elems(N, K) bf16 elements (N rounded up to 16, K to 32, zero padded). The copy
+// is written by a kernel on `st` (W and Wf device pointers, 16-byte aligned, K % 8 == 0).
+size_t rows_frag_elems(int N, int K);
+int rows_frag_pack(const uint16_t *W, int N, int K, uint16_t *Wf, hipStream_t st);
+
+// C[B][N] (row stride ldc) = x[B][K] (fp32, row stride ldx) . W[N][K]^T (bf16, given as its
+// fragment-ordered copy Wf from rows_frag_pack), each x element split into bf16 hi + lo in
+// registers so products keep fp32 accuracy; built for few rows (decode batches), bound by
+// reading W once. K % 8 == 0, ldx % 4 == 0, x and Wf 16-byte aligned. Stream-ordered.
+// Split-K partials go to ws (16-byte aligned, at least gemm_rows_ws_floats(B, N, K) floats);
+// with ws == nullptr or too small they are allocated on `st` for the call.
 size_t gemm_rows_ws_floats(int B, int N, int K);
-int gemm_rows(int B, int N, int K, const float *x, long ldx, const uint16_t *W, float *C, long ldc,
+int gemm_rows(int B, int N, int K, const float *x, long ldx, const uint16_t *Wf, float *C, long ldc,
               hipStream_t st, float *ws = nullptr, size_t ws_floats = 0);
 
 // p[0..n) = 0 on `st` with a kernel (never a memset node).

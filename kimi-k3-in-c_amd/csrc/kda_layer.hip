@@ -77,6 +77,8 @@ struct k3hip_kda_weights {
     void *q, *k, *v, *f_a, *f_b, *b, *g, *o;        // matrices, wdt storage
     float *q_conv, *k_conv, *v_conv, *A_log, *dt_bias, *o_norm;
     void *f_b2, *o2;   // bf16 only: [W | W] along K, for GEMMs on hi/lo-split inputs
+    // bf16 only: decode copies of xin, g, f_b and o in MFMA fragment order (kda_rows.hip)
+    void *xin_f, *g_f, *f_b_f, *o_f;
 };
 
 extern "C" const char *k3hip_last_error(void) { return g_err; }
@@ -110,7 +112,8 @@ extern "C" int k3hip_kda_release(k3hip_kda_weights *w)
     clear_error();
     if (!w) return K3HIP_OK;
     void *ptrs[] = {w->xin, w->f_b, w->g, w->o, w->q_conv, w->k_conv, w->v_conv, w->A_log,
-                    w->dt_bias, w->o_norm, w->f_b2, w->o2};   // q k v f_a b live inside xin
+                    w->dt_bias, w->o_norm, w->f_b2, w->o2, w->xin_f, w->g_f, w->f_b_f,
+                    w->o_f};   // q k v f_a b live inside xin
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
     free(w);
@@ -181,6 +184,21 @@ extern "C" int k3hip_kda_upload(const K3KdaW *w, const K3Cfg *c, k3hip_kda_weigh
     if (rc == K3HIP_OK && w->wdt == K3_WBF16) {
         rc = twice(&d->f_b2, d->f_b, P, (size_t)D);
         if (rc == K3HIP_OK) rc = twice(&d->o2, d->o, (size_t)E, P);
+    }
+    // fragment-ordered copies for the decode projections (row-major stays for prefill)
+    auto frag = [&](void **dst, const void *src, int N, int Kd) -> int {
+        K3_HIP(hipMalloc(dst, rows_frag_elems(N, Kd) * 2));
+        return rows_frag_pack((const uint16_t *)src, N, Kd, (uint16_t *)*dst, nullptr);
+    };
+    if (rc == K3HIP_OK && w->wdt == K3_WBF16 && E % 8 == 0 && D % 8 == 0) {
+        rc = frag(&d->xin_f, d->xin, (int)(3 * P) + D + H, E);
+        if (rc == K3HIP_OK) rc = frag(&d->g_f, d->g, (int)P, E);
+        if (rc == K3HIP_OK) rc = frag(&d->f_b_f, d->f_b, (int)P, D);
+        if (rc == K3HIP_OK) rc = frag(&d->o_f, d->o, E, (int)P);
+        if (rc == K3HIP_OK && hipStreamSynchronize(nullptr) != hipSuccess) {
+            set_error("k3hip_kda_upload: packing the decode weights failed");
+            rc = K3HIP_EHIP;
+        }
     }
     if (rc != K3HIP_OK) {
         char keep[1024];
@@ -494,8 +512,9 @@ extern "C" int k3hip_kda_layer_decode(const k3hip_kda_weights *w, int B, float *
     if (!w || !out || !x || !states) K3_FAIL(K3HIP_EINVAL, "k3hip_kda_layer_decode: NULL argument");
     if (B < 0) K3_FAIL(K3HIP_EINVAL, "k3hip_kda_layer_decode: B=%d", B);
     if (B == 0) return K3HIP_OK;
-    if (w->wdt != K3_WBF16)
-        K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_layer_decode: bf16 weights only (use k3hip_kda_layer_dev)");
+    if (w->wdt != K3_WBF16 || !w->xin_f)
+        K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_layer_decode: bf16 weights with hidden and head dim multiples "
+                                    "of 8 only (use k3hip_kda_layer_dev)");
     const int E = w->hidden, H = w->H, D = w->D, K = w->K;
     const size_t P = (size_t)H * D;
     const long kper = (long)(P * D + 3 * P * (size_t)(K - 1));
@@ -532,8 +551,8 @@ extern "C" int k3hip_kda_layer_decode(const k3hip_kda_weights *w, int B, float *
     float *q = (float *)(bs + off[3]), *k = q + BP, *v = k + BP, *al = v + BP;
     float *beta = (float *)(bs + off[4]), *o = (float *)(bs + off[5]), *y = (float *)(bs + off[6]);
     float *ws = (float *)(bs + off[7]);
-    const uint16_t *Win = (const uint16_t *)w->xin, *Wg = (const uint16_t *)w->g,
-                   *Wfb = (const uint16_t *)w->f_b, *Wo = (const uint16_t *)w->o;
+    const uint16_t *Win = (const uint16_t *)w->xin_f, *Wg = (const uint16_t *)w->g_f,
+                   *Wfb = (const uint16_t *)w->f_b_f, *Wo = (const uint16_t *)w->o_f;
 
     // 1 projections: the fp32 rows against bf16 weights, each weight read once for all B
     //   (kda_rows.hip: x split into bf16 hi + lo in registers); q, k, v, f_a and the beta

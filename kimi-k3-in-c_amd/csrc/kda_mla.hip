@@ -29,10 +29,11 @@
 struct k3hip_mla_weights {
     int E, H, QL, KL, QN, QR, VH, gate;
     float eps;
-    // q_a, kv_a and g (when gated) are row blocks of one allocation xin ([QL + KL + QR + H*VH]
-    // [hidden], in that order): one pass over them projects a decode step's input
-    void *xin;
-    void *q_a, *q_b, *kv_a, *kv_b, *o, *g;   // bf16
+    // q_a, kv_a and g (when gated) are row blocks of one matrix xin ([QL + KL + QR + H*VH]
+    // [hidden], in that order): one pass over them projects a decode step's input. xin, q_b
+    // and o are stored in MFMA fragment order for the few-rows GEMM (kda_rows.hip); kv_b
+    // stays row-major (bf16) for the head-batched absorb GEMMs.
+    void *xin, *q_b, *kv_b, *o;
     float *q_a_norm, *kv_a_norm;
 };
 
@@ -181,7 +182,7 @@ extern "C" int k3hip_mla_release(k3hip_mla_weights *w)
 {
     clear_error();
     if (!w) return K3HIP_OK;
-    void *ptrs[] = {w->xin, w->q_b, w->kv_b, w->o, w->q_a_norm, w->kv_a_norm};   // q_a kv_a g in xin
+    void *ptrs[] = {w->xin, w->q_b, w->kv_b, w->o, w->q_a_norm, w->kv_a_norm};
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
     free(w);
@@ -200,19 +201,20 @@ extern "C" int k3hip_mla_upload(const K3MlaW *w, const K3Cfg *c, k3hip_mla_weigh
     if (!w->q_a || !w->q_b || !w->kv_a || !w->kv_b || !w->o || !w->q_a_norm || !w->kv_a_norm ||
         (c->mla_out_gate && !w->g))
         K3_FAIL(K3HIP_EINVAL, "k3hip_mla_upload: NULL weight");
+    if ((c->hidden & 7) || (c->q_lora & 7) || ((c->n_heads * c->v_head) & 7))
+        K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_mla_upload: hidden=%d, q_lora=%d, heads*v_head=%d not multiples of 8",
+                c->hidden, c->q_lora, c->n_heads * c->v_head);
     k3hip_mla_weights *d = (k3hip_mla_weights *)calloc(1, sizeof *d);
     if (!d) K3_FAIL(K3HIP_ENOMEM, "k3hip_mla_upload: host allocation");
     d->E = c->hidden; d->H = c->n_heads; d->QL = c->q_lora; d->KL = c->kv_lora;
     d->QN = c->qk_nope; d->QR = c->qk_rope; d->VH = c->v_head; d->gate = c->mla_out_gate && w->g;
     d->eps = c->rms_eps;
     const size_t E = d->E, H = d->H, QH = d->QN + d->QR;
-    if (E % 8)
-        K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_mla_upload: hidden=%zu not a multiple of 8", E);
+    const size_t N1 = (size_t)d->QL + d->KL + d->QR + (d->gate ? H * d->VH : 0);
     {
         const size_t rows[3] = {(size_t)d->QL, (size_t)(d->KL + d->QR), d->gate ? H * d->VH : 0};
         const void *src[3] = {w->q_a, w->kv_a, d->gate ? w->g : nullptr};
-        void **dst[3] = {&d->q_a, &d->kv_a, &d->g};
-        if (hipMalloc(&d->xin, (rows[0] + rows[1] + rows[2]) * E * 2) != hipSuccess) {
+        if (hipMalloc(&d->xin, N1 * E * 2) != hipSuccess) {
             (void)hipGetLastError();
             d->xin = nullptr;
             k3hip_mla_release(d);
@@ -221,8 +223,7 @@ extern "C" int k3hip_mla_upload(const K3MlaW *w, const K3Cfg *c, k3hip_mla_weigh
         size_t at = 0;
         for (int i = 0; i < 3; i++) {
             if (!rows[i]) continue;
-            *dst[i] = (char *)d->xin + at * E * 2;
-            if (hipMemcpy(*dst[i], src[i], rows[i] * E * 2, hipMemcpyHostToDevice) != hipSuccess) {
+            if (hipMemcpy((char *)d->xin + at * E * 2, src[i], rows[i] * E * 2, hipMemcpyHostToDevice) != hipSuccess) {
                 (void)hipGetLastError();
                 k3hip_mla_release(d);
                 K3_FAIL(K3HIP_EHIP, "k3hip_mla_upload: weight copy");
@@ -244,6 +245,22 @@ extern "C" int k3hip_mla_upload(const K3MlaW *w, const K3Cfg *c, k3hip_mla_weigh
             k3hip_mla_release(d);
             K3_FAIL(K3HIP_ENOMEM, "k3hip_mla_upload: device copy of %zu bytes", u.bytes);
         }
+    }
+    // xin, q_b and o into MFMA fragment order (the row-major uploads are only the source)
+    struct { void **w; int N, K; } fr[] = {
+        {&d->xin, (int)N1, (int)E}, {&d->q_b, (int)(H * QH), d->QL}, {&d->o, (int)E, (int)(H * d->VH)}};
+    for (auto &f : fr) {
+        void *packed = nullptr;
+        if (hipMalloc(&packed, rows_frag_elems(f.N, f.K) * 2) != hipSuccess ||
+            rows_frag_pack((const uint16_t *)*f.w, f.N, f.K, (uint16_t *)packed, nullptr) != K3HIP_OK ||
+            hipStreamSynchronize(nullptr) != hipSuccess) {
+            (void)hipGetLastError();
+            if (packed) (void)hipFree(packed);
+            k3hip_mla_release(d);
+            K3_FAIL(K3HIP_EHIP, "k3hip_mla_upload: packing the decode weights failed");
+        }
+        (void)hipFree(*f.w);
+        *f.w = packed;
     }
     *out = d;
     return K3HIP_OK;

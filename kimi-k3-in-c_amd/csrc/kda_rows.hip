@@ -7,17 +7,22 @@
 // for all B rows. The work is bound by reading W (B << the bytes per weight row), so the
 // design goal is HBM bandwidth on W, not MFMA rate.
 //
+// Weight layout: the decode copy of W is stored in MFMA fragment order (rows_frag_pack):
+// for each 16-column group g and 32-wide K-step t, the 64 lanes' B-fragments
+// W[16 g + (lane & 15)][32 t + 8 (lane >> 4) .. + 7] lie in one contiguous 1 KB, so every
+// wave load of the weight is one fully used 1 KB span. Reading the row-major matrix in
+// fragment shape touches 16 rows x 64 B per wave load instead and streams about 25% slower.
+//
 // Precision: x stays fp32. Each 8-element slice of an x row is split in registers into
 // bf16 hi + lo (x = hi + lo to ~2^-17 relative), and both halves go through the same bf16
 // MFMA against the bf16 weight (an exact product) into one fp32 accumulator, so every
 // product keeps fp32 accuracy with no extra weight traffic.
 //
-// Work split: a workgroup of 4 waves owns 128 (or 64) output columns (MFMA column tiles of
-// 16) and one K-range; the K-ranges of a column block are split over workgroups (split-K)
-// so that a launch has about two workgroups per CU. Inside a workgroup the waves take
-// interleaved 64-wide K-units, so each wave reads whole 128-byte lines and the four waves
-// together stream 512 contiguous bytes of each weight row at a time. The four wave partials meet in LDS and are summed in a fixed
-// order; the K-range partials go to a workspace and a second kernel sums them in split
+// Work split: a workgroup of 8 waves owns 64 output columns (4 column groups) and one
+// K-range; its waves take the K-steps of the range round robin. The number of K-ranges per
+// column block (split-K) is chosen so that a launch has about one workgroup per CU: wide N
+// runs unsplit, narrow N splits K. The eight wave partials meet in LDS and are summed in a
+// fixed order; K-range partials go to a workspace and a second kernel sums them in range
 // order. Results are therefore reproducible bit for bit.
 #include <algorithm>
 
@@ -31,8 +36,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int RT_WAVES = 4;   // waves per workgroup
-constexpr int RT_U = 2;       // 64-wide K-units per wave whose loads are issued together
+constexpr int RT_WAVES = 8;   // waves per workgroup
+constexpr int RT_NT = 4;      // 16-column groups per workgroup
 constexpr int RT_SMAX = 16;   // most K-ranges per column block
 
 // x = hi + lo, both bf16 (round to nearest even; lo carries the rounding error of hi)
@@ -50,26 +55,45 @@ __device__ __forceinline__ void split_row8(const f4 &a, const f4 &b, bf16x8 &hi,
     }
 }
 
-// Block (nb, s): columns 16 NT nb .. + 16 NT - 1, K-range [s kchunk, min(K, (s + 1) kchunk)).
-// MT = 16-row tiles of x (B <= 16 MT), NT = 16-column tiles. Wave w takes the 64-wide
-// K-units kbeg + 64 (4 i + w): two MFMA K-steps, so each wave reads whole 128-byte lines
-// of every weight row and x row it touches. Out = P + s * split_stride, row stride ldp.
-template <int MT, int NT>
-__global__ __launch_bounds__(64 * RT_WAVES) void rows_gemm_kernel(
-    int B, int N, int K, int kchunk, const float *__restrict__ x, long ldx,
-    const uint16_t *__restrict__ W, float *__restrict__ P, long ldp, long split_stride)
+// out[u] (16 B) for u = (g KT + t) 64 + lane: W[16 g + (lane & 15)][32 t + 8 (lane >> 4) .. + 7],
+// zero past N and K (K % 8 == 0, so a slice is wholly inside or outside)
+__global__ void rows_frag_pack_kernel(const uint16_t *__restrict__ W, int N, int K, uint4 *__restrict__ out,
+                                      size_t units)
 {
-    __shared__ f32x4 red[RT_WAVES][NT][MT][64];
+    const int KT = (K + 31) / 32;
+    for (size_t u = (size_t)blockIdx.x * blockDim.x + threadIdx.x; u < units; u += (size_t)gridDim.x * blockDim.x) {
+        const int lane = (int)(u & 63);
+        const size_t gt = u >> 6;
+        const int t = (int)(gt % KT), g = (int)(gt / KT);
+        const int n = 16 * g + (lane & 15), k = 32 * t + 8 * (lane >> 4);
+        uint4 v = {0, 0, 0, 0};
+        if (n < N && k < K) v = *reinterpret_cast<const uint4 *>(W + (size_t)n * K + k);
+        out[u] = v;
+    }
+}
+
+// Block (nb, s): column groups 4 nb .. 4 nb + 3, K-steps [s tchunk, min(KT, (s + 1) tchunk)).
+// MT = 16-row tiles of x (B <= 16 MT). Wave w takes K-steps tbeg + w, tbeg + w + 8, ...;
+// each step loads the 4 groups' fragments (4 x 1 KB) and the x slice, then runs the hi and
+// lo MFMAs. Out = P + s * split_stride, row stride ldp.
+template <int MT>
+__global__ __launch_bounds__(64 * RT_WAVES) void rows_gemm_kernel(
+    int B, int N, int K, int tchunk, const float *__restrict__ x, long ldx,
+    const uint16_t *__restrict__ Wf, float *__restrict__ P, long ldp, long split_stride)
+{
+    __shared__ f32x4 red[RT_WAVES][RT_NT][MT][64];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int r16 = lane & 15, kg = lane >> 4;
     const int nb = blockIdx.x, s = blockIdx.y;
-    const int kbeg = s * kchunk, kend = min(K, kbeg + kchunk);
+    const int KT = (K + 31) / 32, NG = (N + 15) / 16;
+    const int tbeg = s * tchunk, tend = min(KT, tbeg + tchunk);
 
-    // per-lane row pointers: weight rows of the NT column tiles (clamped to N - 1; their
-    // results are not stored), x rows of the MT row tiles (clamped to B - 1, zeroed)
-    const uint16_t *wrow[NT];
+    // per-lane fragment streams of the 4 column groups (groups past N clamped to the last
+    // one; their results are not stored), x rows of the MT row tiles (clamped to B - 1, zeroed)
+    const bf16x8 *wg[RT_NT];
 #pragma unroll
-    for (int j = 0; j < NT; j++) wrow[j] = W + (size_t)min(16 * (NT * nb + j) + r16, N - 1) * K;
+    for (int j = 0; j < RT_NT; j++)
+        wg[j] = reinterpret_cast<const bf16x8 *>(Wf) + (size_t)min(RT_NT * nb + j, NG - 1) * KT * 64 + lane;
     const float *xrow[MT];
     bool xlive[MT];
 #pragma unroll
@@ -78,67 +102,55 @@ __global__ __launch_bounds__(64 * RT_WAVES) void rows_gemm_kernel(
         xrow[mt] = x + (size_t)min(16 * mt + r16, B - 1) * ldx;
     }
 
-    f32x4 acc[NT][MT];
+    f32x4 acc[RT_NT][MT];
 #pragma unroll
-    for (int j = 0; j < NT; j++)
+    for (int j = 0; j < RT_NT; j++)
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) acc[j][mt] = 0.0f;
 
-    constexpr int NS = 2 * RT_U;   // K-steps of 32 per iteration
-    for (int k0 = kbeg + 64 * w; k0 < kend; k0 += 64 * RT_WAVES * RT_U) {
-        bf16x8 wv[NS][NT];
-        f4 xa[NS][MT], xb[NS][MT];
-        bool live[NS];
+    for (int t = tbeg + w; t < tend; t += RT_WAVES) {
+        bf16x8 wv[RT_NT];
 #pragma unroll
-        for (int u = 0; u < NS; u++) {
-            const int k = k0 + 64 * RT_WAVES * (u >> 1) + 32 * (u & 1) + 8 * kg;
-            live[u] = k < kend;
-            const int kc = live[u] ? k : kbeg;   // kbeg + 8 <= K: K and kbeg are multiples of 8
+        for (int j = 0; j < RT_NT; j++) wv[j] = wg[j][(size_t)t * 64];
+        const int k = 32 * t + 8 * kg;   // K % 8 == 0: the 8-slice is wholly inside or outside
+        const bool kin = k < K;
+        f4 xa[MT], xb[MT];
 #pragma unroll
-            for (int j = 0; j < NT; j++) wv[u][j] = *reinterpret_cast<const bf16x8 *>(wrow[j] + kc);
-#pragma unroll
-            for (int mt = 0; mt < MT; mt++) {
-                xa[u][mt] = *reinterpret_cast<const f4 *>(xrow[mt] + kc);
-                xb[u][mt] = *reinterpret_cast<const f4 *>(xrow[mt] + kc + 4);
-            }
+        for (int mt = 0; mt < MT; mt++) {
+            xa[mt] = *reinterpret_cast<const f4 *>(xrow[mt] + (kin ? k : 0));
+            xb[mt] = *reinterpret_cast<const f4 *>(xrow[mt] + (kin ? k : 0) + 4);
         }
-        __builtin_amdgcn_sched_barrier(0);   // every load of the iteration in flight first
 #pragma unroll
-        for (int u = 0; u < NS; u++) {
+        for (int mt = 0; mt < MT; mt++) {
+            bf16x8 xh, xl;
+            const bool ok = kin && xlive[mt];
+            split_row8(ok ? xa[mt] : f4(0.0f), ok ? xb[mt] : f4(0.0f), xh, xl);
 #pragma unroll
-            for (int mt = 0; mt < MT; mt++) {
-                bf16x8 xh, xl;
-                const bool ok = live[u] && xlive[mt];
-                split_row8(ok ? xa[u][mt] : f4(0.0f), ok ? xb[u][mt] : f4(0.0f), xh, xl);
-#pragma unroll
-                for (int j = 0; j < NT; j++) {
-                    acc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, wv[u][j], acc[j][mt], 0, 0, 0);
-                    acc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, wv[u][j], acc[j][mt], 0, 0, 0);
-                }
+            for (int j = 0; j < RT_NT; j++) {
+                acc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, wv[j], acc[j][mt], 0, 0, 0);
+                acc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, wv[j], acc[j][mt], 0, 0, 0);
             }
         }
     }
 
-    // wave partials -> LDS; wave w sums column tiles w, w + 4, .. over the 4 waves in order
+    // wave partials -> LDS; wave j < 4 sums column group j over the 8 waves in order
 #pragma unroll
-    for (int j = 0; j < NT; j++)
+    for (int j = 0; j < RT_NT; j++)
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) red[w][j][mt][lane] = acc[j][mt];
     __syncthreads();
+    if (w >= RT_NT) return;
     float *out = P + (size_t)s * split_stride;
+    const int n = 16 * (RT_NT * nb + w) + r16;
 #pragma unroll
-    for (int j = w; j < NT; j += RT_WAVES) {
-        const int n = 16 * (NT * nb + j) + r16;
+    for (int mt = 0; mt < MT; mt++) {
+        f32x4 t = red[0][w][mt][lane];
 #pragma unroll
-        for (int mt = 0; mt < MT; mt++) {
-            f32x4 t = red[0][j][mt][lane];
+        for (int ww = 1; ww < RT_WAVES; ww++) t = t + red[ww][w][mt][lane];
 #pragma unroll
-            for (int ww = 1; ww < RT_WAVES; ww++) t = t + red[ww][j][mt][lane];
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int m = 16 * mt + 4 * kg + e;   // MFMA C layout: lane n + 16 j holds rows 4j..4j+3
-                if (m < B && n < N) out[(size_t)m * ldp + n] = t[e];
-            }
+        for (int e = 0; e < 4; e++) {
+            const int m = 16 * mt + 4 * kg + e;   // MFMA C layout: lane n + 16 j holds rows 4j..4j+3
+            if (m < B && n < N) out[(size_t)m * ldp + n] = t[e];
         }
     }
 }
@@ -179,12 +191,12 @@ __global__ void rows_reduce1_kernel(int B, int N, int S, const float *__restrict
     }
 }
 
-template <int MT, int NT>
-int launch_rows(int B, int N, int K, int kchunk, int S, const float *x, long ldx, const uint16_t *W,
+template <int MT>
+int launch_rows(int B, int N, int K, int tchunk, int S, const float *x, long ldx, const uint16_t *Wf,
                 float *P, long ldp, long split_stride, hipStream_t st)
 {
-    hipLaunchKernelGGL((rows_gemm_kernel<MT, NT>), dim3((N + 16 * NT - 1) / (16 * NT), S), dim3(64 * RT_WAVES),
-                       0, st, B, N, K, kchunk, x, ldx, W, P, ldp, split_stride);
+    hipLaunchKernelGGL((rows_gemm_kernel<MT>), dim3((N + 16 * RT_NT - 1) / (16 * RT_NT), S),
+                       dim3(64 * RT_WAVES), 0, st, B, N, K, tchunk, x, ldx, Wf, P, ldp, split_stride);
     K3_LAUNCHED();
     return K3HIP_OK;
 }
@@ -208,27 +220,42 @@ int cu_total()
 namespace {
 
 struct RowsPlan {
-    int nt, S, kchunk;
+    int S, tchunk;
 };
 
-// 128 output columns per workgroup for very wide N (x is re-read once per column block:
-// 25% of the weight bytes at B <= 16), else 64. K is split into ranges of 512 (one
-// iteration per wave: all of a wave's loads in flight at once) up to RT_SMAX ranges;
-// narrow N (few column blocks) uses no more ranges than about four workgroups per CU.
+// About one workgroup per CU: S = CUs / column blocks K-ranges, rounded up from a fraction of
+// 3/4, at most RT_SMAX and at most one per K-step. N wider than ~4/7 of a column block per
+// CU runs unsplit (measured: 161 blocks on 256 CUs unsplit beat 322 split workgroups).
 RowsPlan rows_plan(int N, int K)
 {
+    const int nblk = (N + 16 * RT_NT - 1) / (16 * RT_NT), KT = (K + 31) / 32;
+    int S = (cu_total() + nblk / 4) / nblk;
+    S = std::max(1, std::min({S, RT_SMAX, KT}));
     RowsPlan p;
-    p.nt = N >= 128 * 64 ? 8 : 4;
-    const int nblk = (N + 16 * p.nt - 1) / (16 * p.nt);
-    const int kunits = (K + 511) / 512;
-    int S = std::min(kunits, RT_SMAX);
-    S = std::max(1, std::min(S, (4 * cu_total() + nblk - 1) / nblk));
-    p.kchunk = ((kunits + S - 1) / S) * 512;
-    p.S = (K + p.kchunk - 1) / p.kchunk;
+    p.tchunk = (KT + S - 1) / S;
+    p.S = (KT + p.tchunk - 1) / p.tchunk;
     return p;
 }
 
 }  // namespace
+
+size_t rows_frag_elems(int N, int K)
+{
+    if (N <= 0 || K <= 0) return 0;
+    return (size_t)((N + 15) / 16) * 16 * ((K + 31) / 32) * 32;
+}
+
+int rows_frag_pack(const uint16_t *W, int N, int K, uint16_t *Wf, hipStream_t st)
+{
+    if (N <= 0 || K <= 0) return K3HIP_OK;
+    if ((K & 7) || (((uintptr_t)W | (uintptr_t)Wf) & 15))
+        K3_FAIL(K3HIP_EINVAL, "rows_frag_pack: K=%d needs a multiple of 8 and 16-byte aligned W", K);
+    const size_t units = rows_frag_elems(N, K) / 8;
+    const int grid = (int)std::min<size_t>((units + 255) / 256, 65536);
+    hipLaunchKernelGGL(rows_frag_pack_kernel, dim3(grid), dim3(256), 0, st, W, N, K, (uint4 *)Wf, units);
+    K3_LAUNCHED();
+    return K3HIP_OK;
+}
 
 size_t gemm_rows_ws_floats(int B, int N, int K)
 {
@@ -237,14 +264,14 @@ size_t gemm_rows_ws_floats(int B, int N, int K)
     return p.S > 1 ? (size_t)p.S * std::min(64, B) * N : 0;
 }
 
-int gemm_rows(int B, int N, int K, const float *x, long ldx, const uint16_t *W, float *C, long ldc,
+int gemm_rows(int B, int N, int K, const float *x, long ldx, const uint16_t *Wf, float *C, long ldc,
               hipStream_t st, float *ws, size_t ws_floats)
 {
     if (B <= 0 || N <= 0 || K <= 0) return K3HIP_OK;
-    if ((K & 7) || (ldx & 3) || (((uintptr_t)x | (uintptr_t)W) & 15))
+    if ((K & 7) || (ldx & 3) || (((uintptr_t)x | (uintptr_t)Wf) & 15))
         K3_FAIL(K3HIP_EINVAL, "gemm_rows: K=%d ldx=%ld need multiples of 8 / 4 and 16-byte aligned x, W", K, ldx);
     const RowsPlan pl = rows_plan(N, K);
-    const int S = pl.S, kchunk = pl.kchunk;
+    const int S = pl.S, tchunk = pl.tchunk;
     const size_t need = gemm_rows_ws_floats(B, N, K);
     StreamBuf own;
     if (need && (!ws || ws_floats < need || ((uintptr_t)ws & 15))) {
@@ -263,25 +290,19 @@ int gemm_rows(int B, int N, int K, const float *x, long ldx, const uint16_t *W, 
         }
         const float *xb = x + (size_t)b0 * ldx;
         int rc;
-        if (pl.nt == 8) {
-            if (bb <= 16) rc = launch_rows<1, 8>(bb, N, K, kchunk, S, xb, ldx, W, P, ldp, sstride, st);
-            else if (bb <= 32) rc = launch_rows<2, 8>(bb, N, K, kchunk, S, xb, ldx, W, P, ldp, sstride, st);
-            else rc = launch_rows<4, 8>(bb, N, K, kchunk, S, xb, ldx, W, P, ldp, sstride, st);
-        } else {
-            if (bb <= 16) rc = launch_rows<1, 4>(bb, N, K, kchunk, S, xb, ldx, W, P, ldp, sstride, st);
-            else if (bb <= 32) rc = launch_rows<2, 4>(bb, N, K, kchunk, S, xb, ldx, W, P, ldp, sstride, st);
-            else rc = launch_rows<4, 4>(bb, N, K, kchunk, S, xb, ldx, W, P, ldp, sstride, st);
-        }
+        if (bb <= 16) rc = launch_rows<1>(bb, N, K, tchunk, S, xb, ldx, Wf, P, ldp, sstride, st);
+        else if (bb <= 32) rc = launch_rows<2>(bb, N, K, tchunk, S, xb, ldx, Wf, P, ldp, sstride, st);
+        else rc = launch_rows<4>(bb, N, K, tchunk, S, xb, ldx, Wf, P, ldp, sstride, st);
         if (rc) return rc;
         if (S > 1) {
             const size_t total = (size_t)bb * N;
             float *Cb = C + (size_t)b0 * ldc;
             if (N % 4 == 0 && ldc % 4 == 0 && ((uintptr_t)Cb & 15) == 0) {
-                const int grid = (int)std::min<size_t>((total / 4 + 255) / 256, 8192);
-                hipLaunchKernelGGL(rows_reduce_kernel, dim3(grid), dim3(256), 0, st, bb, N, S, P, Cb, ldc);
+                const int grid = (int)std::min<size_t>((total / 4 + 63) / 64, 16384);
+                hipLaunchKernelGGL(rows_reduce_kernel, dim3(grid), dim3(64), 0, st, bb, N, S, P, Cb, ldc);
             } else {
-                const int grid = (int)std::min<size_t>((total + 255) / 256, 8192);
-                hipLaunchKernelGGL(rows_reduce1_kernel, dim3(grid), dim3(256), 0, st, bb, N, S, P, Cb, ldc);
+                const int grid = (int)std::min<size_t>((total + 63) / 64, 16384);
+                hipLaunchKernelGGL(rows_reduce1_kernel, dim3(grid), dim3(64), 0, st, bb, N, S, P, Cb, ldc);
             }
             K3_LAUNCHED();
         }
