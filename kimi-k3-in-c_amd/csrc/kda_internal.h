@@ -68,6 +68,22 @@ int rows_frag_pack(const uint16_t *W, int N, int K, uint16_t *Wf, hipStream_t st
 size_t gemm_rows_ws_floats(int B, int N, int K);
 int gemm_rows(int B, int N, int K, const float *x, long ldx, const uint16_t *Wf, float *C, long ldc,
               hipStream_t st, float *ws = nullptr, size_t ws_floats = 0);
+// The same product left as its S = gemm_rows_splits(N, K) K-range partials: planes
+// P[s][B][N], whose sum in increasing s is C bit for bit, for a consumer that adds them
+// itself instead of a reduction launch.
+int gemm_rows_splits(int N, int K);
+int gemm_rows_part(int B, int N, int K, const float *x, long ldx, const uint16_t *Wf, float *P, hipStream_t st);
+
+// One decode token of a KDA layer between its projections (kda_step.hip): K1 + K3 + K4 per
+// (head, sequence). Cin rows (stride ldc) hold q | k | v at columns 0, P, 2P and the beta
+// logits at bcol; Cz [B][P] the decay logits (f_b output); gl the output-gate logits as
+// gsplit planes of gplane floats. states: per sequence (stride floats apart) the H D x D
+// state, then the [3][P][conv_k-1] conv history; both updated in place. y [B][P] out.
+int layer_step(int B, int H, int D, int K, float lb, float eps, float q_scale, const float *Cin,
+               long ldc, int bcol, const float *Cz, const float *gl, int gsplit, long gplane,
+               const float *q_conv, const float *k_conv, const float *v_conv, const float *A_log,
+               const float *dt_bias, const float *o_norm, float *states, long stride, float *y,
+               hipStream_t st);
 
 // p[0..n) = 0 on `st` with a kernel (never a memset node).
 int zero_fill(float *p, size_t n, hipStream_t st);

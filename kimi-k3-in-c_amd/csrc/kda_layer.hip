@@ -413,98 +413,8 @@ extern "C" int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *
 }
 
 // ------------------------------------------------------------- batched decode ----
-// K1 for one token of each of B sequences from the fp32 projections (q, k, v and the beta
-// logits in rows of stride ldc, z in rows of P), with sequence b's conv history
-// in its state slot (states + b*stride + H*D*D, [3][P][K-1], oldest first; shifted in
-// place). One wave per (head, sequence); lanes own D/64 adjacent channels (D >= 64) or one.
-// Arithmetic of kda_prep_math.h; L2 sums fp32 per lane, double across the wave.
-template <int D, int K>
-__global__ __launch_bounds__(64) void kda_step_prep_kernel(
-    int B, int H, float lb, long ldc, const float *__restrict__ Cq, const float *__restrict__ Ck,
-    const float *__restrict__ Cv, const float *__restrict__ Cz, const float *__restrict__ Cb,
-    const float *__restrict__ q_conv, const float *__restrict__ k_conv,
-    const float *__restrict__ v_conv, const float *__restrict__ A_log,
-    const float *__restrict__ dt_bias, float *__restrict__ states, long stride,
-    float *__restrict__ q, float *__restrict__ k, float *__restrict__ v,
-    float *__restrict__ alpha, float *__restrict__ beta)
-{
-#pragma clang fp contract(off)
-    constexpr int CPL = D >= 64 ? D / 64 : 1, NH = K - 1;
-    const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
-    const bool active = lane * CPL < D;
-    const size_t P = (size_t)H * D;
-    const size_t c0 = (size_t)h * D + (active ? lane * CPL : 0);
-    float *hist = states + (size_t)b * stride + (size_t)H * D * D;
-    const float *C2[3] = {Cq, Ck, Cv};
-    const float *cw[3] = {q_conv, k_conv, v_conv};
-    float *outp[3] = {q, k, v};
-    float y[3][CPL];
-#pragma unroll
-    for (int t = 0; t < 3; t++)
-#pragma unroll
-        for (int e = 0; e < CPL; e++) {
-            const size_t ch = c0 + e;
-            const float x = C2[t][(size_t)b * ldc + ch];
-            float w[K], win[NH > 0 ? NH : 1];
-#pragma unroll
-            for (int j = 0; j < K; j++) w[j] = cw[t][ch * K + j];
-            float *hs = hist + ((size_t)t * P + ch) * NH;
-#pragma unroll
-            for (int j = 0; j < NH; j++) win[j] = hs[j];
-            y[t][e] = conv_silu<K>(w, win, x);
-            if (active) {
-#pragma unroll
-                for (int j = 0; j + 1 < NH; j++) hs[j] = win[j + 1];
-                if constexpr (NH > 0) hs[NH - 1] = x;
-            }
-        }
-#pragma unroll
-    for (int t = 0; t < 2; t++) {
-        float part = 0.0f;
-#pragma unroll
-        for (int e = 0; e < CPL; e++) part = part + (active ? y[t][e] * y[t][e] : 0.0f);
-        double ss = (double)part;
-#pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
-        const float r = (float)(1.0 / sqrt(ss + 1e-6));
-#pragma unroll
-        for (int e = 0; e < CPL; e++) y[t][e] = y[t][e] * r;
-    }
-    const float a = expf(A_log[h]);
-    if (active) {
-#pragma unroll
-        for (int e = 0; e < CPL; e++) {
-            const size_t ch = c0 + e, at = (size_t)b * P + ch;
-            for (int t = 0; t < 3; t++) outp[t][at] = y[t][e];
-            const float z = Cz[(size_t)b * P + ch];
-            const float g = lb != 0.0f ? gate_bounded(lb, a, z, dt_bias[ch])
-                                       : -a * softplus_ref(z + dt_bias[ch]);
-            alpha[at] = fast_exp(g);
-        }
-    }
-    if (lane == 0)
-        beta[(size_t)b * H + h] = fast_sigmoid(Cb[(size_t)b * ldc + h]);
-}
-
-template <int D>
-static int step_prep_k(int K, dim3 grid, hipStream_t st, int B, int H, float lb, long ldc, const float *Cq,
-                       const float *Ck, const float *Cv, const float *Cz, const float *Cb,
-                       const k3hip_kda_weights *w, float *states, long stride, float *q, float *k,
-                       float *v, float *al, float *beta)
-{
-#define K3_STEP(KK) hipLaunchKernelGGL((kda_step_prep_kernel<D, KK>), grid, dim3(64), 0, st, B, H, lb, ldc, Cq, Ck, Cv, Cz, Cb, w->q_conv, w->k_conv, w->v_conv, w->A_log, w->dt_bias, states, stride, q, k, v, al, beta)
-    switch (K) {
-    case 1: K3_STEP(1); break;
-    case 2: K3_STEP(2); break;
-    case 3: K3_STEP(3); break;
-    case 4: K3_STEP(4); break;
-    default: K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_layer_decode: conv_k=%d not in 1..4", K);
-    }
-#undef K3_STEP
-    K3_LAUNCHED();
-    return K3HIP_OK;
-}
-
+// One token for each of B sequences: projections on the fragment-ordered decode copies,
+// then the fused K1 + K3 + K4 step kernel, then o_proj. Five launches per layer step.
 extern "C" int k3hip_kda_layer_decode(const k3hip_kda_weights *w, int B, float *out, const float *x,
                                       float *states, long state_stride, void *stream)
 {
@@ -527,14 +437,14 @@ extern "C" int k3hip_kda_layer_decode(const k3hip_kda_weights *w, int B, float *
     const size_t BP = (size_t)B * P;
     if ((E & 7) || (D & 7) || (P & 7) || ((uintptr_t)x & 15))
         K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_layer_decode: hidden=%d D=%d need multiples of 8, x 16-byte aligned", E, D);
-    // scratch: q k v f_a b projections [B][NI] | gate | z | q k v alpha | beta | o | y |
+    // scratch: q k v f_a b projections [B][NI] | output-gate partial planes | z | y |
     //          split-K partials (shared by the projections, which run one after another)
     const int NI = 3 * (int)P + D + H;
     const long ldi = (NI + 3) & ~3;   // a multiple of 4: f_a is read in place as an x operand
-    const size_t wsf = std::max({gemm_rows_ws_floats(B, NI, E), gemm_rows_ws_floats(B, (int)P, E),
-                                 gemm_rows_ws_floats(B, (int)P, D), gemm_rows_ws_floats(B, E, (int)P)});
-    size_t sizes[] = {(size_t)B * ldi * 4, BP * 4, BP * 4, 4 * BP * 4, (size_t)B * H * 4, BP * 4,
-                      BP * 4, wsf * 4};
+    const int gs = gemm_rows_splits((int)P, E);
+    const size_t wsf = std::max({gemm_rows_ws_floats(B, NI, E), gemm_rows_ws_floats(B, (int)P, D),
+                                 gemm_rows_ws_floats(B, E, (int)P)});
+    size_t sizes[] = {(size_t)B * ldi * 4, (size_t)gs * BP * 4, BP * 4, BP * 4, wsf * 4};
     constexpr int NB = sizeof sizes / sizeof sizes[0];
     size_t off[NB], total = 0;
     for (int i = 0; i < NB; i++) {
@@ -545,36 +455,24 @@ extern "C" int k3hip_kda_layer_decode(const k3hip_kda_weights *w, int B, float *
     int rc = stream_alloc(buf, total, st);
     if (rc) return rc;
     char *bs = (char *)buf.p;
-    float *Cin = (float *)(bs + off[0]);
-    float *Cq = Cin, *Ck = Cin + P, *Cv = Cin + 2 * P, *fa = Cin + 3 * P, *Cb = fa + D;
-    float *gl = (float *)(bs + off[1]), *Cz = (float *)(bs + off[2]);
-    float *q = (float *)(bs + off[3]), *k = q + BP, *v = k + BP, *al = v + BP;
-    float *beta = (float *)(bs + off[4]), *o = (float *)(bs + off[5]), *y = (float *)(bs + off[6]);
-    float *ws = (float *)(bs + off[7]);
+    float *Cin = (float *)(bs + off[0]), *fa = Cin + 3 * P;
+    float *glp = (float *)(bs + off[1]), *Cz = (float *)(bs + off[2]), *y = (float *)(bs + off[3]);
+    float *ws = (float *)(bs + off[4]);
     const uint16_t *Win = (const uint16_t *)w->xin_f, *Wg = (const uint16_t *)w->g_f,
                    *Wfb = (const uint16_t *)w->f_b_f, *Wo = (const uint16_t *)w->o_f;
 
     // 1 projections: the fp32 rows against bf16 weights, each weight read once for all B
     //   (kda_rows.hip: x split into bf16 hi + lo in registers); q, k, v, f_a and the beta
-    //   logits in one pass over their concatenated weights
+    //   logits in one pass over their concatenated weights; the output gate left as split-K
+    //   planes that the step kernel adds
     if ((rc = gemm_rows(B, NI, E, x, E, Win, Cin, ldi, st, ws, wsf))) return rc;
-    if ((rc = gemm_rows(B, (int)P, E, x, E, Wg, gl, (long)P, st, ws, wsf))) return rc;
+    if ((rc = gemm_rows_part(B, (int)P, E, x, E, Wg, glp, st))) return rc;
     if ((rc = gemm_rows(B, (int)P, D, fa, ldi, Wfb, Cz, (long)P, st, ws, wsf))) return rc;
-    // 2-5 K1 on one token per sequence, conv history carried in each slot
-    const dim3 grid(H, B);
-    switch (D) {
-    case 16: rc = step_prep_k<16>(K, grid, st, B, H, w->gate_lb, ldi, Cq, Ck, Cv, Cz, Cb, w, states, state_stride, q, k, v, al, beta); break;
-    case 32: rc = step_prep_k<32>(K, grid, st, B, H, w->gate_lb, ldi, Cq, Ck, Cv, Cz, Cb, w, states, state_stride, q, k, v, al, beta); break;
-    case 64: rc = step_prep_k<64>(K, grid, st, B, H, w->gate_lb, ldi, Cq, Ck, Cv, Cz, Cb, w, states, state_stride, q, k, v, al, beta); break;
-    default: rc = step_prep_k<128>(K, grid, st, B, H, w->gate_lb, ldi, Cq, Ck, Cv, Cz, Cb, w, states, state_stride, q, k, v, al, beta); break;
-    }
-    if (rc) return rc;
-    // 6 K3 on the B slots
-    if ((rc = decode_strided(B, H, D, states, state_stride, o, q, k, v, al, beta,
-                             1.0f / sqrtf((float)D), st)))
-        return rc;
-    // 7-8 K4, 9 o_proj
-    if ((rc = k3hip_kda_epilogue(B, H, D, w->rms_eps, o, gl, K3HIP_F32, w->o_norm, y, K3HIP_F32, stream)))
+    // 2-8 K1, K3 and K4 on one token per sequence (kda_step.hip), conv history and state in
+    //   each slot, then 9 o_proj
+    if ((rc = layer_step(B, H, D, K, w->gate_lb, w->rms_eps, 1.0f / sqrtf((float)D), Cin, ldi,
+                         3 * (int)P + D, Cz, glp, gs, (long)BP, w->q_conv, w->k_conv, w->v_conv,
+                         w->A_log, w->dt_bias, w->o_norm, states, state_stride, y, st)))
         return rc;
     return gemm_rows(B, E, (int)P, y, (long)P, Wo, out, E, st, ws, wsf);
 }

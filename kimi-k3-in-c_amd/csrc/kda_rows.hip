@@ -225,11 +225,13 @@ struct RowsPlan {
 
 // About one workgroup per CU: S = CUs / column blocks K-ranges, rounded up from a fraction of
 // 3/4, at most RT_SMAX and at most one per K-step. N wider than ~4/7 of a column block per
-// CU runs unsplit (measured: 161 blocks on 256 CUs unsplit beat 322 split workgroups).
+// CU runs unsplit (measured: 161 blocks on 256 CUs unsplit beat 322 split workgroups), and
+// so does a weight of at most 2 MB, whose launch costs more than its reads.
 RowsPlan rows_plan(int N, int K)
 {
     const int nblk = (N + 16 * RT_NT - 1) / (16 * RT_NT), KT = (K + 31) / 32;
     int S = (cu_total() + nblk / 4) / nblk;
+    if ((size_t)N * K <= ((size_t)1 << 20)) S = 1;
     S = std::max(1, std::min({S, RT_SMAX, KT}));
     RowsPlan p;
     p.tchunk = (KT + S - 1) / S;
@@ -262,6 +264,32 @@ size_t gemm_rows_ws_floats(int B, int N, int K)
     if (B <= 0 || N <= 0 || K <= 0) return 0;
     const RowsPlan p = rows_plan(N, K);
     return p.S > 1 ? (size_t)p.S * std::min(64, B) * N : 0;
+}
+
+int gemm_rows_splits(int N, int K)
+{
+    if (N <= 0 || K <= 0) return 1;
+    return rows_plan(N, K).S;
+}
+
+int gemm_rows_part(int B, int N, int K, const float *x, long ldx, const uint16_t *Wf, float *P, hipStream_t st)
+{
+    if (B <= 0 || N <= 0 || K <= 0) return K3HIP_OK;
+    if ((K & 7) || (ldx & 3) || (((uintptr_t)x | (uintptr_t)Wf) & 15))
+        K3_FAIL(K3HIP_EINVAL, "gemm_rows_part: K=%d ldx=%ld need multiples of 8 / 4 and 16-byte aligned x, W", K, ldx);
+    const RowsPlan pl = rows_plan(N, K);
+    const long plane = (long)B * N;
+    for (int b0 = 0; b0 < B; b0 += 64) {
+        const int bb = std::min(64, B - b0);
+        const float *xb = x + (size_t)b0 * ldx;
+        float *Pb = P + (size_t)b0 * N;
+        int rc;
+        if (bb <= 16) rc = launch_rows<1>(bb, N, K, pl.tchunk, pl.S, xb, ldx, Wf, Pb, N, plane, st);
+        else if (bb <= 32) rc = launch_rows<2>(bb, N, K, pl.tchunk, pl.S, xb, ldx, Wf, Pb, N, plane, st);
+        else rc = launch_rows<4>(bb, N, K, pl.tchunk, pl.S, xb, ldx, Wf, Pb, N, plane, st);
+        if (rc) return rc;
+    }
+    return K3HIP_OK;
 }
 
 int gemm_rows(int B, int N, int K, const float *x, long ldx, const uint16_t *Wf, float *C, long ldc,

@@ -1,0 +1,204 @@
+// SPDX-License-Identifier: Apache-2.0
+// kda_step.hip - one decode token of a whole KDA layer between its projections, for gfx950:
+// K1 (short conv + SiLU, L2 norm, decay gate, beta), K3 (the state recurrence) and K4 (head
+// RMSNorm, sigmoid output gate) fused in one kernel, one workgroup per (head, sequence).
+//
+// Replaces, for T = 1, the reference's k3_kda_layer body between the projections and o_proj
+// (src/core/k3_ops.c:896-947): k3_shortconv + SiLU (:133-165), l2norm_ (:845-851), beta
+// (:903), k3_kda_decay (:168-183), k3_kda_step (:186-243), k3_rmsnorm (:94-102) and the
+// sigmoid gate (:940-947).
+//
+// Everything a (head, sequence) pair needs is local to it: its rows of the projections,
+// its conv history and its D x D state. Fusing the three stages keeps q, k, v, alpha, beta
+// and o in LDS instead of HBM and removes two launches per layer step; the state read is
+// issued first so its HBM latency overlaps the K1 arithmetic.
+//
+// Arithmetic: K1 is that of kda_prep_math.h with one half-wave per row (the wide prep
+// kernel's layout: CPL = max(1, D/32) adjacent channels per lane, fp32 L2 sums), K3 that of
+// kda_decode_kernel (same thread tile, same reduction order), K4 that of
+// kda_epilogue2_kernel (fp32 per-lane squares, double across the row's lanes, hardware
+// sigmoid). The output-gate logits may arrive as split-K partial planes of the gate
+// projection; they are added in plane order, which is what the split-K reduction does.
+#include "kda_internal.h"
+#include "kda_prep_math.h"
+
+namespace k3kda {
+
+template <int D, int K>
+__global__ __launch_bounds__(4 * D) void kda_layer_step_kernel(
+    int H, float lb, float eps, float q_scale, const float *__restrict__ Cin, long ldc, int bcol,
+    const float *__restrict__ Cz, const float *__restrict__ gl, int gsplit, long gplane,
+    const float *__restrict__ q_conv, const float *__restrict__ k_conv,
+    const float *__restrict__ v_conv, const float *__restrict__ A_log,
+    const float *__restrict__ dt_bias, const float *__restrict__ o_norm,
+    float *__restrict__ states, long stride, float *__restrict__ y)
+{
+#pragma clang fp contract(off)
+    constexpr int NT = 4 * D;
+    constexpr int CPR = D / 4;      // float4 column groups per state row
+    constexpr int RPP = NT / CPR;   // rows covered by one pass of the workgroup (16)
+    constexpr int NPASS = D / RPP;  // float4s of state held per thread
+    static_assert(CPR * RPP == NT && NPASS * RPP == D, "tile shape");
+    constexpr int CPL = D >= 32 ? D / 32 : 1;   // K1 channels per lane of a half-wave
+    constexpr int NH = K - 1;
+
+    __shared__ float s_q[D], s_k[D], s_v[D], s_a[D];
+    __shared__ f4 s_red[RPP][CPR];
+    __shared__ f4 s_u[CPR];
+    __shared__ float s_beta;
+
+    const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+    const int cg = tid % CPR, rs = tid / CPR;
+    const size_t P = (size_t)H * D;
+
+    // state first: its latency overlaps the K1 arithmetic below
+    f4 *Sp = reinterpret_cast<f4 *>(states + (size_t)b * stride + (size_t)h * D * D);
+    f4 s[NPASS];
+#pragma unroll
+    for (int m = 0; m < NPASS; m++) s[m] = Sp[(rs + m * RPP) * CPR + cg];
+
+    // K1: task 0..3 = q, k, v, decay gate; half-wave hw takes tasks hw, hw + NT/32, ...
+    const int hw = tid >> 5, l32 = tid & 31;
+    const bool active = l32 * CPL < D;
+    const int cl = active ? l32 * CPL : 0;   // channel within the head
+    const size_t c0 = (size_t)h * D + cl;
+    float *hist = states + (size_t)b * stride + (size_t)H * D * D;   // [3][P][K-1]
+    for (int task = hw; task < 4; task += NT / 32) {
+        float yv[CPL];
+        if (task < 3) {
+            const float *cw = task == 0 ? q_conv : (task == 1 ? k_conv : v_conv);
+#pragma unroll
+            for (int e = 0; e < CPL; e++) {
+                const size_t ch = c0 + e;
+                const float cur = Cin[(size_t)b * ldc + (size_t)task * P + ch];
+                float w[K], win[NH > 0 ? NH : 1];
+#pragma unroll
+                for (int j = 0; j < K; j++) w[j] = cw[ch * K + j];
+                float *hs = hist + ((size_t)task * P + ch) * NH;
+#pragma unroll
+                for (int j = 0; j < NH; j++) win[j] = hs[j];
+                yv[e] = active ? conv_silu<K>(w, win, cur) : 0.0f;
+                if (active) {
+#pragma unroll
+                    for (int j = 0; j + 1 < NH; j++) hs[j] = win[j + 1];
+                    if constexpr (NH > 0) hs[NH - 1] = cur;
+                }
+            }
+            if (task < 2) l2norm_half<CPL>(yv);   // uniform per half-wave: both halves of a wave
+            float *dst = task == 0 ? s_q : (task == 1 ? s_k : s_v);
+            if (active)
+#pragma unroll
+                for (int e = 0; e < CPL; e++) dst[cl + e] = task == 0 ? yv[e] * q_scale : yv[e];
+        } else if (active) {
+            const float a = expf(A_log[h]);
+#pragma unroll
+            for (int e = 0; e < CPL; e++) {
+                const size_t ch = c0 + e;
+                const float z = Cz[(size_t)b * P + ch];
+                const float g = lb != 0.0f ? gate_bounded(lb, a, z, dt_bias[ch])
+                                           : -a * softplus_ref(z + dt_bias[ch]);   // softplus gate
+                s_a[cl + e] = fast_exp(g);
+            }
+        }
+    }
+    if (tid == 0) s_beta = fast_sigmoid(Cin[(size_t)b * ldc + bcol + h]);
+    __syncthreads();
+
+    // K3 (kda_decode_kernel): decay the rows, partial u over this thread's rows
+    const f4 vv = reinterpret_cast<const f4 *>(s_v)[cg];
+    const float bt = s_beta;
+    f4 u = 0.0f;
+#pragma unroll
+    for (int m = 0; m < NPASS; m++) {
+        const int r = rs + m * RPP;
+        const float kr = s_k[r];
+        s[m] = s[m] * s_a[r];
+        if (kr != 0.0f) u = u + kr * s[m];
+    }
+    s_red[rs][cg] = u;
+    __syncthreads();
+    if (tid < CPR) {
+        f4 t = s_red[0][tid];
+#pragma unroll
+        for (int r = 1; r < RPP; r++) t = t + s_red[r][tid];
+        s_u[tid] = t;
+    }
+    __syncthreads();
+    const f4 d = vv - s_u[cg];
+    f4 acc = 0.0f;
+#pragma unroll
+    for (int m = 0; m < NPASS; m++) {
+        const int r = rs + m * RPP;
+        const float kr = s_k[r], qr = s_q[r];
+        if (kr != 0.0f) s[m] = s[m] + (kr * bt) * d;
+        if (qr != 0.0f) acc = acc + qr * s[m];
+        __builtin_nontemporal_store(s[m], &Sp[(rs + m * RPP) * CPR + cg]);
+    }
+    s_red[rs][cg] = acc;   // every read of s_red above finished before the last barrier
+    __syncthreads();
+    if (tid >= CPR) return;
+
+    // K4 (kda_epilogue2_kernel) on o = the CPR lanes' float4s: RMSNorm, then the gate
+    f4 x = s_red[0][tid];
+#pragma unroll
+    for (int r = 1; r < RPP; r++) x = x + s_red[r][tid];
+    const size_t at = (size_t)b * P + (size_t)h * D + 4 * tid;
+    f4 gt = *reinterpret_cast<const f4 *>(gl + at);
+    for (int sp = 1; sp < gsplit; sp++) gt = gt + *reinterpret_cast<const f4 *>(gl + (size_t)sp * gplane + at);
+    const f4 w = reinterpret_cast<const f4 *>(o_norm)[tid];
+    double ss = (double)(((x.x * x.x) + (x.y * x.y)) + ((x.z * x.z) + (x.w * x.w)));
+#pragma unroll
+    for (int m = CPR / 2; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+    const float inv = (float)(1.0 / sqrt(ss / (double)D + (double)eps));
+    f4 out;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-gt[e] * 1.4426950408889634f));
+        out[e] = ((w[e] * x[e]) * inv) * sg;
+    }
+    *reinterpret_cast<f4 *>(y + at) = out;
+}
+
+template <int D>
+static int launch_step(int K, int B, int H, float lb, float eps, float qs, const float *Cin, long ldc,
+                       int bcol, const float *Cz, const float *gl, int gsplit, long gplane,
+                       const float *q_conv, const float *k_conv, const float *v_conv,
+                       const float *A_log, const float *dt_bias, const float *o_norm, float *states,
+                       long stride, float *y, hipStream_t st)
+{
+#define K3_STEP(KK)                                                                              \
+    hipLaunchKernelGGL((kda_layer_step_kernel<D, KK>), dim3(H, B), dim3(4 * D), 0, st, H, lb, eps, qs, \
+                       Cin, ldc, bcol, Cz, gl, gsplit, gplane, q_conv, k_conv, v_conv, A_log,    \
+                       dt_bias, o_norm, states, stride, y)
+    switch (K) {
+    case 1: K3_STEP(1); break;
+    case 2: K3_STEP(2); break;
+    case 3: K3_STEP(3); break;
+    case 4: K3_STEP(4); break;
+    default: K3_FAIL(K3HIP_EUNSUPPORTED, "layer step: conv_k=%d not in 1..4", K);
+    }
+#undef K3_STEP
+    K3_LAUNCHED();
+    return K3HIP_OK;
+}
+
+int layer_step(int B, int H, int D, int K, float lb, float eps, float q_scale, const float *Cin,
+               long ldc, int bcol, const float *Cz, const float *gl, int gsplit, long gplane,
+               const float *q_conv, const float *k_conv, const float *v_conv, const float *A_log,
+               const float *dt_bias, const float *o_norm, float *states, long stride, float *y,
+               hipStream_t st)
+{
+    if (B <= 0 || H <= 0) return K3HIP_OK;
+    if (gsplit < 1 || ((uintptr_t)gl & 15) || (gplane & 3) || ((uintptr_t)y & 15) || ((uintptr_t)states & 15) ||
+        (stride & 3))
+        K3_FAIL(K3HIP_EINVAL, "layer step: gate planes, y or states misaligned");
+    switch (D) {
+    case 16: return launch_step<16>(K, B, H, lb, eps, q_scale, Cin, ldc, bcol, Cz, gl, gsplit, gplane, q_conv, k_conv, v_conv, A_log, dt_bias, o_norm, states, stride, y, st);
+    case 32: return launch_step<32>(K, B, H, lb, eps, q_scale, Cin, ldc, bcol, Cz, gl, gsplit, gplane, q_conv, k_conv, v_conv, A_log, dt_bias, o_norm, states, stride, y, st);
+    case 64: return launch_step<64>(K, B, H, lb, eps, q_scale, Cin, ldc, bcol, Cz, gl, gsplit, gplane, q_conv, k_conv, v_conv, A_log, dt_bias, o_norm, states, stride, y, st);
+    case 128: return launch_step<128>(K, B, H, lb, eps, q_scale, Cin, ldc, bcol, Cz, gl, gsplit, gplane, q_conv, k_conv, v_conv, A_log, dt_bias, o_norm, states, stride, y, st);
+    default: K3_FAIL(K3HIP_EUNSUPPORTED, "layer step: D=%d not in {16,32,64,128}", D);
+    }
+}
+
+}  // namespace k3kda
