@@ -62,6 +62,8 @@ __global__ __launch_bounds__(256) void kda_epilogue_kernel(long rows, int H, flo
 // y as a bf16 hi/lo pair (y = hi + lo to about 2^-17), rows [T][2P]: hi in the first P
 // columns, lo in the last P -- the input of a K = 2P bf16 GEMM against [W | W].
 constexpr int Y_SPLIT = 2;
+// y as fp16 [T][P] (the o_proj GEMM's fp16 operand; |y| <= sqrt(D) max|o_norm|)
+constexpr int Y_F16 = K3_DT_F16;
 
 template <int D, int GDT, int YDT>
 __global__ __launch_bounds__(256) void kda_epilogue2_kernel(long rows, int H, float eps,
@@ -99,7 +101,13 @@ __global__ __launch_bounds__(256) void kda_epilogue2_kernel(long rows, int H, fl
             v[e] = ((w[e] * x[e]) * inv) * sg;
         }
         if (live) {
-            if constexpr (YDT == Y_SPLIT) {
+            if constexpr (YDT == Y_F16) {
+                uint16_t hv[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) hv[e] = __builtin_bit_cast(uint16_t, (_Float16)v[e]);
+                *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(y) + base) =
+                    uint2{(uint32_t)hv[0] | ((uint32_t)hv[1] << 16), (uint32_t)hv[2] | ((uint32_t)hv[3] << 16)};
+            } else if constexpr (YDT == Y_SPLIT) {
                 // row r = t*H + h of y2 [T][2P]: hi at t*2P + h*D, lo P further
                 const size_t at = base + (size_t)(r / H) * (size_t)(H * D);
                 uint16_t hb[4], lb[4];
@@ -157,7 +165,7 @@ static int epi_types(int gdt, int ydt, long rows, int H, float eps, const float 
 }
 
 int epilogue_split(int T, int H, int D, float eps, const float *o, const void *gate, int gate_dtype,
-                   const float *o_norm, void *y2, hipStream_t st)
+                   const float *o_norm, void *y2, hipStream_t st, bool y_f16)
 {
     const long rows = (long)T * H;
     if (rows == 0) return K3HIP_OK;
@@ -167,6 +175,14 @@ int epilogue_split(int T, int H, int D, float eps, const float *o, const void *g
     long blocks = (rows + 4 * (256 / D) - 1) / (4 * (256 / D));
     if (blocks > 16384) blocks = 16384;
     const bool g16 = gate_dtype == K3HIP_BF16;
+    if (y_f16) {
+#define K3_EPI16(DD, G) hipLaunchKernelGGL((kda_epilogue2_kernel<DD, G, Y_F16>), dim3((unsigned)blocks), dim3(256), 0, st, rows, H, eps, o, gate, o_norm, y2)
+        if (D == 128) { if (g16) K3_EPI16(128, K3HIP_BF16); else K3_EPI16(128, K3HIP_F32); }
+        else { if (g16) K3_EPI16(64, K3HIP_BF16); else K3_EPI16(64, K3HIP_F32); }
+#undef K3_EPI16
+        K3_LAUNCHED();
+        return K3HIP_OK;
+    }
     if (D == 128) {
         if (g16) hipLaunchKernelGGL((kda_epilogue2_kernel<128, K3HIP_BF16, Y_SPLIT>), dim3((unsigned)blocks), dim3(256), 0, st, rows, H, eps, o, gate, o_norm, y2);
         else hipLaunchKernelGGL((kda_epilogue2_kernel<128, K3HIP_F32, Y_SPLIT>), dim3((unsigned)blocks), dim3(256), 0, st, rows, H, eps, o, gate, o_norm, y2);

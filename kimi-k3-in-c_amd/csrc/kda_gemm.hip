@@ -10,7 +10,7 @@
 // (K x M, ld K), D = C^T (N x M, ld N).
 //
 // Per device: one handle and one workspace, created on first use. On the first call of a
-// shape (M, N, K, C dtype) up to 8 heuristic candidates are timed on that call's buffers and
+// shape (M, N, K, C dtype) up to 24 heuristic candidates are timed on that call's buffers and
 // the fastest is cached; that first call synchronizes its stream (keep it out of graph
 // capture). Later calls are stream-ordered on the caller's stream.
 #include <hipblaslt/hipblaslt.h>
@@ -80,12 +80,12 @@ int set_batch(hipblasLtMatrixLayout_t l, int batch, long stride)
 
 // Candidates from the heuristic, each timed on the call's own buffers (first call of a
 // shape only; that call synchronizes the stream). The fastest is kept.
-constexpr int NCAND = 8;
+constexpr int NCAND = 24;
 
 int make_plan(DevGemm &d, const GemmDesc &g, Plan &p, const void *A, const void *B, void *Cm,
               hipStream_t st)
 {
-    const hipDataType abt = g.ab_dtype == K3HIP_BF16 ? HIP_R_16BF : HIP_R_32F;
+    const hipDataType abt = g.ab_dtype == K3HIP_BF16 ? HIP_R_16BF : g.ab_dtype == K3_DT_F16 ? HIP_R_16F : HIP_R_32F;
     const hipDataType ct = g.c_dtype == K3HIP_BF16 ? HIP_R_16BF : HIP_R_32F;
     K3_LT(hipblasLtMatmulDescCreate(&p.op, HIPBLAS_COMPUTE_32F, HIP_R_32F));
     // column-major view: C^T (N x M) = op(B') . op(A'), B' = B, A' = A
@@ -153,7 +153,7 @@ int gemm(const GemmDesc &g, const void *A, const void *B, void *C, hipStream_t s
 {
     if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.batch <= 0) return K3HIP_OK;
     if ((g.c_dtype != K3HIP_BF16 && g.c_dtype != K3HIP_F32) ||
-        (g.ab_dtype != K3HIP_BF16 && g.ab_dtype != K3HIP_F32))
+        (g.ab_dtype != K3HIP_BF16 && g.ab_dtype != K3HIP_F32 && g.ab_dtype != K3_DT_F16))
         K3_FAIL(K3HIP_EINVAL, "gemm: dtypes %d/%d", g.ab_dtype, g.c_dtype);
     int dev = 0;
     K3_HIP(hipGetDevice(&dev));
@@ -185,6 +185,15 @@ int gemm_bf16(int M, int N, int K, const void *A, const void *W, void *C, int c_
     GemmDesc g;
     g.M = M; g.N = N; g.K = K;
     g.ab_dtype = K3HIP_BF16; g.c_dtype = c_dtype; g.b_trans = true;
+    g.lda = K; g.ldb = K; g.ldc = N;
+    return gemm(g, A, W, C, st);
+}
+
+int gemm_f16(int M, int N, int K, const void *A, const void *W, void *C, int c_dtype, hipStream_t st)
+{
+    GemmDesc g;
+    g.M = M; g.N = N; g.K = K;
+    g.ab_dtype = K3_DT_F16; g.c_dtype = c_dtype; g.b_trans = true;
     g.lda = K; g.ldb = K; g.ldc = N;
     return gemm(g, A, W, C, st);
 }

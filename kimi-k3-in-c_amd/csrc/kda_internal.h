@@ -12,6 +12,9 @@ int proj(int T, int in, int out, const float *x, const void *W, int wdt, float *
 // Row-major C[M][N] = A[M][K] . op(B) with fp32 accumulation (hipBLASLt): op(B) = B^T for
 // B [N][K] (b_trans) or B for B [K][N]; A and B both bf16 or both fp32; C bf16 or fp32;
 // leading dimensions in elements; `batch` strided problems (strides in elements).
+// fp16 operands/results, internal only (the public dtypes are K3HIP_F32 and K3HIP_BF16)
+constexpr int K3_DT_F16 = 3;
+
 struct GemmDesc {
     int M = 0, N = 0, K = 0;
     int ab_dtype = K3HIP_BF16, c_dtype = K3HIP_F32;
@@ -25,11 +28,14 @@ int gemm(const GemmDesc &g, const void *A, const void *B, void *C, hipStream_t s
 
 // C[M][N] = A[M][K] . W[N][K]^T on bf16 MFMA, A, W bf16 row-major, C bf16 or fp32.
 int gemm_bf16(int M, int N, int K, const void *A, const void *W, void *C, int c_dtype, hipStream_t st);
+// The same on fp16 MFMA (A, W fp16 row-major), fp32 accumulation.
+int gemm_f16(int M, int N, int K, const void *A, const void *W, void *C, int c_dtype, hipStream_t st);
 
 // K4 with y written as a bf16 hi/lo pair into y2 [T][2P] (hi columns 0..P-1, lo P..2P-1),
 // for an o_proj GEMM with K = 2P against [W_o | W_o]. D = 64 / 128, 16-byte aligned.
+// y as fp16 [T][P] (y_f16 true) or as a bf16 hi/lo pair [T][2P] (hi in the first P columns)
 int epilogue_split(int T, int H, int D, float eps, const float *o, const void *gate, int gate_dtype,
-                   const float *o_norm, void *y2, hipStream_t st);
+                   const float *o_norm, void *y2, hipStream_t st, bool y_f16 = false);
 
 // x [B][N] fp32 -> y [2B][N] bf16: rows 0..B-1 = hi, rows B..2B-1 = lo = bf16(x - hi), the
 // input of a GEMM that reads each weight once for both halves.

@@ -76,7 +76,8 @@ struct k3hip_kda_weights {
     void *xin;
     void *q, *k, *v, *f_a, *f_b, *b, *g, *o;        // matrices, wdt storage
     float *q_conv, *k_conv, *v_conv, *A_log, *dt_bias, *o_norm;
-    void *f_b2, *o2;   // bf16 only: [W | W] along K, for GEMMs on hi/lo-split inputs
+    void *f_b2;   // bf16 only: [W | W] along K, for the f_b GEMM on a hi/lo-split f_a
+    void *o16;    // bf16 only: W_o as fp16 (exact), for the prefill o_proj on fp16 y
     // bf16 only: decode copies of xin, g, f_b and o in MFMA fragment order (kda_rows.hip)
     void *xin_f, *g_f, *f_b_f, *o_f;
 };
@@ -98,6 +99,18 @@ extern "C" int k3hip_device_count(void)
     return n;
 }
 
+// bf16 -> fp16: exact for values inside fp16's normal range; *bad = 1 when a value is beyond
+// fp16's largest finite value (or not finite)
+__global__ void bf16_to_f16_kernel(const uint16_t *__restrict__ w, uint16_t *__restrict__ h, size_t n,
+                                   int *__restrict__ bad)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const float f = bf2f(w[i]);
+        if (!(fabsf(f) <= 65504.0f)) *bad = 1;
+        h[i] = __builtin_bit_cast(uint16_t, (_Float16)f);
+    }
+}
+
 static int upload(void **dst, const void *src, size_t bytes)
 {
     *dst = nullptr;
@@ -112,7 +125,7 @@ extern "C" int k3hip_kda_release(k3hip_kda_weights *w)
     clear_error();
     if (!w) return K3HIP_OK;
     void *ptrs[] = {w->xin, w->f_b, w->g, w->o, w->q_conv, w->k_conv, w->v_conv, w->A_log,
-                    w->dt_bias, w->o_norm, w->f_b2, w->o2, w->xin_f, w->g_f, w->f_b_f,
+                    w->dt_bias, w->o_norm, w->f_b2, w->o16, w->xin_f, w->g_f, w->f_b_f,
                     w->o_f};   // q k v f_a b live inside xin
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
@@ -181,9 +194,34 @@ extern "C" int k3hip_kda_upload(const K3KdaW *w, const K3Cfg *c, k3hip_kda_weigh
         K3_HIP(hipMemcpy2D((char *)*dst + rb, 2 * rb, src, rb, rb, rows, hipMemcpyDeviceToDevice));
         return K3HIP_OK;
     };
+    // W_o as fp16 for the prefill o_proj (y is RMS-normalised, so fp16 holds it)
+    auto to_f16 = [&](void **dst, const void *src, size_t n) -> int {
+        int *bad = nullptr, hbad = 0;
+        K3_HIP(hipMalloc(dst, n * 2));
+        K3_HIP(hipMalloc(&bad, sizeof(int)));
+        int r = K3HIP_OK;
+        if (hipMemcpy(bad, &hbad, sizeof(int), hipMemcpyHostToDevice) != hipSuccess) r = K3HIP_EHIP;
+        if (r == K3HIP_OK) {
+            const size_t blocks = std::min<size_t>((n + 255) / 256, 8192);
+            hipLaunchKernelGGL(bf16_to_f16_kernel, dim3((unsigned)blocks), dim3(256), 0, nullptr,
+                               (const uint16_t *)src, (uint16_t *)*dst, n, bad);
+            if (hipGetLastError() != hipSuccess || hipMemcpy(&hbad, bad, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess)
+                r = K3HIP_EHIP;
+        }
+        (void)hipFree(bad);
+        if (r) {
+            set_error("k3hip_kda_upload: fp16 copy of W_o failed");
+            return r;
+        }
+        if (hbad) {
+            (void)hipFree(*dst);
+            *dst = nullptr;   // the prefill refuses these weights; decode does not need the copy
+        }
+        return K3HIP_OK;
+    };
     if (rc == K3HIP_OK && w->wdt == K3_WBF16) {
         rc = twice(&d->f_b2, d->f_b, P, (size_t)D);
-        if (rc == K3HIP_OK) rc = twice(&d->o2, d->o, (size_t)E, P);
+        if (rc == K3HIP_OK) rc = to_f16(&d->o16, d->o, (size_t)E * P);
     }
     // fragment-ordered copies for the decode projections (row-major stays for prefill)
     auto frag = [&](void **dst, const void *src, int N, int Kd) -> int {
@@ -343,8 +381,10 @@ extern "C" int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *
     if ((x_dtype != K3HIP_F32 && x_dtype != K3HIP_BF16) || (out_dtype != K3HIP_F32 && out_dtype != K3HIP_BF16))
         K3_FAIL(K3HIP_EINVAL, "k3hip_kda_layer_prefill: x_dtype=%d out_dtype=%d", x_dtype, out_dtype);
     const int E = w->hidden, H = w->H, D = w->D, K = w->K;
-    if (w->wdt != K3_WBF16 || !w->o2 || !w->f_b2)
+    if (w->wdt != K3_WBF16 || !w->f_b2)
         K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_layer_prefill: bf16 weights only (use k3hip_kda_layer_dev)");
+    if (!w->o16)
+        K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_layer_prefill: W_o has values beyond fp16 range (use k3hip_kda_layer_dev)");
     if (!chunk_gate_ok(w->gate_lb) || (D != 64 && D != 128) || K > 4)
         K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_layer_prefill: gate_lb=%g D=%d conv_k=%d outside the "
                 "chunked prefill (use k3hip_kda_layer_dev)", w->gate_lb, D, K);
@@ -354,10 +394,12 @@ extern "C" int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *
     const size_t wsb = k3hip_kda_chunk_workspace(T, H, D, 64);
     // scratch, 256-byte aligned pieces:
     //   0 x bf16 | 1 q k v gate projections fp32 | 2 f_a fp32 | 3 f_a hi/lo bf16 | 4 z fp32 |
-    //   5 b logits | 6 o fp32 | 7 y hi/lo bf16 | 8 zero state | 9 chunk workspace
+    //   5 b logits | 6 o fp32 | 7 y fp16 | 8 zero state | 9 chunk workspace |
+    //   10 fp32 o_proj result for a bf16 out (hipBLASLt has no fp16 x fp16 -> bf16 GEMM)
     size_t sizes[] = {x_dtype == K3HIP_F32 ? (size_t)T * E * 2 : 0, 4 * TP * 4, (size_t)T * D * 4,
-                      (size_t)T * D * 4, TP * 4, (size_t)T * H * 4, TP * 4, TP * 4,
-                      state ? 0 : (size_t)H * D * D * 4, wsb};
+                      (size_t)T * D * 4, TP * 4, (size_t)T * H * 4, TP * 4, TP * 2,
+                      state ? 0 : (size_t)H * D * D * 4, wsb,
+                      out_dtype == K3HIP_BF16 ? (size_t)T * E * 4 : 0};
     constexpr int NB = sizeof sizes / sizeof sizes[0];
     size_t off[NB], total = 0;
     for (int i = 0; i < NB; i++) {
@@ -381,7 +423,7 @@ extern "C" int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *
     uint16_t *fa2 = (uint16_t *)(base + off[3]);
     float *z = (float *)(base + off[4]), *bl = (float *)(base + off[5]);
     float *o = (float *)(base + off[6]);
-    uint16_t *y2 = (uint16_t *)(base + off[7]);
+    uint16_t *y16 = (uint16_t *)(base + off[7]);
     float *S = state;
     if (!S) {
         S = (float *)(base + off[8]);
@@ -406,10 +448,17 @@ extern "C" int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *
                                 w->k_conv, w->v_conv, w->A_log, w->dt_bias, cs,
                                 1.0f / sqrtf((float)D), S, o, base + off[9], wsb, stream)))
         return rc;
-    // 7-8 head RMSNorm, then the gate; y as a bf16 hi/lo pair
-    if ((rc = epilogue_split(T, H, D, w->rms_eps, o, gl, K3HIP_F32, w->o_norm, y2, st))) return rc;
-    // 9 o_proj: K = 2P against [W_o | W_o]
-    return gemm_bf16(T, E, 2 * (int)P, y2, w->o2, out, out_dtype, st);
+    // 7-8 head RMSNorm, then the gate; y in fp16 (11-bit significand: the o_proj product
+    //   keeps ~3e-4 relative error, inside the prefill tolerance, at bf16 MFMA speed)
+    if ((rc = epilogue_split(T, H, D, w->rms_eps, o, gl, K3HIP_F32, w->o_norm, y16, st, true))) return rc;
+    // 9 o_proj on fp16 MFMA against the fp16 copy of W_o
+    if (out_dtype == K3HIP_F32) return gemm_f16(T, E, (int)P, y16, w->o16, out, K3HIP_F32, st);
+    float *o32 = (float *)(base + off[10]);
+    if ((rc = gemm_f16(T, E, (int)P, y16, w->o16, o32, K3HIP_F32, st))) return rc;
+    const size_t n = (size_t)T * E;
+    hipLaunchKernelGGL(to_bf16_kernel, dim3(grid_for(n)), dim3(256), 0, st, o32, (uint16_t *)out, n);
+    K3_LAUNCHED();
+    return K3HIP_OK;
 }
 
 // ------------------------------------------------------------- batched decode ----
