@@ -333,7 +333,7 @@ def bench_layer(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
         "wall_ms_per_step": wall / steps * 1e3,
         "config": {"workload": "kda_layer_prefill", "hidden": E, "heads": H, "head_dim": D, "T": T,
                    "chunk": 64, "batch": 1, "conv_k": K, "weights": "bf16", "activations": "bf16 in",
-                   "intermediates": "fp32 (hi/lo bf16 pairs into the f_b and o_proj GEMMs)"},
+                   "intermediates": "fp32; f_a as a bf16 hi/lo pair into f_b; y in fp16 into o_proj (fp16 copy of W_o)"},
         "roofline": {"kernel": "k3hip_kda_layer_prefill (full layer, full-layer accounting)",
                      "bound": "mfma", "achieved": flops / step_s / 1e12, "peak": BF16_PEAK / 1e12,
                      "unit": "TFLOP/s", "frac": flops / step_s / BF16_PEAK, "traffic": None,
