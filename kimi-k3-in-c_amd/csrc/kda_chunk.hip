@@ -711,7 +711,11 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra_act(
 //                           S = diag(e^G_last) S + (K e^(G_last - G))^T Vn
 // Per chunk: state waves publish S to LDS -> barrier -> row waves publish Vn -> barrier
 // -> row waves finish O while state waves update S. Each role prefetches the next chunk's
-// operands into a second register set (used alternately, no copies).
+// operands into a second register set (used alternately, no copies), issuing the loads in
+// windows where it does not hold up the other role: state waves between the two barriers
+// (they wait for Vn there), row waves spread over their products (P2_MID). A step's O rows
+// are stored at the start of the next step, before its loads, so the stores do not queue
+// behind a full vector-memory path (c2 prefill kernels 598 -> 565 us).
 template <int D, int NW> struct RowOps {
     static constexpr int KSI = D / 32;
     Frag wf[KSI], qf[KSI], af[2];
@@ -722,6 +726,12 @@ template <int D> struct StateOps {
     Frag kf[RTW][2];
     f32x4 gl[RTW];
 };
+
+// Of the next chunk's row operands (load_row_part parts 0 .. KSI), a row wave issues parts
+// 0 .. P2_MID-1 between the K-steps of this step's W S / Q S products and the rest after
+// barrier (2), so its loads share the CU's vector-memory path with the state waves' loads
+// (issued between the two barriers) instead of all queueing at the start of the step.
+constexpr int P2_MID = 3;
 
 // Row wave w's operands of one chunk: W, Q e^G and A_qk fragments of its 16 token rows
 // (shared by all of the workgroup's column tiles) and U for each tile ct0 .. ct0+NW-1.
@@ -741,6 +751,26 @@ __device__ __forceinline__ void load_row_ops(RowOps<D, NW> &op, const char *blk,
 #pragma unroll
     for (int j = 0; j < NW; j++)
         op.u[j] = *reinterpret_cast<const f32x4 *>(blk + WL::UC + ((size_t)(w * WL::NCT + ct0 + j) * 64 + lane) * 16);
+}
+
+// One part of load_row_ops: part < KSI loads K-step `part` of W and Q e^G; part == KSI the
+// A_qk fragments and U.
+template <int D, int NW>
+__device__ __forceinline__ void load_row_part(RowOps<D, NW> &op, const char *blk, int w, int lane, int ct0, int part)
+{
+    using WL = Ws<D>;
+    constexpr int KSI = WL::KSI;
+    if (part < KSI) {
+        op.wf[part] = load_frag(blk + WL::WF + (size_t)(w * KSI + part) * 2048, lane);
+        op.qf[part] = load_frag(blk + WL::QF + (size_t)(w * KSI + part) * 2048, lane);
+    } else {
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++)
+            if (ks == 0 || w >= 2) op.af[ks] = load_frag(blk + WL::AF + (size_t)(w * 2 + ks) * 2048, lane);
+#pragma unroll
+        for (int j = 0; j < NW; j++)
+            op.u[j] = *reinterpret_cast<const f32x4 *>(blk + WL::UC + ((size_t)(w * WL::NCT + ct0 + j) * 64 + lane) * 16);
+    }
 }
 
 // sw = state-wave index 0..3; its tiles are rows 16*(RTW*sw + r) .. +15
@@ -798,12 +828,11 @@ template <int D> struct P2Lds {
     static constexpr size_t VF = (size_t)2 * 2 * 1024;
 };
 
-template <int D, int NW>
+template <int D, int NW, typename Mid, typename After2>
 __device__ __forceinline__ void row_step(const RowOps<D, NW> &op, const char *sSF, char *sVF, int w,
-                                         int lane, int nrows, float *ob, size_t P)
+                                         int lane, f32x4 (&oval)[NW], Mid &&mid, After2 &&after2)
 {
     constexpr int KSI = D / 32;
-    const int m = lane & 15, kg = lane >> 4;
     f32x4 ao[NW];
 #pragma unroll
     for (int j = 0; j < NW; j++) {
@@ -820,11 +849,13 @@ __device__ __forceinline__ void row_step(const RowOps<D, NW> &op, const char *sS
                 aw0 = mma3(aw0, op.wf[ks].hi, op.wf[ks].lo, sf.hi, sf.lo);
                 ao0 = mma3(ao0, op.qf[ks].hi, op.qf[ks].lo, sf.hi, sf.lo);
             }
+            if (j == 0) mid(ks);
         }
         publish_frag4(sVF + (size_t)j * P2Lds<D>::VF, w, lane, op.u[j] - (aw0 + aw1));
         ao[j] = ao0 + ao1;
     }
     __syncthreads();   // (2) Vn published
+    after2();
 #pragma unroll
     for (int j = 0; j < NW; j++) {
         const char *vf_j = sVF + (size_t)j * P2Lds<D>::VF;
@@ -834,12 +865,22 @@ __device__ __forceinline__ void row_step(const RowOps<D, NW> &op, const char *sS
             const Frag v1 = read_frag(vf_j, 1, lane);
             a = mma3(a, op.af[1].hi, op.af[1].lo, v1.hi, v1.lo);
         }
+        oval[j] = a;
+    }
+}
+
+// O rows of one chunk step from row wave w (stored one step later, ahead of that step's loads)
+template <int NW>
+__device__ __forceinline__ void store_o(const f32x4 (&oval)[NW], int w, int lane, int nrows, float *ob, size_t P)
+{
+    const int m = lane & 15, kg = lane >> 4;
+#pragma unroll
+    for (int j = 0; j < NW; j++)
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const int t = 16 * w + 4 * kg + e;
-            if (t < nrows) ob[(size_t)t * P + 16 * j + m] = a[e];
+            if (t < nrows) ob[(size_t)t * P + 16 * j + m] = oval[j][e];
         }
-    }
 }
 
 template <int D, int NW>
@@ -902,17 +943,36 @@ __global__ __launch_bounds__(512) void kda_chunk_state(int T, int H, const char 
         RowOps<D, NW> opA, opB;
         float *ob = o + (size_t)h * D + j0;
         load_row_ops<D, NW>(opA, blk_of(0), w, lane, ct0);
+        f32x4 pend[NW];
+        int pend_c = -1;
+        auto mid_of = [&](RowOps<D, NW> &op, int cc) {
+            return [&op, cc, &blk_of, w, lane, ct0](int ks) {
+                if (ks < P2_MID) load_row_part<D, NW>(op, blk_of(cc), w, lane, ct0, ks);
+                if (ks == D / 32 - 1 && P2_MID > D / 32) load_row_part<D, NW>(op, blk_of(cc), w, lane, ct0, D / 32);
+            };
+        };
+        auto after_of = [&](RowOps<D, NW> &op, int cc) {
+            return [&op, cc, &blk_of, w, lane, ct0]() {
+#pragma unroll
+                for (int p = P2_MID; p <= D / 32; p++) load_row_part<D, NW>(op, blk_of(cc), w, lane, ct0, p);
+                __builtin_amdgcn_sched_barrier(0);
+            };
+        };
+        auto flush = [&]() {
+            if (pend_c >= 0) store_o<NW>(pend, w, lane, T - pend_c * CH, ob + (size_t)pend_c * CH * P, P);
+        };
         for (int c = 0; c < nch; c += 2) {
-            load_row_ops<D, NW>(opB, blk_of(c + 1), w, lane, ct0);
-            __builtin_amdgcn_sched_barrier(0);   // keep the prefetch ahead of the step
             __syncthreads();   // (1) S published
-            row_step<D, NW>(opA, sSF, sVF, w, lane, T - c * CH, ob + (size_t)c * CH * P, P);
+            flush();
+            row_step<D, NW>(opA, sSF, sVF, w, lane, pend, mid_of(opB, c + 1), after_of(opB, c + 1));
+            pend_c = c;
             if (c + 1 >= nch) break;
-            load_row_ops<D, NW>(opA, blk_of(c + 2), w, lane, ct0);
-            __builtin_amdgcn_sched_barrier(0);
             __syncthreads();
-            row_step<D, NW>(opB, sSF, sVF, w, lane, T - (c + 1) * CH, ob + (size_t)(c + 1) * CH * P, P);
+            flush();
+            row_step<D, NW>(opB, sSF, sVF, w, lane, pend, mid_of(opA, c + 2), after_of(opA, c + 2));
+            pend_c = c + 1;
         }
+        flush();
     } else {
         const int sw = w - 4;
         // L2 warm-up. The workgroups of one head together touch every 64-byte line of the
@@ -949,20 +1009,20 @@ __global__ __launch_bounds__(512) void kda_chunk_state(int T, int H, const char 
         touch(tB, PF - 1);
         state_publish<D, NW>(accS, sSF, sw, lane);
         for (int c = 0; c < nch; c += 2) {
+            __syncthreads();   // (1)
             load_state_ops<D>(opB, blk_of(c + 1), sw, lane);
             consume(tA);
             touch(tA, c + PF);
             __builtin_amdgcn_sched_barrier(0);
-            __syncthreads();   // (1)
             __syncthreads();   // (2) Vn published
             state_update<D, NW>(opA, accS, sVF, lane);
             state_publish<D, NW>(accS, sSF, sw, lane);   // row waves read sSF before (2)
             if (c + 1 >= nch) break;
+            __syncthreads();
             load_state_ops<D>(opA, blk_of(c + 2), sw, lane);
             consume(tB);
             touch(tB, c + 1 + PF);
             __builtin_amdgcn_sched_barrier(0);
-            __syncthreads();
             __syncthreads();
             state_update<D, NW>(opB, accS, sVF, lane);
             state_publish<D, NW>(accS, sSF, sw, lane);
