@@ -16,9 +16,12 @@
 // few-rows bf16 GEMM of kda_rows.hip (fp32 activations split into bf16 hi + lo in registers,
 // each weight read once for all B; q_a, kv_a and g in one pass over their concatenated
 // weights), so activations keep fp32 accuracy. The absorption (W_UK_h^T q) and the final
-// W_UV_h are bf16 GEMMs batched over heads on hi/lo row pairs (2B rows). The attention is two strided-batched fp32 GEMMs
-// (scores, then P . cache) around the reference's softmax (fp32 scores times
-// (nope+rope)^-0.5, max, expf, double sum).
+// W_UV_h are bf16 GEMMs batched over heads on hi/lo row pairs (2B rows). The attention reads
+// the cache once where the shape fits the fused kernel (kda_mla_attn.hip: split-bf16 MFMA
+// scores, online softmax with the reference's scale (nope+rope)^-0.5, split-bf16 weighted
+// sum of the latents; heads <= 64, kv_lora <= 512, kv_lora + rope <= 576); other shapes take
+// two strided-batched fp32 GEMMs (scores, then P . cache) around the reference's softmax
+// (fp32 scores times (nope+rope)^-0.5, max, expf, double sum).
 #include <math.h>
 #include <stdlib.h>
 
@@ -285,15 +288,20 @@ extern "C" int k3hip_mla_decode(const k3hip_mla_weights *w, int B, int pos, int 
     const int HV = H * VH;
     if ((QL & 7) || (HV & 7))
         K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_mla_decode: q_lora=%d, heads*v_head=%d not multiples of 8", QL, HV);
+    // attention in one pass over the cache (kda_mla_attn.hip) where the shape fits it, else
+    // as two strided-batched fp32 GEMMs around the softmax
+    const bool fused = mla_attention_supported(H, KL, CW) && !((uintptr_t)cache & 15);
     // scratch: q_a kv_a g projections [B][ld1] | q_a normed | q | q hi/lo | absorb halves | qcat |
-    //          scores | chat | chat hi/lo | W_UV halves | o | split-K partials
+    //          scores or the fused attention's workspace | chat | chat hi/lo | W_UV halves | o |
+    //          split-K partials
     const int N1 = QL + CW + (w->gate ? HV : 0);
     const long ld1 = (N1 + 3) & ~3;
     const size_t wsf = std::max({gemm_rows_ws_floats(B, N1, E), gemm_rows_ws_floats(B, H * QH, QL),
                                  gemm_rows_ws_floats(B, E, HV)});
     size_t sizes[] = {(size_t)B * ld1 * 4, (size_t)B * QL * 4, (size_t)B * H * QH * 4,
                       (size_t)2 * B * H * QH * 2, (size_t)2 * B * H * CW * 4, (size_t)B * H * CW * 4,
-                      (size_t)B * H * Tn * 4, (size_t)B * H * KL * 4, (size_t)2 * B * H * KL * 2,
+                      fused ? mla_attention_ws_bytes(B, H, KL, Tn) : (size_t)B * H * Tn * 4,
+                      fused ? 0 : (size_t)B * H * KL * 4, (size_t)2 * B * H * KL * 2,
                       (size_t)2 * B * HV * 4, (size_t)B * HV * 4, wsf * 4};
     constexpr int NB = sizeof sizes / sizeof sizes[0];
     size_t off[NB], total = 0;
@@ -334,32 +342,39 @@ extern "C" int k3hip_mla_decode(const k3hip_mla_weights *w, int B, int pos, int 
     hipLaunchKernelGGL(mla_qcat_kernel, dim3(mla_grid((size_t)B * H * CW)), dim3(256), 0, st, A2, q, B, H,
                        QN, QR, KL, qcat);
     K3_LAUNCHED();
-    // scores S_b [H][Tn] = qcat_b [H][CW] . cache_b[0..Tn)^T, per sequence
-    GemmDesc gs;
-    gs.M = H; gs.N = Tn; gs.K = CW; gs.ab_dtype = K3HIP_F32; gs.c_dtype = K3HIP_F32; gs.b_trans = true;
-    gs.lda = CW; gs.ldb = CW; gs.ldc = Tn; gs.batch = B;
-    gs.sa = (long)H * CW; gs.sb = (long)cap * CW; gs.sc = (long)H * Tn;
-    gs.tune = false;   // a new length every step: take the heuristic's first choice
-    if ((rc = gemm(gs, qcat, cache, S, st))) return rc;
-    {
-        const float scale = 1.0f / sqrtf((float)QH);
-        if (Tn <= 256 * 8)
-            hipLaunchKernelGGL((mla_softmax_reg_kernel<8>), dim3(B * H), dim3(256), 0, st, S, Tn, Tn, scale);
-        else if (Tn <= 256 * 32)
-            hipLaunchKernelGGL((mla_softmax_reg_kernel<32>), dim3(B * H), dim3(256), 0, st, S, Tn, Tn, scale);
-        else
-            hipLaunchKernelGGL(mla_softmax_kernel, dim3(B * H), dim3(256), 0, st, S, Tn, Tn, scale);
-        K3_LAUNCHED();
+    if (fused) {
+        // chat as the bf16 hi/lo rows of the W_UV GEMM, straight from the attention
+        if ((rc = mla_attention(B, H, KL, CW, Tn, cap, 1.0f / sqrtf((float)QH), qcat, cache, ch2, S,
+                                mla_attention_ws_bytes(B, H, KL, Tn), st)))
+            return rc;
+    } else {
+        // scores S_b [H][Tn] = qcat_b [H][CW] . cache_b[0..Tn)^T, per sequence
+        GemmDesc gs;
+        gs.M = H; gs.N = Tn; gs.K = CW; gs.ab_dtype = K3HIP_F32; gs.c_dtype = K3HIP_F32; gs.b_trans = true;
+        gs.lda = CW; gs.ldb = CW; gs.ldc = Tn; gs.batch = B;
+        gs.sa = (long)H * CW; gs.sb = (long)cap * CW; gs.sc = (long)H * Tn;
+        gs.tune = false;   // a new length every step: take the heuristic's first choice
+        if ((rc = gemm(gs, qcat, cache, S, st))) return rc;
+        {
+            const float scale = 1.0f / sqrtf((float)QH);
+            if (Tn <= 256 * 8)
+                hipLaunchKernelGGL((mla_softmax_reg_kernel<8>), dim3(B * H), dim3(256), 0, st, S, Tn, Tn, scale);
+            else if (Tn <= 256 * 32)
+                hipLaunchKernelGGL((mla_softmax_reg_kernel<32>), dim3(B * H), dim3(256), 0, st, S, Tn, Tn, scale);
+            else
+                hipLaunchKernelGGL(mla_softmax_kernel, dim3(B * H), dim3(256), 0, st, S, Tn, Tn, scale);
+            K3_LAUNCHED();
+        }
+        // chat_b [H][KL] = P_b [H][Tn] . cache_b[0..Tn)[0..KL)
+        GemmDesc gp;
+        gp.M = H; gp.N = KL; gp.K = Tn; gp.ab_dtype = K3HIP_F32; gp.c_dtype = K3HIP_F32; gp.b_trans = false;
+        gp.lda = Tn; gp.ldb = CW; gp.ldc = KL; gp.batch = B;
+        gp.sa = (long)H * Tn; gp.sb = (long)cap * CW; gp.sc = (long)H * KL;
+        gp.tune = false;
+        if ((rc = gemm(gp, S, cache, chat, st))) return rc;
+        if ((rc = split_rows2(chat, ch2, B, H * KL, st))) return rc;
     }
-    // chat_b [H][KL] = P_b [H][Tn] . cache_b[0..Tn)[0..KL)
-    GemmDesc gp;
-    gp.M = H; gp.N = KL; gp.K = Tn; gp.ab_dtype = K3HIP_F32; gp.c_dtype = K3HIP_F32; gp.b_trans = false;
-    gp.lda = Tn; gp.ldb = CW; gp.ldc = KL; gp.batch = B;
-    gp.sa = (long)H * Tn; gp.sb = (long)cap * CW; gp.sc = (long)H * KL;
-    gp.tune = false;
-    if ((rc = gemm(gp, S, cache, chat, st))) return rc;
     // W_UV: per head h, [chat hi; lo] (2B x KL) . W_UV_h^T (KL x VH), batched over heads; gate
-    if ((rc = split_rows2(chat, ch2, B, H * KL, st))) return rc;
     GemmDesc gu;
     gu.M = 2 * B; gu.N = VH; gu.K = KL; gu.ab_dtype = K3HIP_BF16; gu.c_dtype = K3HIP_F32; gu.b_trans = true;
     gu.lda = (long)H * KL; gu.ldb = KL; gu.ldc = HV; gu.batch = H;

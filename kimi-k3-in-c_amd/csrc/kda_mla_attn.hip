@@ -1,0 +1,400 @@
+// SPDX-License-Identifier: Apache-2.0
+// kda_mla_attn.hip - the attention of the absorbed MLA decode step in one pass over the
+// compressed-latent cache, for gfx950.
+//
+// For sequence b and head h, with qcat_h = [W_UK_h^T q_nope_h, q_rope_h] and the cache rows
+// cache_t = [latent_t, rope_t] (t < Tn):
+//   p_t = softmax_t(scale * qcat_h . cache_t),   chat_h = sum_t p_t latent_t
+// which is the reference's k3_mla_cached attention (src/core/k3_ops.c:321-424: fp32 scores
+// times (nope+rope)^-0.5, max, exponentials, normalised weights, weighted sum of values) with
+// kv_b absorbed. The cache (302 MB at 16 sequences x 8192 positions x 576 floats) dominates
+// the bytes, so the kernel reads it exactly once, and everything else stays on the chip:
+//
+//  * A workgroup owns one sequence and a contiguous range of positions (~CUs/B ranges per
+//    sequence) and walks it in tiles of 16 positions (16 contiguous cache rows). A tile is
+//    loaded two tiles ahead into registers with 16-byte loads, split into bf16 hi/lo and
+//    staged row-major in LDS (double-buffered, one barrier per tile).
+//  * Four waves, one per SIMD; wave w owns heads 16w..16w+15 and lane l always works for
+//    head 16w + (l & 15), so a head's softmax state and its weighted sums sit in the same
+//    lanes and nothing is exchanged between waves:
+//      scores^T (positions x heads) = cache tile (16 x CW) . qcat^T on split-bf16 MFMA
+//        (16x16x32, cache rows read from LDS, q fragments held in registers for the whole
+//        range); lane l ends with the scores of its head at 4 of the tile's positions;
+//      online softmax in base 2: running max M (exchanged between the 4 lanes of a head),
+//        per-lane partial sums, the weighted sums rescaled by 2^(M_old - M_new) only when
+//        some max of the wave grew;
+//      chat^T (latent channels x heads) += latent tile^T . P on split-bf16 MFMA (16x16x16):
+//        the transposed latent fragments come straight from the row-major tile through
+//        ds_read_b64_tr_b16, and P is the score product's output without leaving the lanes.
+//  * Each workgroup writes its unnormalised sums with (M, l); a second kernel merges the
+//    ranges of a sequence (weights 2^(M_s - M*)) in range order, divides by the merged sum and
+//    writes chat directly as the bf16 hi/lo rows of the W_UV GEMM.
+#include <math.h>
+
+#include <algorithm>
+
+#include "kda_internal.h"
+
+namespace k3kda {
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef s16x4 __attribute__((address_space(3))) *lds_s16x4_ptr;
+
+constexpr int AT_T = 16;             // positions per tile
+constexpr int AT_NT = 512;           // threads per workgroup: 8 waves, two per SIMD
+constexpr int AT_MAXKS = 18;         // 32-channel K-steps of the scores (kv_lora + rope <= 576)
+constexpr int AT_KSW = AT_MAXKS / 2; // K-steps per wave
+constexpr int AT_MAXCT = 32;         // 16-channel tiles of the latent (kv_lora <= 512)
+constexpr int AT_CTW = AT_MAXCT / 2; // latent channel tiles per wave
+constexpr int AT_MAXU = 5;           // 16-byte cache loads per thread per tile (kv_lora + rope <= 576)
+constexpr int AT_MAXSPLIT = 64;      // position ranges per sequence
+constexpr float AT_LOG2E = 1.4426950408889634f;
+
+// LDS: 2 buffers x {hi, lo} x [AT_T][AT_PR] bf16. Rows hold the 576 channels of the largest
+// shape (smaller shapes are zero past their kv_lora + rope, so every shape runs the same
+// products). The row pitch in dwords is 4 (4 AT_MAXKS + 1): the 16 rows of one 16-byte
+// fragment read start in 16 different 4-bank groups.
+constexpr int AT_PR = 32 * AT_MAXKS + 8;
+constexpr size_t AT_PLANE = (size_t)AT_T * AT_PR;   // bf16
+constexpr size_t AT_LDS = 4 * AT_PLANE * 2 + 8 * 64 * 16;   // bytes: tiles, partial scores
+
+struct AtGeom {
+    int H, CW, KL;
+};
+
+__device__ __forceinline__ void split2(float a, float b, bf16x2 &hi, bf16x2 &lo)
+{
+    hi = __builtin_convertvector(f2{a, b}, bf16x2);
+    const uint32_t u = __builtin_bit_cast(uint32_t, hi);
+    lo = __builtin_convertvector(f2{a - __uint_as_float(u << 16), b - __uint_as_float(u & 0xffff0000u)}, bf16x2);
+}
+
+// acc + ah.bh + ah.bl + al.bh, 16x16x32 bf16 MFMA (A rows x K, B K x columns)
+__device__ __forceinline__ f32x4 mma3_32(f32x4 acc, const bf16x8 &ah, const bf16x8 &al, const bf16x8 &bh,
+                                         const bf16x8 &bl)
+{
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
+}
+
+// the same on 16x16x16 bf16 MFMA (4 K values per lane)
+__device__ __forceinline__ f32x4 mma3_16(f32x4 acc, const s16x4 &ah, const s16x4 &al, const s16x4 &bh,
+                                         const s16x4 &bl)
+{
+    acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(al, bh, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bl, acc, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bh, acc, 0, 0, 0);
+}
+
+// Workgroup (sp, b): positions [Tn sp / nsplit, Tn (sp + 1) / nsplit) of sequence b.
+// Wave w: head tile ht = w % 4 (heads 16 ht .. 16 ht + 15), half hf = w / 4. Lane l works for
+// head h = 16 ht + (l & 15); kg = l >> 4 picks its K slice in the score product and its 4
+// positions of each tile (4 kg .. 4 kg + 3) in the softmax. The two waves of a head tile
+// split the score product's channels (K-steps 9 hf .. 9 hf + 8) and the weighted sum's latent
+// channels (256 hf .. 256 hf + 255); they add their partial scores in the same order through
+// LDS, so both run the identical softmax.
+// FULL: kv_lora + rope = 576, every staging unit of a row exists.
+template <bool FULL>
+__global__ __launch_bounds__(AT_NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void mla_attn_kernel(
+    AtGeom g, int Tn, int cap, int nsplit, float scale2, const float *__restrict__ qcat,
+    const float *__restrict__ cache, float *__restrict__ pctx, float *__restrict__ pm, float *__restrict__ pl)
+{
+    extern __shared__ __attribute__((aligned(16))) uint16_t at_smem[];
+    f32x4 *sS = reinterpret_cast<f32x4 *>(at_smem + 4 * AT_PLANE);   // partial scores [2][4][64]
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int m = lane & 15, kg = lane >> 4, ht = w & 3, hf = w >> 2;
+    const int sp = blockIdx.x, b = blockIdx.y;
+    const int p0 = (int)((long)Tn * sp / nsplit), p1 = (int)((long)Tn * (sp + 1) / nsplit);
+    const int ntile = (p1 - p0 + AT_T - 1) / AT_T;
+    const int H = g.H, CW = FULL ? 32 * AT_MAXKS : g.CW, KL = g.KL;
+    const int h = 16 * ht + m;
+    const bool act = 16 * ht < H;   // wave-uniform: this wave has heads
+
+    // q B-fragments of this wave's K-steps (K = channels 32 ks + 8 kg .. +7, column = head h),
+    // hi/lo, zero past CW and for heads past H
+    bf16x8 qh[AT_KSW], ql[AT_KSW];
+#pragma unroll
+    for (int i = 0; i < AT_KSW; i++) {
+        float x[8];
+        const int c = 32 * (AT_KSW * hf + i) + 8 * kg;
+        const bool ok = h < H;
+        const float *src = qcat + ((size_t)b * H + (ok ? h : 0)) * CW;
+#pragma unroll
+        for (int e = 0; e < 8; e += 4) {
+            const f4 v = ok && c + e < CW ? *reinterpret_cast<const f4 *>(src + c + e) : f4{0.0f, 0.0f, 0.0f, 0.0f};
+            x[e] = v.x; x[e + 1] = v.y; x[e + 2] = v.z; x[e + 3] = v.w;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            bf16x2 hh, ll;
+            split2(x[e], x[e + 1], hh, ll);
+            qh[i][e] = hh[0]; qh[i][e + 1] = hh[1];
+            ql[i][e] = ll[0]; ql[i][e + 1] = ll[1];
+        }
+    }
+    // channels CW .. 575 of every staged row stay zero (both buffers, hi and lo)
+    if (!FULL) {
+        const int padw = 32 * AT_MAXKS - CW;
+        for (int i = tid; i < 4 * AT_T * padw; i += AT_NT) {
+            const int pl4 = i / (AT_T * padw), r = (i / padw) % AT_T, c = CW + i % padw;
+            at_smem[pl4 * AT_PLANE + (size_t)r * AT_PR + c] = 0;
+        }
+    }
+
+    // staging: thread (r = tid / 32, q = tid % 32) owns row r of a tile and its 16-byte units
+    // q + 32 k (floats 4 q + 128 k .. +3), so 32 threads read 512 contiguous bytes
+    const int sr = tid >> 5, sq = 4 * (tid & 31);
+    f4 R[AT_MAXU];
+#pragma unroll
+    for (int k = 0; k < AT_MAXU; k++) R[k] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    auto load_tile = [&](int tile) {
+        const int tl = min(tile, ntile - 1);
+        const int pos = min(p0 + AT_T * tl + sr, p1 - 1);   // past the range: a valid row, masked later
+        const float *row = cache + ((size_t)b * cap + pos) * CW + sq;
+#pragma unroll
+        for (int k = 0; k < AT_MAXU; k++)
+            if ((FULL && k < AT_MAXU - 1) || sq + 128 * k < CW) R[k] = *reinterpret_cast<const f4 *>(row + 128 * k);
+    };
+    auto stage = [&](int buf) {
+        uint16_t *hi = at_smem + (size_t)(2 * buf) * AT_PLANE + sr * AT_PR + sq, *lo = hi + AT_PLANE;
+#pragma unroll
+        for (int k = 0; k < AT_MAXU; k++)
+            if ((FULL && k < AT_MAXU - 1) || sq + 128 * k < CW) {
+                bf16x2 h0, l0, h1, l1;
+                split2(R[k].x, R[k].y, h0, l0);
+                split2(R[k].z, R[k].w, h1, l1);
+                *reinterpret_cast<uint2 *>(hi + 128 * k) = uint2{__builtin_bit_cast(uint32_t, h0), __builtin_bit_cast(uint32_t, h1)};
+                *reinterpret_cast<uint2 *>(lo + 128 * k) = uint2{__builtin_bit_cast(uint32_t, l0), __builtin_bit_cast(uint32_t, l1)};
+            }
+    };
+
+    f32x4 acc[AT_CTW];
+#pragma unroll
+    for (int j = 0; j < AT_CTW; j++) acc[j] = 0.0f;
+    float M = -INFINITY, lsum = 0.0f;
+
+    // scores^T partial over this wave's K-steps: D[position 4 kg + e][head m]
+    auto scores = [&](int buf) {
+        const uint16_t *hi = at_smem + (size_t)(2 * buf) * AT_PLANE + m * AT_PR + 32 * AT_KSW * hf + 8 * kg;
+        const uint16_t *lo = hi + AT_PLANE;
+        f32x4 s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < AT_KSW; i++) {
+            const bf16x8 ah = *reinterpret_cast<const bf16x8 *>(hi + 32 * i);
+            const bf16x8 al = *reinterpret_cast<const bf16x8 *>(lo + 32 * i);
+            if (i & 1) s1 = mma3_32(s1, ah, al, qh[i], ql[i]);
+            else s0 = mma3_32(s0, ah, al, qh[i], ql[i]);
+        }
+        return s0 + s1;
+    };
+    // online softmax of the tile's scores s (this lane: head h, positions p0 + 16 it + 4 kg + e)
+    // and the weighted sum over this wave's latent channel tiles
+    auto update = [&](int buf, int it, f32x4 s) {
+        const uint16_t *hi = at_smem + (size_t)(2 * buf) * AT_PLANE, *lo = hi + AT_PLANE;
+        const int t0 = p0 + AT_T * it + 4 * kg;
+        float x[4], mt = -INFINITY;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            x[e] = t0 + e < p1 ? s[e] * scale2 : -INFINITY;
+            mt = fmaxf(mt, x[e]);
+        }
+        mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+        const float mn = fmaxf(M, mt);
+        const float alpha = __builtin_amdgcn_exp2f(M - mn);   // 0 on the first tile (M = -inf)
+        float p[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) p[e] = __builtin_amdgcn_exp2f(x[e] - mn);   // 0 where masked
+        lsum = lsum * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+        M = mn;
+        if (__ballot(alpha != 1.0f)) {   // some max of the wave grew
+#pragma unroll
+            for (int j = 0; j < AT_CTW; j++) acc[j] *= alpha;
+        }
+        // P as the B operand (K = positions 4 kg .. +3, column = head m), hi/lo
+        bf16x2 h01, l01, h23, l23;
+        split2(p[0], p[1], h01, l01);
+        split2(p[2], p[3], h23, l23);
+        const s16x4 ph = __builtin_bit_cast(s16x4, uint2{__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23)});
+        const s16x4 pq = __builtin_bit_cast(s16x4, uint2{__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23)});
+        // chat^T[channel 16 j + 4 kg + e][head m] += latent^T . P over channel tiles
+        // AT_CTW hf .. +AT_CTW-1; this lane's transposed-read source: position
+        // 4 kg + ((lane >> 2) & 3), channels 16 j + 4 (lane & 3) .. +3
+        const int to = (4 * kg + ((lane >> 2) & 3)) * AT_PR + 4 * (lane & 3) + 16 * AT_CTW * hf;
+#pragma unroll
+        for (int j = 0; j < AT_CTW; j++) {
+            const s16x4 ah = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(hi + to + 16 * j));
+            const s16x4 al = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(lo + to + 16 * j));
+            acc[j] = mma3_16(acc[j], ah, al, ph, pq);
+        }
+    };
+
+    load_tile(0);
+    stage(0);
+    load_tile(1);
+    __syncthreads();
+    // iteration it: scores of tile it (buffer it & 1); the partial scores meet in LDS; tile
+    // it + 1 (loaded one iteration earlier) is staged into the other buffer and the registers
+    // refilled with tile it + 2; the softmax and weighted sum of tile it
+    for (int it = 0; it < ntile; it++) {
+        const int buf = it & 1;
+        f32x4 s = 0.0f;
+        if (act) {
+            s = scores(buf);
+            sS[(hf * 4 + ht) * 64 + lane] = s;
+        }
+        if (it + 1 < ntile) stage(buf ^ 1);
+        __syncthreads();
+        if (it + 2 < ntile) load_tile(it + 2);
+        if (act) update(buf, it, sS[ht * 64 + lane] + sS[(4 + ht) * 64 + lane]);
+        __syncthreads();
+    }
+
+    // unnormalised sums of this wave's channels and (M, l) of this range for head h
+    lsum += __shfl_xor(lsum, 16, 64);
+    lsum += __shfl_xor(lsum, 32, 64);
+    if (act && h < H) {
+        float *outp = pctx + (((size_t)b * nsplit + sp) * H + h) * KL + 16 * AT_CTW * hf + 4 * kg;
+#pragma unroll
+        for (int j = 0; j < AT_CTW; j++)
+            if (16 * (AT_CTW * hf + j) < KL) *reinterpret_cast<f4 *>(outp + 16 * j) = f4{acc[j][0], acc[j][1], acc[j][2], acc[j][3]};
+        if (kg == 0 && hf == 0) {
+            pm[((size_t)b * nsplit + sp) * H + h] = M;
+            pl[((size_t)b * nsplit + sp) * H + h] = lsum;
+        }
+    }
+}
+
+// Block (h, b): merge the nsplit ranges of sequence b, head h, in range order; write
+// chat = sum / l as bf16 hi (row b) and lo (row B + b) of ch2 [2B][H KL]. Thread i covers
+// channels 4i .. 4i + 3 (and every 4 * blockDim further).
+__global__ __launch_bounds__(128) void mla_attn_merge_kernel(int B, int H, int KL, int nsplit,
+                                                             const float *__restrict__ pctx,
+                                                             const float *__restrict__ pm,
+                                                             const float *__restrict__ pl,
+                                                             uint16_t *__restrict__ ch2)
+{
+    __shared__ float sw[AT_MAXSPLIT];
+    __shared__ float sl;
+    const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+    const float *mrow = pm + (size_t)b * nsplit * H + h, *lrow = pl + (size_t)b * nsplit * H + h;
+    if (tid < 64) {
+        float mx = -INFINITY;
+        for (int s = 0; s < nsplit; s++) mx = fmaxf(mx, mrow[(size_t)s * H]);
+        const float wv = tid < nsplit ? __builtin_amdgcn_exp2f(mrow[(size_t)tid * H] - mx) : 0.0f;
+        if (tid < nsplit) sw[tid] = wv;
+        float lv = tid < nsplit ? wv * lrow[(size_t)tid * H] : 0.0f;
+        // the weighted sums of the ranges, added in a fixed tree into lane 0
+        for (int o = 1; o < 64; o <<= 1) {
+            const float t = __shfl_down(lv, o, 64);
+            if ((tid & (2 * o - 1)) == 0) lv += t;
+        }
+        if (tid == 0) sl = lv;
+    }
+    __syncthreads();
+    const float rl = 1.0f / sl;
+    const size_t BN = (size_t)B * H * KL;
+    for (int c = 4 * tid; c < KL; c += 4 * blockDim.x) {
+        f4 a = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int s = 0; s < nsplit; s++)
+            a += sw[s] * *reinterpret_cast<const f4 *>(pctx + (((size_t)b * nsplit + s) * H + h) * KL + c);
+        const size_t i = ((size_t)b * H + h) * KL + c;
+        const float v[4] = {a.x * rl, a.y * rl, a.z * rl, a.w * rl};
+        uint16_t hv[4], lv[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            hv[e] = f2bf(v[e]);
+            lv[e] = f2bf(v[e] - bf2f(hv[e]));
+        }
+        *reinterpret_cast<uint2 *>(ch2 + i) = uint2{hv[0] | ((uint32_t)hv[1] << 16), hv[2] | ((uint32_t)hv[3] << 16)};
+        *reinterpret_cast<uint2 *>(ch2 + BN + i) = uint2{lv[0] | ((uint32_t)lv[1] << 16), lv[2] | ((uint32_t)lv[3] << 16)};
+    }
+}
+
+int at_cus()
+{
+    static int n = 0;
+    if (!n) {
+        int dev = 0, c = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && c > 0)
+            n = c;
+        else
+            n = 256;
+    }
+    return n;
+}
+
+bool at_geom(int H, int KL, int CW, AtGeom &g)
+{
+    if (H <= 0 || H > 64 || KL <= 0 || (KL % 16) || KL > 16 * AT_MAXCT || CW < KL || (CW % 4) ||
+        CW > 32 * AT_MAXKS)
+        return false;
+    g.H = H;
+    g.CW = CW;
+    g.KL = KL;
+    return true;
+}
+
+int at_nsplit(int B, int Tn)
+{
+    return std::min({AT_MAXSPLIT, std::max(1, (at_cus() + B - 1) / B), std::max(1, Tn / AT_T)});
+}
+
+}  // namespace
+
+size_t mla_attention_ws_bytes(int B, int H, int KL, int Tn)
+{
+    const int nsplit = at_nsplit(B, Tn);
+    const size_t r = (size_t)B * nsplit * H;
+    return ((r * KL * 4 + 255) & ~(size_t)255) + 2 * ((r * 4 + 255) & ~(size_t)255);
+}
+
+bool mla_attention_supported(int H, int KL, int CW)
+{
+    AtGeom g;
+    return at_geom(H, KL, CW, g);
+}
+
+int mla_attention(int B, int H, int KL, int CW, int Tn, int cap, float scale, const float *qcat,
+                  const float *cache, uint16_t *ch2, void *ws, size_t ws_bytes, hipStream_t st)
+{
+    AtGeom g;
+    if (!at_geom(H, KL, CW, g))
+        K3_FAIL(K3HIP_EUNSUPPORTED, "mla attention: heads=%d kv_lora=%d kv_lora+rope=%d outside the fused kernel", H, KL, CW);
+    if (B <= 0 || Tn <= 0 || Tn > cap) K3_FAIL(K3HIP_EINVAL, "mla attention: B=%d Tn=%d cap=%d", B, Tn, cap);
+    const int nsplit = at_nsplit(B, Tn);
+    const size_t need = mla_attention_ws_bytes(B, H, KL, Tn);
+    if (!ws || ws_bytes < need || ((uintptr_t)ws & 255) || ((uintptr_t)cache & 15) || ((uintptr_t)qcat & 15))
+        K3_FAIL(K3HIP_EINVAL, "mla attention: workspace %zu < %zu bytes, or a misaligned buffer", ws_bytes, need);
+    const size_t r = (size_t)B * nsplit * H;
+    float *pctx = (float *)ws;
+    float *pm = (float *)((char *)ws + ((r * KL * 4 + 255) & ~(size_t)255));
+    float *pl = (float *)((char *)pm + ((r * 4 + 255) & ~(size_t)255));
+    static bool attr = false;
+    if (!attr) {
+        K3_HIP(hipFuncSetAttribute((const void *)mla_attn_kernel<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   (int)AT_LDS));
+        K3_HIP(hipFuncSetAttribute((const void *)mla_attn_kernel<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   (int)AT_LDS));
+        attr = true;
+    }
+    if (CW == 32 * AT_MAXKS)
+        hipLaunchKernelGGL(mla_attn_kernel<true>, dim3(nsplit, B), dim3(AT_NT), AT_LDS, st, g, Tn, cap, nsplit,
+                           scale * AT_LOG2E, qcat, cache, pctx, pm, pl);
+    else
+        hipLaunchKernelGGL(mla_attn_kernel<false>, dim3(nsplit, B), dim3(AT_NT), AT_LDS, st, g, Tn, cap, nsplit,
+                           scale * AT_LOG2E, qcat, cache, pctx, pm, pl);
+    K3_LAUNCHED();
+    hipLaunchKernelGGL(mla_attn_merge_kernel, dim3(H, B), dim3(128), 0, st, B, H, KL, nsplit, pctx, pm, pl, ch2);
+    K3_LAUNCHED();
+    return K3HIP_OK;
+}
+
+}  // namespace k3kda
