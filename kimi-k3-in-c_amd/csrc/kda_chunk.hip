@@ -121,6 +121,14 @@ __device__ __forceinline__ void lds8(float (&x)[8], const float *p)
     x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
 }
 
+// CPL (2 or 4) consecutive floats to an LDS address aligned to 4 CPL bytes, as one store.
+template <int CPL>
+__device__ __forceinline__ void store_cpl(float *p, const float (&v)[CPL])
+{
+    if constexpr (CPL == 4) *reinterpret_cast<f4 *>(p) = f4{v[0], v[1], v[2], v[3]};
+    else *reinterpret_cast<f2 *>(p) = f2{v[0], v[1]};
+}
+
 // Split x and store it as lane `lane` of the fragment block at `blk`.
 __device__ __forceinline__ void store_frag(char *blk, int lane, const float (&x)[8])
 {
@@ -218,6 +226,24 @@ __device__ __forceinline__ void p1_item(float *lds, const float (&vreg)[2][8], c
     //     in sT (both zeroed beforehand). The 10 blocks (a, b), b <= a, of 16x16 are dealt
     //     as jobs w and w + 8 to wave w: waves w and w + 4 share a SIMD, so the SIMDs take
     //     3, 3, 2 and 2 blocks.
+    // (6 early) (k e^(G_last - G))^T as A-fragments [D/16][2]: the SIMDs that take two of the
+    //      A blocks (waves 2, 3, 6, 7) take these as well
+    if (NCT * 2 == 16 && (w & 2)) {
+        const int kw = (w & 1) + ((w >> 2) << 1);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int fb = 4 * kw + q, rt = fb >> 1, ks = fb & 1;
+            const int i = SB * rt + m;
+            const float gl = sG[(CH - 1) * PD + i];
+            float x[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int s = 32 * ks + 8 * kg + e;
+                x[e] = sK[s * PD + i] * exp2_fast(gl - sG[s * PD + i]);
+            }
+            store_frag(blk + WL::KF + (size_t)fb * 2048, lane, x);
+        }
+    }
     for (int j = w; j < 10; j += NW) {
         const int a = j < 1 ? 0 : j < 3 ? 1 : j < 6 ? 2 : 3;
         const int b = j - a * (a + 1) / 2;
@@ -259,23 +285,13 @@ __device__ __forceinline__ void p1_item(float *lds, const float (&vreg)[2][8], c
     __syncthreads();
 
     hook(1);
-    // (3b) A_qk as A-fragments [rt 4][ks 2], one fragment lane per thread; q e^G (q scaled)
-    //      as A-fragments [rt 4][KSI] from the staged q.
+    // (3b) A_qk as A-fragments [rt 4][ks 2], one fragment lane per thread (q e^G follows
+    //      in the shadow of the diagonal inverses, (k e^(G_last - G))^T came with the A blocks).
     {
         const int fb = tid >> 6, rt = fb >> 1, ks = fb & 1;
         float x[8];
         lds8(x, &sT[(SB * rt + m) * PA + 32 * ks + 8 * kg]);
         store_frag(blk + WL::AF + (size_t)fb * 2048, lane, x);
-    }
-    for (int f = tid; f < 4 * KSI * 64; f += P1_THREADS) {
-        const int fb = f >> 6, rt = fb / KSI, ks = fb % KSI;
-        const int t = SB * rt + m, i0 = 32 * ks + 8 * kg;
-        float x[8], gx[8];
-        lds8(x, &sX[t * PD + i0]);
-        lds8(gx, &sG[t * PD + i0]);
-#pragma unroll
-        for (int e = 0; e < 8; e++) x[e] = x[e] * exp2_fast(gx[e]);
-        store_frag(blk + WL::QF + (size_t)fb * 2048, lane, x);
     }
     __syncthreads();
     for (int e = tid; e < CH * PA; e += P1_THREADS) sT[e] = 0.0f;
@@ -339,6 +355,18 @@ __device__ __forceinline__ void p1_item(float *lds, const float (&vreg)[2][8], c
 #pragma unroll
                 for (int e = 0; e < 4; e++) sT[(o + 4 * kg + e) * PA + o + m] = x[e];
             }
+        }
+    } else {
+        // meanwhile waves 4..7: q e^G (q scaled) as A-fragments [rt 4][KSI]
+        for (int fb = w - 4; fb < 4 * KSI; fb += 4) {
+            const int rt = fb / KSI, ks = fb % KSI;
+            const int t = SB * rt + m, i0 = 32 * ks + 8 * kg;
+            float x[8], gx[8];
+            lds8(x, &sX[t * PD + i0]);
+            lds8(gx, &sG[t * PD + i0]);
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[e] = x[e] * exp2_fast(gx[e]);
+            store_frag(blk + WL::QF + (size_t)fb * 2048, lane, x);
         }
     }
     __syncthreads();
@@ -429,18 +457,21 @@ __device__ __forceinline__ void p1_item(float *lds, const float (&vreg)[2][8], c
     }
 
     hook(6);
-    // (6) (k e^(G_last - G))^T as A-fragments [D/16][2]; e^G_last.
-    for (int f = tid; f < NCT * 2 * 64; f += P1_THREADS) {
-        const int fb = f >> 6, rt = fb >> 1, ks = fb & 1;
-        const int i = SB * rt + m;
-        const float gl = sG[(CH - 1) * PD + i];
-        float x[8];
+    // (6) (k e^(G_last - G))^T as A-fragments [D/16][2] where the A stage has not written them
+    //     (D = 64); e^G_last.
+    if (NCT * 2 != 16) {
+        for (int f = tid; f < NCT * 2 * 64; f += P1_THREADS) {
+            const int fb = f >> 6, rt = fb >> 1, ks = fb & 1;
+            const int i = SB * rt + m;
+            const float gl = sG[(CH - 1) * PD + i];
+            float x[8];
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const int s = 32 * ks + 8 * kg + e;
-            x[e] = sK[s * PD + i] * exp2_fast(gl - sG[s * PD + i]);
+            for (int e = 0; e < 8; e++) {
+                const int s = 32 * ks + 8 * kg + e;
+                x[e] = sK[s * PD + i] * exp2_fast(gl - sG[s * PD + i]);
+            }
+            store_frag(blk + WL::KF + (size_t)fb * 2048, lane, x);
         }
-        store_frag(blk + WL::KF + (size_t)fb * 2048, lane, x);
     }
     if (tid < D) reinterpret_cast<float *>(blk + WL::GL)[tid] = exp2_fast(sG[(CH - 1) * PD + tid]);
     __syncthreads();   // every LDS read of this item is done before the next one is staged
@@ -674,14 +705,20 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra_act(
             l2norm_half<CPL>(y[1][r]);
             const int t = r0 + r;
             const bool live = t < Tc;
+            float vg[CPL], vk[CPL], vx[CPL], vv[CPL];
 #pragma unroll
             for (int e = 0; e < CPL; e++) {
-                const int i = t * PD + c0 + e;
-                sG[i] = live ? gate_bounded(lb, a, zr[r][e], sDT[c0 + e]) : 0.0f;
-                sK[i] = live ? y[1][r][e] : 0.0f;
-                sX[i] = live ? y[0][r][e] * qs : 0.0f;
-                sV[i] = live ? y[2][r][e] : 0.0f;
+                vg[e] = live ? gate_bounded(lb, a, zr[r][e], sDT[c0 + e]) : 0.0f;
+                vk[e] = live ? y[1][r][e] : 0.0f;
+                vx[e] = live ? y[0][r][e] * qs : 0.0f;
+                vv[e] = live ? y[2][r][e] : 0.0f;
             }
+            // one 8- or 16-byte store per row and tensor (c0 and the pitch are multiples of CPL)
+            const int i = t * PD + c0;
+            store_cpl<CPL>(sG + i, vg);
+            store_cpl<CPL>(sK + i, vk);
+            store_cpl<CPL>(sX + i, vx);
+            store_cpl<CPL>(sV + i, vv);
         }
         if (tid < CH) sB[tid] = tid < Tc ? fast_sigmoid(pbl) : 0.0f;
         __syncthreads();
