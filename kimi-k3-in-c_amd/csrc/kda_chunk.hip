@@ -638,7 +638,7 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra_act(
         for (int part = 0; part < 5; part++) fetch(lo, part);
 
     int head = -1;
-    float a = 0.0f;
+    float a2 = 0.0f;
     for (int item = lo; item < hi; item++) {
         const int h = item / nch, c = item % nch;
         const int t0 = c * CH, Tc = min(CH, T - t0);
@@ -655,7 +655,7 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra_act(
                 sW[i] = j < K ? convw[b][((size_t)h * D + ch) * K + j] : 0.0f;
             }
             for (int i = tid; i < D; i += P1_THREADS) sDT[i] = dt_bias[(size_t)h * D + i];
-            a = expf(A_log[h]);
+            a2 = gate_a2(expf(A_log[h]));
             head = h;
             __syncthreads();
         }
@@ -708,7 +708,7 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra_act(
             float vg[CPL], vk[CPL], vx[CPL], vv[CPL];
 #pragma unroll
             for (int e = 0; e < CPL; e++) {
-                vg[e] = live ? gate_bounded(lb, a, zr[r][e], sDT[c0 + e]) : 0.0f;
+                vg[e] = live ? gate_bounded(lb, a2, zr[r][e], sDT[c0 + e]) : 0.0f;
                 vk[e] = live ? y[1][r][e] : 0.0f;
                 vx[e] = live ? y[0][r][e] * qs : 0.0f;
                 vv[e] = live ? y[2][r][e] : 0.0f;

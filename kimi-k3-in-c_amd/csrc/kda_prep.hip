@@ -211,7 +211,7 @@ __global__ __launch_bounds__(256) void kda_prep2_kernel(
             RowIO<CPL, K3HIP_F32>::load(zz, z, row + c0);
 #pragma unroll
             for (int e = 0; e < CPL; e++) {
-                if (lb != 0.0f) gv[e] = gate_bounded(lb, a, zz[e], dtb[e]);
+                if (lb != 0.0f) gv[e] = gate_bounded(lb, gate_a2(a), zz[e], dtb[e]);
                 else gv[e] = -a * softplus_ref(zz[e] + dtb[e]);   // no lower bound: softplus gate
                 av[e] = fast_exp(gv[e]);
             }

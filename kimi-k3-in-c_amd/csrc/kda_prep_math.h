@@ -17,14 +17,14 @@ __device__ __forceinline__ float fast_sigmoid(float x) { return __builtin_amdgcn
 
 // One conv output: taps w[0..K-1] over x_{t-K+1} .. x_t, where win[0..K-2] are the K-1
 // older inputs (oldest first) and cur = x_t. acc = w[K-1] x_t, then += w[j] win[j] in
-// order of j with separate roundings; the result is acc * sigmoid(acc).
+// order of j as fused multiply-adds (the reference rounds product and sum separately: a
+// difference of at most an ulp of the partial sum per tap); the result is acc * sigmoid(acc).
 template <int K>
 __device__ __forceinline__ float conv_silu(const float (&w)[K], const float *win, float cur)
 {
-#pragma clang fp contract(off)
     float acc = w[K - 1] * cur;
 #pragma unroll
-    for (int j = 0; j < K - 1; j++) acc = acc + w[j] * win[j];
+    for (int j = 0; j < K - 1; j++) acc = __builtin_fmaf(w[j], win[j], acc);
     return acc * fast_sigmoid(acc);
 }
 
@@ -64,11 +64,13 @@ __device__ __forceinline__ void l2norm_half(float (&y)[CPL])
     for (int e = 0; e < CPL; e++) y[e] = y[e] * r;
 }
 
-// Bounded decay gate g = lb * sigmoid(a (z + dt_bias)), a = expf(A_log[h]).
-__device__ __forceinline__ float gate_bounded(float lb, float a, float z, float dtb)
+// Bounded decay gate g = lb * sigmoid(a (z + dt_bias)), a = expf(A_log[h]), from
+// a2 = gate_a2(a) = -a log2(e): lb / (1 + 2^((z + dt_bias) a2)).
+__device__ __forceinline__ float gate_a2(float a) { return a * -1.4426950408889634f; }
+__device__ __forceinline__ float gate_bounded(float lb, float a2, float z, float dtb)
 {
 #pragma clang fp contract(off)
-    return lb * fast_sigmoid(a * (z + dtb));
+    return lb * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f((z + dtb) * a2));
 }
 
 // Row access for CPL = 2 / 4 adjacent channels of fp32 or bf16 activations.

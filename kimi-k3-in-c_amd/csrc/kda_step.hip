@@ -95,7 +95,7 @@ __global__ __launch_bounds__(4 * D) void kda_layer_step_kernel(
             for (int e = 0; e < CPL; e++) {
                 const size_t ch = c0 + e;
                 const float z = Cz[(size_t)b * P + ch];
-                const float g = lb != 0.0f ? gate_bounded(lb, a, z, dt_bias[ch])
+                const float g = lb != 0.0f ? gate_bounded(lb, gate_a2(a), z, dt_bias[ch])
                                            : -a * softplus_ref(z + dt_bias[ch]);   // softplus gate
                 s_a[cl + e] = fast_exp(g);
             }
