@@ -223,16 +223,17 @@ __device__ __forceinline__ void p1_item(float *lds, const float (&vreg)[2][8], c
 
     hook(0);
     // (3) A_kk (times beta_t, strictly lower) into sA; A_qk (lower with the diagonal) staged
-    //     in sT (both zeroed beforehand). The 10 blocks (a, b), b <= a, of 16x16 are dealt
-    //     as jobs w and w + 8 to wave w: waves w and w + 4 share a SIMD, so the SIMDs take
-    //     3, 3, 2 and 2 blocks.
-    // (6 early) (k e^(G_last - G))^T as A-fragments [D/16][2]: the SIMDs that take two of the
-    //      A blocks (waves 2, 3, 6, 7) take these as well
-    if (NCT * 2 == 16 && (w & 2)) {
-        const int kw = (w & 1) + ((w >> 2) << 1);
+    //     in sT (both zeroed beforehand), in 16x16 blocks (a, b), b <= a. A wave takes one
+    //     row block a and up to two column blocks, so the row operands (k and q times
+    //     e^(G_t - G_p)) are built once for both: waves 0-3 take (3; 0,1), (3; 2,3), (2; 0,1),
+    //     (1; 0,1), waves 6 and 7 (2; 2) and (0; 0). Waves 4 and 5 meanwhile build
+    //     (k e^(G_last - G))^T as A-fragments [D/16][2], half each. Waves w and w + 4 share a
+    //     SIMD, so each SIMD has one two-block wave and one lighter wave.
+    if (w == 4 || w == 5) {
+        constexpr int NKF = NCT * 2 / 2;   // fragments per wave
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const int fb = 4 * kw + q, rt = fb >> 1, ks = fb & 1;
+        for (int q = 0; q < NKF; q++) {
+            const int fb = NKF * (w - 4) + q, rt = fb >> 1, ks = fb & 1;
             const int i = SB * rt + m;
             const float gl = sG[(CH - 1) * PD + i];
             float x[8];
@@ -243,43 +244,55 @@ __device__ __forceinline__ void p1_item(float *lds, const float (&vreg)[2][8], c
             }
             store_frag(blk + WL::KF + (size_t)fb * 2048, lane, x);
         }
-    }
-    for (int j = w; j < 10; j += NW) {
-        const int a = j < 1 ? 0 : j < 3 ? 1 : j < 6 ? 2 : 3;
-        const int b = j - a * (a + 1) / 2;
+    } else {
+        // wave -> (row block a, first column block b0, column blocks nb)
+        const int a = w == 0 || w == 1 ? 3 : w == 2 || w == 6 ? 2 : w == 3 ? 1 : 0;
+        const int b0 = w == 1 ? 2 : w == 6 ? 2 : 0;
+        const int nb = w >= 6 ? 1 : 2;
         const int p = SB * a + 8;    // pivot row: the middle of row block a
         const int t = SB * a + m;    // A-operand row (token t)
-        const int s = SB * b + m;    // B-operand row (token s)
-        f32x4 akk = 0.0f, aqk = 0.0f;
+        f32x4 akk[2] = {0.0f, 0.0f}, aqk[2] = {0.0f, 0.0f};
 #pragma unroll
         for (int ks = 0; ks < KSI; ks++) {
             const int i0 = 32 * ks + 8 * kg;
-            float lk[8], lq[8], r[8], gp[8], gt[8], gs[8];
+            float lk[8], lq[8], gp[8], gt[8];
             lds8(gp, &sG[p * PD + i0]);
             lds8(gt, &sG[t * PD + i0]);
-            lds8(gs, &sG[s * PD + i0]);
             lds8(lk, &sK[t * PD + i0]);
             lds8(lq, &sX[t * PD + i0]);
-            lds8(r, &sK[s * PD + i0]);
 #pragma unroll
             for (int e = 0; e < 8; e++) {
                 const float ft = exp2_fast(gt[e] - gp[e]);
                 lk[e] = lk[e] * ft;
                 lq[e] = lq[e] * ft;
-                r[e] = r[e] * exp2_fast(gp[e] - gs[e]);
             }
-            bf16x8 kh, kl, qh, ql, rh, rl;
+            bf16x8 kh, kl, qh, ql;
             split8(lk, kh, kl);
             split8(lq, qh, ql);
-            split8(r, rh, rl);
-            akk = mma3(akk, kh, kl, rh, rl);
-            aqk = mma3(aqk, qh, ql, rh, rl);
+#pragma unroll
+            for (int jb = 0; jb < 2; jb++) {
+                if (jb >= nb) break;
+                const int s = SB * (b0 + jb) + m;   // B-operand row (token s)
+                float r[8], gs[8];
+                lds8(gs, &sG[s * PD + i0]);
+                lds8(r, &sK[s * PD + i0]);
+#pragma unroll
+                for (int e = 0; e < 8; e++) r[e] = r[e] * exp2_fast(gp[e] - gs[e]);
+                bf16x8 rh, rl;
+                split8(r, rh, rl);
+                akk[jb] = mma3(akk[jb], kh, kl, rh, rl);
+                aqk[jb] = mma3(aqk[jb], qh, ql, rh, rl);
+            }
         }
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int tt = SB * a + 4 * kg + e, ss = SB * b + m;
-            sA[tt * PA + ss] = ss < tt ? akk[e] * sB[tt] : 0.0f;
-            sT[tt * PA + ss] = ss <= tt ? aqk[e] : 0.0f;
+        for (int jb = 0; jb < 2; jb++) {
+            if (jb >= nb) break;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int tt = SB * a + 4 * kg + e, ss = SB * (b0 + jb) + m;
+                sA[tt * PA + ss] = ss < tt ? akk[jb][e] * sB[tt] : 0.0f;
+                sT[tt * PA + ss] = ss <= tt ? aqk[jb][e] : 0.0f;
+            }
         }
     }
     __syncthreads();
@@ -457,22 +470,7 @@ __device__ __forceinline__ void p1_item(float *lds, const float (&vreg)[2][8], c
     }
 
     hook(6);
-    // (6) (k e^(G_last - G))^T as A-fragments [D/16][2] where the A stage has not written them
-    //     (D = 64); e^G_last.
-    if (NCT * 2 != 16) {
-        for (int f = tid; f < NCT * 2 * 64; f += P1_THREADS) {
-            const int fb = f >> 6, rt = fb >> 1, ks = fb & 1;
-            const int i = SB * rt + m;
-            const float gl = sG[(CH - 1) * PD + i];
-            float x[8];
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const int s = 32 * ks + 8 * kg + e;
-                x[e] = sK[s * PD + i] * exp2_fast(gl - sG[s * PD + i]);
-            }
-            store_frag(blk + WL::KF + (size_t)fb * 2048, lane, x);
-        }
-    }
+    // (6) e^G_last.
     if (tid < D) reinterpret_cast<float *>(blk + WL::GL)[tid] = exp2_fast(sG[(CH - 1) * PD + tid]);
     __syncthreads();   // every LDS read of this item is done before the next one is staged
 }
