@@ -174,8 +174,23 @@ __device__ __forceinline__ char *blk_addr(char *ws, int c, int H, int h)
     return ws + ((size_t)c * H + h) * Ws<D>::SIZE;
 }
 
+// Zero the six 16x16 blocks of Tm's staging area sT ([64][PA]) above the diagonal: the A_qk
+// fragments and the W/U products read them, and no stage writes them.
+template <int D>
+__device__ __forceinline__ void zero_upper(float *sT, int tid)
+{
+    constexpr int PA = P1Lds<D>::PA;
+#pragma unroll
+    for (int j = 0; j < 6 * 256 / P1_THREADS; j++) {
+        const int i = tid + P1_THREADS * j, q = i >> 8;
+        const int a = q < 3 ? 0 : q < 5 ? 1 : 2, b = q < 3 ? q + 1 : q < 5 ? q - 1 : 3;
+        sT[(SB * a + ((i >> 4) & 15)) * PA + SB * b + (i & 15)] = 0.0f;
+    }
+}
+
 // Everything of one (chunk, head) item after its inputs are staged: g in sG, k in sK,
-// q * q_scale in sX (rows past the end of the sequence zero), beta in sB, sA zero, and this
+// q * q_scale in sX (rows past the end of the sequence zero), beta in sB, the blocks of sT
+// above its diagonal zero (zero_upper; nothing else of sA or sT is read before written), and this
 // wave's column tile of v in vreg. Writes the item's workspace block. Every LDS read of the
 // item is complete when it returns.
 // hook(0) .. hook(6) are called between the stages; the fused kernel issues its prefetch of
@@ -306,9 +321,7 @@ __device__ __forceinline__ void p1_item(float *lds, const float (&vreg)[2][8], c
         lds8(x, &sT[(SB * rt + m) * PA + 32 * ks + 8 * kg]);
         store_frag(blk + WL::AF + (size_t)fb * 2048, lane, x);
     }
-    __syncthreads();
-    for (int e = tid; e < CH * PA; e += P1_THREADS) sT[e] = 0.0f;
-    __syncthreads();
+    __syncthreads();   // the inverse below overwrites every block of sT at or below the diagonal
 
     hook(2);
     // (4a) diagonal blocks of Tm = (I + A)^-1. A 16x16 strictly lower block N is nilpotent
@@ -491,7 +504,7 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra(int T, int H, floa
 {
     using L = P1Lds<D>;
     using WL = Ws<D>;
-    constexpr int PD = L::PD, PA = L::PA, NCT = WL::NCT;
+    constexpr int PD = L::PD, NCT = WL::NCT;
     extern __shared__ __attribute__((aligned(16))) float lds[];
     float *sG = lds + L::G, *sK = lds + L::K, *sX = lds + L::X, *sA = lds + L::A, *sB = lds + L::B;
 
@@ -546,7 +559,7 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra(int T, int H, floa
             *reinterpret_cast<f4 *>(&sK[t * PD + i4]) = live ? pk[j] : f4(0.0f);
             *reinterpret_cast<f4 *>(&sX[t * PD + i4]) = live ? pq[j] * qs : f4(0.0f);
         }
-        for (int e = tid; e < 2 * CH * PA; e += P1_THREADS) sA[e] = 0.0f;   // A and Tm
+        zero_upper<D>(sA + CH * L::PA, tid);
         if (tid < CH) sB[tid] = tid < Tc ? pb : 0.0f;
         __syncthreads();
         fetch(min(item + (int)gridDim.x, nitems - 1));
@@ -582,7 +595,7 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra_act(
 {
     using L = P1Lds<D>;
     using WL = Ws<D>;
-    constexpr int PD = L::PD, PA = L::PA, NCT = WL::NCT;
+    constexpr int PD = L::PD, NCT = WL::NCT;
     constexpr int CPL = D / 32, NH = K - 1, RL = CH / 16, NR = RL + NH;
     static_assert(RL >= NH, "only the first run of a chunk reaches before the chunk");
     static_assert(3 * D * NH <= 4 * 3 * 16 * 17, "conv history fits the inverse scratch area");
@@ -731,8 +744,8 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra_act(
                     vreg[ks][e] = w < NCT ? x : 0.0f;
                 }
         }
-        __syncthreads();   // v staging read before A is cleared
-        for (int e = tid; e < 2 * CH * PA; e += P1_THREADS) sA[e] = 0.0f;   // A and Tm
+        __syncthreads();   // v staging read before the A/Tm area is written
+        zero_upper<D>(sA + CH * L::PA, tid);
         const int next = min(item + 1, hi - 1);
         p1_item<D>(lds, vreg, blk_addr<D>(ws, c, H, h), [&](int part) { fetch(next, part); });
     }
