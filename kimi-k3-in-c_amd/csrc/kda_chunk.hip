@@ -129,13 +129,15 @@ __device__ __forceinline__ void store_cpl(float *p, const float (&v)[CPL])
     else *reinterpret_cast<f2 *>(p) = f2{v[0], v[1]};
 }
 
-// Split x and store it as lane `lane` of the fragment block at `blk`.
+// Split x and store it as lane `lane` of the fragment block at `blk`. Workspace stores are
+// nontemporal: the block is read back by the next kernel from HBM (its L2 warm-up touches),
+// so keeping it in this kernel's L2 only displaces the inputs (c2 phase 1: -5 us).
 __device__ __forceinline__ void store_frag(char *blk, int lane, const float (&x)[8])
 {
     bf16x8 hi, lo;
     split8(x, hi, lo);
-    *reinterpret_cast<bf16x8 *>(blk + lane * 16) = hi;
-    *reinterpret_cast<bf16x8 *>(blk + 1024 + lane * 16) = lo;
+    __builtin_nontemporal_store(hi, reinterpret_cast<bf16x8 *>(blk + lane * 16));
+    __builtin_nontemporal_store(lo, reinterpret_cast<bf16x8 *>(blk + 1024 + lane * 16));
 }
 
 struct Frag {
@@ -466,7 +468,7 @@ __device__ __forceinline__ void p1_item(float *lds, const float (&vreg)[2][8], c
         }
 #pragma unroll
         for (int a = 0; a < 4; a++) {
-            *reinterpret_cast<f32x4 *>(blk + WL::UC + ((size_t)(a * NCT + nt) * 64 + lane) * 16) = au[a];
+            __builtin_nontemporal_store(au[a], reinterpret_cast<f32x4 *>(blk + WL::UC + ((size_t)(a * NCT + nt) * 64 + lane) * 16));
 #pragma unroll
             for (int e = 0; e < 4; e++) sX[(SB * a + 4 * kg + e) * PD + n0 + m] = aw[a][e];
         }
