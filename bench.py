@@ -97,6 +97,21 @@ def ev_pair(torch):
     return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
 
+RAMP_S = 0.3
+
+
+def ramp(torch, step):
+    """Untimed: repeat the workload's own step for RAMP_S seconds before its warm-up steps.
+    From idle the GPU takes tens of milliseconds of sustained load to reach its working
+    clocks (c2 core: 0.63 ms per step after 3 warm-up steps, 0.585 after 20, 0.56 after
+    ~60), so a few warm-up steps alone measure the ramp, not the kernels."""
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < RAMP_S:
+        for _ in range(4):
+            step()
+        torch.cuda.synchronize()
+
+
 # -------------------------------------------------------------------- decode ----
 def bench_decode(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
     B, H, D = DEC["B"], DEC["H"], DEC["D"]
@@ -113,6 +128,7 @@ def bench_decode(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
         o = torch.empty((B, H, D), device="cuda")
         sets.append((S, o, q.contiguous(), k.contiguous(), v, alpha, beta))
     qs = 1.0 / math.sqrt(D)
+    ramp(torch, lambda: [k3.kda_decode(*sets[j], qs) for j in range(nsets)])
     for i in range(warmup):
         k3.kda_decode(*sets[i % nsets], qs)
     torch.cuda.synchronize()
@@ -236,6 +252,7 @@ def bench_prefill(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
             if fallback is None:
                 raise
             mode = fallback
+    ramp(torch, step)
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -314,6 +331,7 @@ def bench_layer(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
 
     step()
     torch.cuda.synchronize()
+    ramp(torch, step)
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -413,6 +431,7 @@ def bench_hybrid(torch, k3, steps: int, warmup: int) -> dict:
     h = kda_part()
     mla_part(h)
     torch.cuda.synchronize()
+    ramp(torch, lambda: mla_part(kda_part()))
     for _ in range(warmup):
         mla_part(kda_part())
     torch.cuda.synchronize()
