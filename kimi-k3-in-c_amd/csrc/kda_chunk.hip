@@ -331,7 +331,9 @@ __device__ __forceinline__ void p1_item(float *lds, const float (&vreg)[2][8], c
     //      squarings and three products, each a 16x16x16 fp32 MFMA product (4 x 16x16x4).
     //      Wave w < 4 inverts block w with all 64 lanes; the factors commute, so X is built
     //      as X = I + N^8, X += N^4 X, X += N^2 X, X -= N X.
+    //      The inverting waves raise their issue priority over the filler work of their SIMD.
     if (w < 4) {
+        __builtin_amdgcn_s_setprio(3);
         const int o = SB * w;
         float *N2 = sNS + (size_t)w * 3 * 272, *N4 = N2 + 272, *X = N4 + 272;
         const float *Nb = sA + o * PA + o;   // N, pitch PA
@@ -384,6 +386,7 @@ __device__ __forceinline__ void p1_item(float *lds, const float (&vreg)[2][8], c
                 for (int e = 0; e < 4; e++) sT[(o + 4 * kg + e) * PA + o + m] = x[e];
             }
         }
+        __builtin_amdgcn_s_setprio(0);
     } else {
         // meanwhile waves 4..7: q e^G (q scaled) as A-fragments [rt 4][KSI]
         for (int fb = w - 4; fb < 4 * KSI; fb += 4) {
@@ -884,6 +887,7 @@ __device__ __forceinline__ void row_step(const RowOps<D, NW> &op, const char *sS
 {
     constexpr int KSI = D / 32;
     f32x4 ao[NW];
+    __builtin_amdgcn_s_setprio(3);   // W S -> Vn is the step's critical path: issue it first
 #pragma unroll
     for (int j = 0; j < NW; j++) {
         // Vn = U - W S and O = Q S; two accumulators per product shorten the MFMA chains
@@ -904,6 +908,7 @@ __device__ __forceinline__ void row_step(const RowOps<D, NW> &op, const char *sS
         publish_frag4(sVF + (size_t)j * P2Lds<D>::VF, w, lane, op.u[j] - (aw0 + aw1));
         ao[j] = ao0 + ao1;
     }
+    __builtin_amdgcn_s_setprio(0);
     __syncthreads();   // (2) Vn published
     after2();
 #pragma unroll
@@ -1068,8 +1073,10 @@ __global__ __launch_bounds__(512) void kda_chunk_state(int T, int H, const char 
             touch(tA, c + PF);
             __builtin_amdgcn_sched_barrier(0);
             __syncthreads();   // (2) Vn published
+            __builtin_amdgcn_s_setprio(3);   // the S update is the other half of the critical path
             state_update<D, NW>(opA, accS, sVF, lane);
-            state_publish<D, NW>(accS, sSF, sw, lane);   // row waves read sSF before (2)
+            state_publish<D, NW>(accS, sSF, sw, lane);
+            __builtin_amdgcn_s_setprio(0);   // row waves read sSF before (2)
             if (c + 1 >= nch) break;
             __syncthreads();
             load_state_ops<D>(opA, blk_of(c + 2), sw, lane);
@@ -1077,8 +1084,10 @@ __global__ __launch_bounds__(512) void kda_chunk_state(int T, int H, const char 
             touch(tB, c + 1 + PF);
             __builtin_amdgcn_sched_barrier(0);
             __syncthreads();
+            __builtin_amdgcn_s_setprio(3);
             state_update<D, NW>(opB, accS, sVF, lane);
             state_publish<D, NW>(accS, sSF, sw, lane);
+            __builtin_amdgcn_s_setprio(0);
         }
 #pragma unroll
         for (int j = 0; j < NW; j++)
