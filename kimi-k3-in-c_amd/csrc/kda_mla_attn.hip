@@ -10,25 +10,28 @@
 // kv_b absorbed. The cache (302 MB at 16 sequences x 8192 positions x 576 floats) dominates
 // the bytes, so the kernel reads it exactly once, and everything else stays on the chip:
 //
-//  * A workgroup owns one sequence and a contiguous range of positions (~CUs/B ranges per
-//    sequence) and walks it in tiles of 16 positions (16 contiguous cache rows). A tile is
-//    loaded two tiles ahead into registers with 16-byte loads, split into bf16 hi/lo and
-//    staged row-major in LDS (double-buffered, one barrier per tile).
-//  * Four waves, one per SIMD; wave w owns heads 16w..16w+15 and lane l always works for
-//    head 16w + (l & 15), so a head's softmax state and its weighted sums sit in the same
-//    lanes and nothing is exchanged between waves:
+//  * A workgroup (8 waves, two per SIMD) owns one sequence and a contiguous range of
+//    positions (~CUs/B ranges per sequence) and walks it in tiles of 16 positions (16
+//    contiguous cache rows). A tile is loaded one tile ahead into registers with 16-byte
+//    loads, split into bf16 hi/lo and staged row-major in LDS (double-buffered).
+//  * Wave w works for head tile w % 4 (16 heads) and lane l always for head 16 (w % 4) +
+//    (l & 15), so a head's softmax state and its weighted sums sit in the same lanes:
 //      scores^T (positions x heads) = cache tile (16 x CW) . qcat^T on split-bf16 MFMA
 //        (16x16x32, cache rows read from LDS, q fragments held in registers for the whole
-//        range); lane l ends with the scores of its head at 4 of the tile's positions;
+//        range); the two waves of a head tile take half of the channels each and add their
+//        partial scores in the same order through LDS, so lane l of both ends with the same
+//        scores of its head at 4 of the tile's positions;
 //      online softmax in base 2: running max M (exchanged between the 4 lanes of a head),
 //        per-lane partial sums, the weighted sums rescaled by 2^(M_old - M_new) only when
 //        some max of the wave grew;
-//      chat^T (latent channels x heads) += latent tile^T . P on split-bf16 MFMA (16x16x16):
-//        the transposed latent fragments come straight from the row-major tile through
-//        ds_read_b64_tr_b16, and P is the score product's output without leaving the lanes.
+//      chat^T (latent channels x heads) += latent tile^T . P on split-bf16 MFMA (16x16x16),
+//        256 of the latent channels per wave: the transposed latent fragments come straight
+//        from the row-major tile through ds_read_b64_tr_b16, and P is the score product's
+//        output without leaving the lanes.
+//    Two barriers per tile: partial scores published, tile consumed.
 //  * Each workgroup writes its unnormalised sums with (M, l); a second kernel merges the
-//    ranges of a sequence (weights 2^(M_s - M*)) in range order, divides by the merged sum and
-//    writes chat directly as the bf16 hi/lo rows of the W_UV GEMM.
+//    ranges of a sequence (weights 2^(M_s - M*), the sums in a fixed order), divides by the
+//    merged sum and writes chat directly as the bf16 hi/lo rows of the W_UV GEMM.
 #include <math.h>
 
 #include <algorithm>

@@ -30,13 +30,6 @@ HIPCC_FLAGS = [
     f"-I{REPO / 'include'}", f"-I{CSRC}",
 ]
 
-# Per-source additions. The MLA attention kernel holds ~340 registers per lane at one wave
-# per SIMD; the VGPR form of the MFMA keeps its accumulators out of the AGPR<->VGPR copies
-# the default form inserts around every tile.
-EXTRA_FLAGS = {
-    "kda_mla_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
-}
-
 
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
@@ -47,7 +40,7 @@ def hipcc() -> str:
 
 def _compile(src: Path, verbose: bool) -> Path:
     obj = BUILD / (src.stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{r.stdout}\n{r.stderr}")
