@@ -288,9 +288,11 @@ __global__ __launch_bounds__(128) void mla_attn_merge_kernel(int B, int H, int K
     const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
     const float *mrow = pm + (size_t)b * nsplit * H + h, *lrow = pl + (size_t)b * nsplit * H + h;
     if (tid < 64) {
-        float mx = -INFINITY;
-        for (int s = 0; s < nsplit; s++) mx = fmaxf(mx, mrow[(size_t)s * H]);
-        const float wv = tid < nsplit ? __builtin_amdgcn_exp2f(mrow[(size_t)tid * H] - mx) : 0.0f;
+        const float mv = tid < nsplit ? mrow[(size_t)tid * H] : -INFINITY;
+        float mx = mv;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        const float wv = tid < nsplit ? __builtin_amdgcn_exp2f(mv - mx) : 0.0f;
         if (tid < nsplit) sw[tid] = wv;
         float lv = tid < nsplit ? wv * lrow[(size_t)tid * H] : 0.0f;
         // the weighted sums of the ranges, added in a fixed tree into lane 0
@@ -305,6 +307,7 @@ __global__ __launch_bounds__(128) void mla_attn_merge_kernel(int B, int H, int K
     const size_t BN = (size_t)B * H * KL;
     for (int c = 4 * tid; c < KL; c += 4 * blockDim.x) {
         f4 a = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 8
         for (int s = 0; s < nsplit; s++)
             a += sw[s] * *reinterpret_cast<const f4 *>(pctx + (((size_t)b * nsplit + s) * H + h) * KL + c);
         const size_t i = ((size_t)b * H + h) * KL + c;
