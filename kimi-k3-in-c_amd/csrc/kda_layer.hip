@@ -316,16 +316,25 @@ __global__ void to_bf16_kernel(const float *__restrict__ x, uint16_t *__restrict
         y[i] = f2bf(x[i]);
 }
 
-// x [rows][cols] fp32 -> y [rows][2 cols] bf16 with x = hi + lo: hi in columns 0..cols-1,
-// lo = bf16(x - hi) in cols..2cols-1 (the input of a K = 2 cols GEMM against [W | W]).
-__global__ void split_rows_kernel(const float *__restrict__ x, uint16_t *__restrict__ y, int cols, size_t n)
+// x [rows][D + H] fp32 (the f_a and b projections of one GEMM) -> y [rows][2D] bf16 with
+// f_a = hi + lo: hi in columns 0..D-1, lo = bf16(f_a - hi) in D..2D-1 (the input of a K = 2D
+// GEMM against [W | W]); the b logits are copied out to bl [rows][H].
+__global__ void split_fa_b_kernel(const float *__restrict__ x, uint16_t *__restrict__ y,
+                                  float *__restrict__ bl, int D, int H, size_t n)
 {
+    const int cols = D + H;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (size_t)gridDim.x * blockDim.x) {
-        const size_t r = i / (size_t)cols, c = i % (size_t)cols;
-        const uint16_t hi = f2bf(x[i]);
-        y[r * 2 * cols + c] = hi;
-        y[r * 2 * cols + cols + c] = f2bf(x[i] - __uint_as_float((uint32_t)hi << 16));
+        const size_t r = i / (size_t)cols;
+        const int c = (int)(i - r * (size_t)cols);
+        const float v = x[i];
+        if (c < D) {
+            const uint16_t hi = f2bf(v);
+            y[r * 2 * D + c] = hi;
+            y[r * 2 * D + D + c] = f2bf(v - __uint_as_float((uint32_t)hi << 16));
+        } else {
+            bl[r * H + (c - D)] = v;
+        }
     }
 }
 
@@ -393,10 +402,10 @@ extern "C" int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *
     const size_t P = (size_t)H * D, TP = (size_t)T * P;
     const size_t wsb = k3hip_kda_chunk_workspace(T, H, D, 64);
     // scratch, 256-byte aligned pieces:
-    //   0 x bf16 | 1 q k v gate projections fp32 | 2 f_a fp32 | 3 f_a hi/lo bf16 | 4 z fp32 |
+    //   0 x bf16 | 1 q k v gate projections fp32 | 2 f_a and b fp32 [T][D + H] | 3 f_a hi/lo bf16 | 4 z fp32 |
     //   5 b logits | 6 o fp32 | 7 y fp16 | 8 zero state | 9 chunk workspace |
     //   10 fp32 o_proj result for a bf16 out (hipBLASLt has no fp16 x fp16 -> bf16 GEMM)
-    size_t sizes[] = {x_dtype == K3HIP_F32 ? (size_t)T * E * 2 : 0, 4 * TP * 4, (size_t)T * D * 4,
+    size_t sizes[] = {x_dtype == K3HIP_F32 ? (size_t)T * E * 2 : 0, 4 * TP * 4, (size_t)T * (D + H) * 4,
                       (size_t)T * D * 4, TP * 4, (size_t)T * H * 4, TP * 4, TP * 2,
                       state ? 0 : (size_t)H * D * D * 4, wsb,
                       out_dtype == K3HIP_BF16 ? (size_t)T * E * 4 : 0};
@@ -433,14 +442,25 @@ extern "C" int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *
 
     // 1 projections on bf16 MFMA with fp32 accumulation and fp32 results; f_b takes f_a as a
     //   bf16 hi/lo pair (K = 2D against [W_fb | W_fb]) so z keeps fp32 accuracy
-    if ((rc = gemm_bf16(T, (int)P, E, xb, w->q, qp, K3HIP_F32, st))) return rc;
-    if ((rc = gemm_bf16(T, (int)P, E, xb, w->k, kp, K3HIP_F32, st))) return rc;
-    if ((rc = gemm_bf16(T, (int)P, E, xb, w->v, vp, K3HIP_F32, st))) return rc;
+    //   q, k, v are consecutive row blocks of one weight allocation and qp, kp, vp consecutive
+    //   T x P results, so they run as one batched GEMM (batch stride 0 on x)
+    {
+        GemmDesc g;
+        g.M = T; g.N = (int)P; g.K = E;
+        g.lda = E; g.ldb = E; g.ldc = (long)P;
+        g.batch = 3; g.sa = 0; g.sb = (long)P * E; g.sc = (long)TP;
+        const uint16_t *wq = (const uint16_t *)w->q;
+        if (w->k != wq + P * E || w->v != wq + 2 * P * E)
+            K3_FAIL(K3HIP_EINVAL, "kda layer: q, k, v weights are not one allocation");
+        if ((rc = gemm(g, xb, w->q, qp, st))) return rc;
+    }
     if ((rc = gemm_bf16(T, (int)P, E, xb, w->g, gl, K3HIP_F32, st))) return rc;
-    if ((rc = gemm_bf16(T, H, E, xb, w->b, bl, K3HIP_F32, st))) return rc;
-    if ((rc = gemm_bf16(T, D, E, xb, w->f_a, fa, K3HIP_F32, st))) return rc;
-    hipLaunchKernelGGL(split_rows_kernel, dim3(grid_for((size_t)T * D)), dim3(256), 0, st, fa, fa2, D,
-                       (size_t)T * D);
+    //   f_a and b are consecutive row blocks too: one N = D + H GEMM, split apart below
+    if ((const char *)w->b != (const char *)w->f_a + (size_t)D * E * 2)
+        K3_FAIL(K3HIP_EINVAL, "kda layer: f_a, b weights are not one allocation");
+    if ((rc = gemm_bf16(T, D + H, E, xb, w->f_a, fa, K3HIP_F32, st))) return rc;
+    hipLaunchKernelGGL(split_fa_b_kernel, dim3(grid_for((size_t)T * (D + H))), dim3(256), 0, st, fa,
+                       fa2, bl, D, H, (size_t)T * (D + H));
     K3_LAUNCHED();
     if ((rc = gemm_bf16(T, (int)P, 2 * D, fa2, w->f_b2, z, K3HIP_F32, st))) return rc;
     // 2-5 K1 fused into 6 K2 (chunked): the prepared q, k, v, g never reach HBM
