@@ -223,10 +223,11 @@ int k3hip_kda_layer_dev(const k3hip_kda_weights *w, int T, float *out, const flo
 
 /* The whole k3_kda_layer for a T-token prefill on bf16 weights (K3_WBF16) and bf16
  * activations: the projections (src/core/k3_ops.c:879-886, :946, :948) as bf16 MFMA GEMMs
- * with fp32 accumulation (hipBLASLt) and fp32 results; f_a and the epilogue output enter
- * their GEMMs (f_b, o_proj) as bf16 hi/lo pairs against [W | W], so no intermediate is
- * rounded to bf16 (a single bf16 rounding of q, k, v or y alone costs several times the
- * 2e-3 prefill bar). Then K1, K2 (chunked), K4 and o_proj.
+ * with fp32 accumulation (hipBLASLt) and fp32 results; f_a enters the f_b GEMM as a bf16
+ * hi/lo pair against [W_fb | W_fb], and the epilogue output y (RMS-normalised) enters o_proj
+ * in fp16 against an fp16 copy of W_o, so q, k, v and z are never rounded to bf16 (a single
+ * bf16 rounding of q, k, v or y alone costs several times the 2e-3 prefill bar). Then K1,
+ * K2 (chunked), K4 and o_proj.
  *   x [T][hidden] (x_dtype: fp32 inputs are rounded to bf16 first); out [T][hidden]
  *   (out_dtype); state as in k3_kda_layer (device, nullable).
  * Needs D = 64 / 128, conv_k <= 4 and -80/15 <= gate_lb < 0; otherwise
