@@ -210,11 +210,37 @@ int k3hip_kda_epilogue(int T, int H, int D, float rms_eps,
                        const float *o, const void *gate, int gate_dtype,
                        const float *o_norm, void *y, int y_dtype, void *stream);
 
+/* The projection GEMM of the bf16 prefill path (hand-written gfx950 MFMA kernel): every
+ * per-token k3_mmw call of src/core/k3_ops.c:879-886, :946, :948 (k3_matmul_bf16,
+ * :1122-1227) for T tokens is one row block of
+ *   C[M][N] = A[M][K] . B[N][K]^T      A activations, B the weight as stored ([out][in])
+ * with fp32 accumulation. ab_dtype K3HIP_BF16 or K3HIP_F16 (A and B alike); c_dtype
+ * K3HIP_F32, K3HIP_BF16 or K3HIP_F16; leading dimensions in elements. Needs K % 64 == 0,
+ * lda, ldb multiples of 8, ldc >= N, A and B 16-byte aligned (else K3HIP_EUNSUPPORTED).
+ * Stream-ordered, allocates nothing, bit-reproducible. */
+enum { K3HIP_F16 = 3 };
+int k3hip_proj_gemm(int M, int N, int K, int ab_dtype, const void *A, long lda, const void *B, long ldb,
+                    void *C, int c_dtype, long ldc, void *stream);
+
 /* Device-resident weights for the full layer. Matrices keep their wdt (fp32 or bf16);
  * the small fp32 vectors are copied as is. */
 typedef struct k3hip_kda_weights k3hip_kda_weights;
 int k3hip_kda_upload(const K3KdaW *w, const K3Cfg *c, k3hip_kda_weights **out);
 int k3hip_kda_release(k3hip_kda_weights *w);
+
+/* What an upload copies. DEV is always made: the matrices in their own storage and the fp32
+ * vectors, all that k3hip_kda_layer_dev reads. PREFILL adds the derived copies of the bf16
+ * prefill path (k3hip_kda_layer_prefill), DECODE the MFMA fragment-ordered copies of the
+ * batched decode path (k3hip_kda_layer_decode); those entry points return K3HIP_EINVAL on
+ * weights uploaded without their part. k3hip_kda_upload makes every part. The drop-in
+ * k3_kda_layer uploads DEV only, per call (the reference binds weights per call too). */
+enum { K3HIP_UPLOAD_DEV = 1, K3HIP_UPLOAD_PREFILL = 2, K3HIP_UPLOAD_DECODE = 4, K3HIP_UPLOAD_ALL = 7 };
+int k3hip_kda_upload_ex(const K3KdaW *w, const K3Cfg *c, int parts, k3hip_kda_weights **out);
+/* Device bytes an uploaded weight set holds. */
+size_t k3hip_kda_weights_bytes(const k3hip_kda_weights *w);
+/* Bytes the calling thread's last k3_kda_layer call copied between host and device (its
+ * weight upload, x, out and state): the drop-in's transfer cost per call. */
+size_t k3hip_kda_dropin_bytes(void);
 
 /* The whole k3_kda_layer on device pointers: projections, K1, K2 (T>1) or K3 (T==1),
  * K4, o_proj. x,out [T][hidden] fp32; state as in k3_kda_layer (device, nullable). */

@@ -1104,7 +1104,7 @@ __global__ __launch_bounds__(512) void kda_chunk_state(int T, int H, const char 
 bool chunk_ready() { return true; }
 
 // Compute units of the current device (cached per device).
-static int cu_count(int &ncu)
+int cu_count(int &ncu)
 {
     static int cache[64];
     int dev = 0;

@@ -87,6 +87,10 @@ __global__ __launch_bounds__(256) void kda_epilogue2_kernel(long rows, int H, fl
             const uint2 u = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(gate) + base);
             gt = f4{__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
                     __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u)};
+        } else if constexpr (GDT == K3_DT_F16) {
+            typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+            const h4 u = *reinterpret_cast<const h4 *>(reinterpret_cast<const _Float16 *>(gate) + base);
+            gt = f4{(float)u[0], (float)u[1], (float)u[2], (float)u[3]};
         } else {
             gt = *reinterpret_cast<const f4 *>(reinterpret_cast<const float *>(gate) + base);
         }
@@ -177,7 +181,8 @@ int epilogue_split(int T, int H, int D, float eps, const float *o, const void *g
     const bool g16 = gate_dtype == K3HIP_BF16;
     if (y_f16) {
 #define K3_EPI16(DD, G) hipLaunchKernelGGL((kda_epilogue2_kernel<DD, G, Y_F16>), dim3((unsigned)blocks), dim3(256), 0, st, rows, H, eps, o, gate, o_norm, y2)
-        if (D == 128) { if (g16) K3_EPI16(128, K3HIP_BF16); else K3_EPI16(128, K3HIP_F32); }
+        if (gate_dtype == K3_DT_F16) { if (D == 128) K3_EPI16(128, K3_DT_F16); else K3_EPI16(64, K3_DT_F16); }
+        else if (D == 128) { if (g16) K3_EPI16(128, K3HIP_BF16); else K3_EPI16(128, K3HIP_F32); }
         else { if (g16) K3_EPI16(64, K3HIP_BF16); else K3_EPI16(64, K3HIP_F32); }
 #undef K3_EPI16
         K3_LAUNCHED();

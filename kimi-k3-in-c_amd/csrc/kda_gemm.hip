@@ -9,10 +9,12 @@
 // column-major terms C^T = W . A^T, i.e. op(A) = T on W (K x N, ld K), op(B) = N on A
 // (K x M, ld K), D = C^T (N x M, ld N).
 //
-// Per device: one handle and one workspace, created on first use. On the first call of a
-// shape (M, N, K, C dtype) up to 24 heuristic candidates are timed on that call's buffers and
-// the fastest is cached; that first call synchronizes its stream (keep it out of graph
-// capture). Later calls are stream-ordered on the caller's stream.
+// Per device: one handle, created on first use. The algorithm of a shape is hipBLASLt's
+// heuristic first choice, never a timing, so two processes run the same kernel and produce
+// the same bits. A plan (descriptors + algorithm) is cached per shape; shapes that change
+// every call (GemmDesc::cache = false, e.g. a growing decode context) build one, run it and
+// destroy it. An algorithm that needs workspace gets it stream-ordered on the caller's
+// stream for that call, so calls in flight on different streams never share it.
 #include <hipblaslt/hipblaslt.h>
 
 #include <map>
@@ -25,7 +27,7 @@ namespace k3kda {
 
 namespace {
 
-constexpr size_t GEMM_WS = 64ull << 20;   // hipBLASLt workspace per device
+constexpr size_t GEMM_WS = 64ull << 20;   // largest workspace an algorithm may ask for
 constexpr int MAX_DEV = 64;
 
 struct Plan {
@@ -39,9 +41,17 @@ typedef std::tuple<int, int, int, int, int, int, long, long, long, int, long, lo
 
 struct DevGemm {
     hipblasLtHandle_t h = nullptr;
-    void *ws = nullptr;
     std::map<Key, Plan> plans;
 };
+
+void destroy_plan(Plan &p)
+{
+    if (p.la) (void)hipblasLtMatrixLayoutDestroy(p.la);
+    if (p.lb) (void)hipblasLtMatrixLayoutDestroy(p.lb);
+    if (p.lc) (void)hipblasLtMatrixLayoutDestroy(p.lc);
+    if (p.op) (void)hipblasLtMatmulDescDestroy(p.op);
+    p = Plan();
+}
 
 std::mutex g_mu;
 DevGemm g_dev[MAX_DEV];
@@ -78,13 +88,8 @@ int set_batch(hipblasLtMatrixLayout_t l, int batch, long stride)
     return K3HIP_OK;
 }
 
-// Candidates from the heuristic, each timed on the call's own buffers (first call of a
-// shape only; that call synchronizes the stream). The fastest is kept if it beats the
-// heuristic's first choice by more than 10%.
-constexpr int NCAND = 24;
-
-int make_plan(DevGemm &d, const GemmDesc &g, Plan &p, const void *A, const void *B, void *Cm,
-              hipStream_t st)
+// The heuristic's first algorithm for the shape (deterministic: no timing).
+int make_plan(DevGemm &d, const GemmDesc &g, Plan &p)
 {
     const hipDataType abt = g.ab_dtype == K3HIP_BF16 ? HIP_R_16BF : g.ab_dtype == K3_DT_F16 ? HIP_R_16F : HIP_R_32F;
     const hipDataType ct = g.c_dtype == K3HIP_BF16 ? HIP_R_16BF : HIP_R_32F;
@@ -106,49 +111,29 @@ int make_plan(DevGemm &d, const GemmDesc &g, Plan &p, const void *A, const void 
     const uint64_t wmax = GEMM_WS;
     hipblasStatus_t s = hipblasLtMatmulPreferenceSetAttribute(
         pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wmax, sizeof wmax);
-    hipblasLtMatmulHeuristicResult_t res[NCAND];
+    hipblasLtMatmulHeuristicResult_t res[1];
     int n = 0;
     if (s == HIPBLAS_STATUS_SUCCESS)
-        s = hipblasLtMatmulAlgoGetHeuristic(d.h, p.op, p.la, p.lb, p.lc, p.lc, pref, NCAND, res, &n);
+        s = hipblasLtMatmulAlgoGetHeuristic(d.h, p.op, p.la, p.lb, p.lc, p.lc, pref, 1, res, &n);
     (void)hipblasLtMatmulPreferenceDestroy(pref);
-    if (s != HIPBLAS_STATUS_SUCCESS || n == 0)
+    if (s != HIPBLAS_STATUS_SUCCESS || n == 0 || res[0].state != HIPBLAS_STATUS_SUCCESS)
         K3_FAIL(K3HIP_EUNSUPPORTED, "hipBLASLt has no algorithm for a %dx%dx%d (batch %d) GEMM (%s)",
                 g.M, g.N, g.K, g.batch, lt_status(s));
-    int best = 0;
-    if (n > 1 && g.tune) {
-        hipEvent_t e0, e1;
-        K3_HIP(hipEventCreate(&e0));
-        K3_HIP(hipEventCreate(&e1));
-        const float alpha = 1.0f, beta = 0.0f;
-        float best_ms = 1e30f, first_ms = 1e30f;
-        for (int i = 0; i < n; i++) {
-            if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > GEMM_WS) continue;
-            auto run = [&]() {
-                return hipblasLtMatmul(d.h, p.op, &alpha, B, p.la, A, p.lb, &beta, Cm, p.lc, Cm, p.lc,
-                                       &res[i].algo, res[i].workspaceSize ? d.ws : nullptr,
-                                       res[i].workspaceSize, st);
-            };
-            if (run() != HIPBLAS_STATUS_SUCCESS) continue;   // warm-up; skip what fails
-            K3_HIP(hipEventRecord(e0, st));
-            for (int r = 0; r < 3; r++) (void)run();
-            K3_HIP(hipEventRecord(e1, st));
-            K3_HIP(hipEventSynchronize(e1));
-            float ms = 0.0f;
-            K3_HIP(hipEventElapsedTime(&ms, e0, e1));
-            if (i == 0) first_ms = ms;
-            if (ms < best_ms) {
-                best_ms = ms;
-                best = i;
-            }
-        }
-        (void)hipEventDestroy(e0);
-        (void)hipEventDestroy(e1);
-        // back-to-back timing on warm caches is noisy and favours some tilings that are not
-        // faster in a pipeline: leave the heuristic's first choice only for a clear win
-        if (best_ms > 0.9f * first_ms) best = 0;
+    p.algo = res[0].algo;
+    p.ws = res[0].workspaceSize;
+    return K3HIP_OK;
+}
+
+int run_plan(DevGemm &d, const Plan &p, const void *A, const void *B, void *C, hipStream_t st)
+{
+    StreamBuf ws;
+    if (p.ws) {
+        int rc = stream_alloc(ws, p.ws, st);
+        if (rc) return rc;
     }
-    p.algo = res[best].algo;
-    p.ws = res[best].workspaceSize;
+    const float alpha = 1.0f, beta = 0.0f;
+    K3_LT(hipblasLtMatmul(d.h, p.op, &alpha, B, p.la, A, p.lb, &beta, C, p.lc, C, p.lc, &p.algo, ws.p,
+                          p.ws, st));
     return K3HIP_OK;
 }
 
@@ -165,24 +150,27 @@ int gemm(const GemmDesc &g, const void *A, const void *B, void *C, hipStream_t s
     if (dev < 0 || dev >= MAX_DEV) K3_FAIL(K3HIP_EUNSUPPORTED, "gemm: device %d", dev);
     std::lock_guard<std::mutex> lock(g_mu);
     DevGemm &d = g_dev[dev];
-    if (!d.h) {
-        K3_LT(hipblasLtCreate(&d.h));
-        K3_HIP(hipMalloc(&d.ws, GEMM_WS));
+    if (!d.h) K3_LT(hipblasLtCreate(&d.h));
+    if (!g.cache) {
+        Plan p;
+        int rc = make_plan(d, g, p);
+        if (rc == K3HIP_OK) rc = run_plan(d, p, A, B, C, st);
+        destroy_plan(p);
+        return rc;
     }
-    const Key key{g.M, g.N, g.K, g.ab_dtype, g.c_dtype, (g.b_trans ? 1 : 0) | (g.tune ? 2 : 0), g.lda,
-                  g.ldb, g.ldc, g.batch, g.sa, g.sb, g.sc};
+    const Key key{g.M, g.N, g.K, g.ab_dtype, g.c_dtype, g.b_trans ? 1 : 0, g.lda, g.ldb, g.ldc, g.batch,
+                  g.sa, g.sb, g.sc};
     auto it = d.plans.find(key);
     if (it == d.plans.end()) {
         Plan p;
-        int rc = make_plan(d, g, p, A, B, C, st);
-        if (rc) return rc;
+        int rc = make_plan(d, g, p);
+        if (rc) {
+            destroy_plan(p);
+            return rc;
+        }
         it = d.plans.emplace(key, p).first;
     }
-    const Plan &p = it->second;
-    const float alpha = 1.0f, beta = 0.0f;
-    K3_LT(hipblasLtMatmul(d.h, p.op, &alpha, B, p.la, A, p.lb, &beta, C, p.lc, C, p.lc, &p.algo,
-                          p.ws ? d.ws : nullptr, p.ws, st));
-    return K3HIP_OK;
+    return run_plan(d, it->second, A, B, C, st);
 }
 
 int gemm_bf16(int M, int N, int K, const void *A, const void *W, void *C, int c_dtype, hipStream_t st)

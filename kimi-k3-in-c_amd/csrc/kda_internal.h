@@ -13,7 +13,7 @@ int proj(int T, int in, int out, const float *x, const void *W, int wdt, float *
 // B [N][K] (b_trans) or B for B [K][N]; A and B both bf16 or both fp32; C bf16 or fp32;
 // leading dimensions in elements; `batch` strided problems (strides in elements).
 // fp16 operands/results, internal only (the public dtypes are K3HIP_F32 and K3HIP_BF16)
-constexpr int K3_DT_F16 = 3;
+constexpr int K3_DT_F16 = K3HIP_F16;
 
 struct GemmDesc {
     int M = 0, N = 0, K = 0;
@@ -22,7 +22,7 @@ struct GemmDesc {
     long lda = 0, ldb = 0, ldc = 0;
     int batch = 1;
     long sa = 0, sb = 0, sc = 0;
-    bool tune = true;   // time the heuristic's candidates on the first call of the shape
+    bool cache = true;  // keep the plan for later calls of the shape (false: a shape seen once)
 };
 int gemm(const GemmDesc &g, const void *A, const void *B, void *C, hipStream_t st);
 
@@ -30,6 +30,22 @@ int gemm(const GemmDesc &g, const void *A, const void *B, void *C, hipStream_t s
 int gemm_bf16(int M, int N, int K, const void *A, const void *W, void *C, int c_dtype, hipStream_t st);
 // The same on fp16 MFMA (A, W fp16 row-major), fp32 accumulation.
 int gemm_f16(int M, int N, int K, const void *A, const void *W, void *C, int c_dtype, hipStream_t st);
+
+// Hand-written MFMA GEMM (kda_mm.hip): C[M][N] = A[M][K] . B[N][K]^T, A and B both bf16
+// (ab = K3HIP_BF16) or both fp16 (K3_DT_F16), K-contiguous rows (lda, ldb in elements), fp32
+// accumulation; C fp32, fp16 or bf16 (out), row stride ldc. With gcols > 0, output columns
+// [g*gcols, (g+1)*gcols) are written to the matrix at C + g*gstride elements (one launch
+// filling several row-major outputs). Needs K % 64 == 0, lda and ldb multiples of 8 and
+// 16-byte aligned A and B (mm_supported); returns K3HIP_EUNSUPPORTED otherwise.
+bool mm_supported(int K, long lda, long ldb);
+int mm(int M, int N, int K, int ab, const void *A, long lda, const void *B, long ldb, void *C, int out, long ldc,
+       hipStream_t st, int gcols = 0, long gstride = 0);
+// The same product as `splits` fp32 K-range partial planes P[s][M][N] (ld N), s increasing
+// with K; their sum in increasing s is the product, bit for bit on every run.
+// mm_splits(M, N, K, CUs) picks a split count that fills the GPU for narrow shapes.
+int mm_splits(int M, int N, int K, int ncu);
+int mm_splitk(int M, int N, int K, int splits, int ab, const void *A, long lda, const void *B, long ldb, float *P,
+              hipStream_t st);
 
 // K4 with y written as a bf16 hi/lo pair into y2 [T][2P] (hi columns 0..P-1, lo P..2P-1),
 // for an o_proj GEMM with K = 2P against [W_o | W_o]. D = 64 / 128, 16-byte aligned.
@@ -109,6 +125,9 @@ int zero_fill(float *p, size_t n, hipStream_t st);
 // dtype dt, launched after every reader of the incoming history on `st`.
 int conv_state_update(int T, int P, int K, int dt, const void *qi, const void *ki, const void *vi,
                       float *cs, hipStream_t st);
+
+// Compute units of the current device (cached per device).
+int cu_count(int &ncu);
 
 // True once the chunked prefill kernel is built into this library.
 bool chunk_ready();

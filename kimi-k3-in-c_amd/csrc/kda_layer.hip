@@ -69,7 +69,8 @@ int stream_alloc(StreamBuf &b, size_t bytes, hipStream_t st)
 using namespace k3kda;
 
 struct k3hip_kda_weights {
-    int hidden, H, D, K, wdt;
+    int hidden, H, D, K, wdt, parts;   // parts: the K3HIP_UPLOAD_* copies that were made
+    size_t bytes;                      // device bytes held
     float gate_lb, rms_eps;
     // q, k, v, f_a, b are row blocks of one allocation xin ([3P + D + H][hidden], in that
     // order), so a decode step projects into all five with one pass over the weights
@@ -111,12 +112,19 @@ __global__ void bf16_to_f16_kernel(const uint16_t *__restrict__ w, uint16_t *__r
     }
 }
 
-static int upload(void **dst, const void *src, size_t bytes)
+// Bytes the calling thread's last k3_kda_layer call copied host to device (weights,
+// activations, state) and back; the drop-in's cost beyond its arithmetic.
+static thread_local size_t g_dropin_h2d, g_dropin_d2h;
+static thread_local bool g_in_dropin;   // counting: inside k3_kda_layer
+
+static int upload(void **dst, const void *src, size_t bytes, size_t *held)
 {
     *dst = nullptr;
     if (!src) K3_FAIL(K3HIP_EINVAL, "k3hip_kda_upload: NULL weight");
     K3_HIP(hipMalloc(dst, bytes ? bytes : 4));
     K3_HIP(hipMemcpy(*dst, src, bytes, hipMemcpyHostToDevice));
+    *held += bytes;
+    if (g_in_dropin) g_dropin_h2d += bytes;
     return K3HIP_OK;
 }
 
@@ -135,8 +143,18 @@ extern "C" int k3hip_kda_release(k3hip_kda_weights *w)
 
 extern "C" int k3hip_kda_upload(const K3KdaW *w, const K3Cfg *c, k3hip_kda_weights **out)
 {
+    return k3hip_kda_upload_ex(w, c, K3HIP_UPLOAD_ALL, out);
+}
+
+extern "C" size_t k3hip_kda_weights_bytes(const k3hip_kda_weights *w) { return w ? w->bytes : 0; }
+
+extern "C" size_t k3hip_kda_dropin_bytes(void) { return g_dropin_h2d + g_dropin_d2h; }
+
+extern "C" int k3hip_kda_upload_ex(const K3KdaW *w, const K3Cfg *c, int parts, k3hip_kda_weights **out)
+{
     clear_error();
     if (!w || !c || !out) K3_FAIL(K3HIP_EINVAL, "k3hip_kda_upload: NULL argument");
+    if (parts & ~K3HIP_UPLOAD_ALL) K3_FAIL(K3HIP_EINVAL, "k3hip_kda_upload_ex: parts=%#x", parts);
     *out = nullptr;
     const int E = c->hidden, H = c->kda_heads, D = c->kda_head_dim, K = c->conv_k;
     if (E <= 0 || H <= 0 || D <= 0 || K <= 0)
@@ -145,7 +163,7 @@ extern "C" int k3hip_kda_upload(const K3KdaW *w, const K3Cfg *c, k3hip_kda_weigh
         K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_upload: weight tag %d (fp32=0, bf16=1 only)", w->wdt);
     k3hip_kda_weights *d = (k3hip_kda_weights *)calloc(1, sizeof *d);
     if (!d) K3_FAIL(K3HIP_ENOMEM, "k3hip_kda_upload: host allocation");
-    d->hidden = E; d->H = H; d->D = D; d->K = K; d->wdt = w->wdt;
+    d->hidden = E; d->H = H; d->D = D; d->K = K; d->wdt = w->wdt; d->parts = parts | K3HIP_UPLOAD_DEV;
     d->gate_lb = c->gate_lb; d->rms_eps = c->rms_eps;
     const size_t P = (size_t)H * D, es = w->wdt == K3_WBF16 ? 2 : 4;
     int rc = K3HIP_OK;
@@ -172,10 +190,12 @@ extern "C" int k3hip_kda_upload(const K3KdaW *w, const K3Cfg *c, k3hip_kda_weigh
                 set_error("k3hip_kda_upload: weight copy failed");
                 rc = K3HIP_EHIP;
             }
+            d->bytes += rows[i] * rowb;
+            if (g_in_dropin) g_dropin_h2d += rows[i] * rowb;
             at += rows[i];
         }
     }
-#define UP(field, src, bytes) if (rc == K3HIP_OK) rc = upload((void **)&d->field, src, bytes)
+#define UP(field, src, nbytes) if (rc == K3HIP_OK) rc = upload((void **)&d->field, src, nbytes, &d->bytes)
     UP(f_b, w->f_b, P * D * es);
     UP(g, w->g, P * E * es);
     UP(o, w->o, (size_t)E * P * es);
@@ -190,6 +210,7 @@ extern "C" int k3hip_kda_upload(const K3KdaW *w, const K3Cfg *c, k3hip_kda_weigh
     auto twice = [&](void **dst, const void *src, size_t rows, size_t cols) -> int {
         const size_t rb = cols * 2;
         K3_HIP(hipMalloc(dst, rows * rb * 2));
+        d->bytes += rows * rb * 2;
         K3_HIP(hipMemcpy2D(*dst, 2 * rb, src, rb, rb, rows, hipMemcpyDeviceToDevice));
         K3_HIP(hipMemcpy2D((char *)*dst + rb, 2 * rb, src, rb, rb, rows, hipMemcpyDeviceToDevice));
         return K3HIP_OK;
@@ -198,6 +219,7 @@ extern "C" int k3hip_kda_upload(const K3KdaW *w, const K3Cfg *c, k3hip_kda_weigh
     auto to_f16 = [&](void **dst, const void *src, size_t n) -> int {
         int *bad = nullptr, hbad = 0;
         K3_HIP(hipMalloc(dst, n * 2));
+        d->bytes += n * 2;
         K3_HIP(hipMalloc(&bad, sizeof(int)));
         int r = K3HIP_OK;
         if (hipMemcpy(bad, &hbad, sizeof(int), hipMemcpyHostToDevice) != hipSuccess) r = K3HIP_EHIP;
@@ -214,21 +236,23 @@ extern "C" int k3hip_kda_upload(const K3KdaW *w, const K3Cfg *c, k3hip_kda_weigh
             return r;
         }
         if (hbad) {
+            d->bytes -= n * 2;
             (void)hipFree(*dst);
             *dst = nullptr;   // the prefill refuses these weights; decode does not need the copy
         }
         return K3HIP_OK;
     };
-    if (rc == K3HIP_OK && w->wdt == K3_WBF16) {
+    if (rc == K3HIP_OK && w->wdt == K3_WBF16 && (parts & K3HIP_UPLOAD_PREFILL)) {
         rc = twice(&d->f_b2, d->f_b, P, (size_t)D);
         if (rc == K3HIP_OK) rc = to_f16(&d->o16, d->o, (size_t)E * P);
     }
     // fragment-ordered copies for the decode projections (row-major stays for prefill)
     auto frag = [&](void **dst, const void *src, int N, int Kd) -> int {
         K3_HIP(hipMalloc(dst, rows_frag_elems(N, Kd) * 2));
+        d->bytes += rows_frag_elems(N, Kd) * 2;
         return rows_frag_pack((const uint16_t *)src, N, Kd, (uint16_t *)*dst, nullptr);
     };
-    if (rc == K3HIP_OK && w->wdt == K3_WBF16 && E % 8 == 0 && D % 8 == 0) {
+    if (rc == K3HIP_OK && w->wdt == K3_WBF16 && E % 8 == 0 && D % 8 == 0 && (parts & K3HIP_UPLOAD_DECODE)) {
         rc = frag(&d->xin_f, d->xin, (int)(3 * P) + D + H, E);
         if (rc == K3HIP_OK) rc = frag(&d->g_f, d->g, (int)P, E);
         if (rc == K3HIP_OK) rc = frag(&d->f_b_f, d->f_b, (int)P, D);
@@ -338,6 +362,29 @@ __global__ void split_fa_b_kernel(const float *__restrict__ x, uint16_t *__restr
     }
 }
 
+// The f_a / b projection left as `splits` K-range partial planes P[s][rows][D + H]: their sum
+// in increasing s, f_a (columns 0..D-1) written as the bf16 pair y [rows][2D] (hi | lo, the
+// input of the K = 2D GEMM against [W_fb | W_fb]) and the b logits to bl [rows][H].
+__global__ void fab_reduce_kernel(const float *__restrict__ P, int splits, uint16_t *__restrict__ y,
+                                  float *__restrict__ bl, int D, int H, size_t n)
+{
+    const int cols = D + H;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x) {
+        float v = P[i];
+        for (int s = 1; s < splits; s++) v += P[(size_t)s * n + i];
+        const size_t r = i / (size_t)cols;
+        const int c = (int)(i - r * (size_t)cols);
+        if (c < D) {
+            const uint16_t hi = f2bf(v);
+            y[r * 2 * D + c] = hi;
+            y[r * 2 * D + D + c] = f2bf(v - __uint_as_float((uint32_t)hi << 16));
+        } else {
+            bl[r * H + (c - D)] = v;
+        }
+    }
+}
+
 static unsigned grid_for(size_t n)
 {
     size_t b = (n + 255) / 256;
@@ -390,8 +437,10 @@ extern "C" int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *
     if ((x_dtype != K3HIP_F32 && x_dtype != K3HIP_BF16) || (out_dtype != K3HIP_F32 && out_dtype != K3HIP_BF16))
         K3_FAIL(K3HIP_EINVAL, "k3hip_kda_layer_prefill: x_dtype=%d out_dtype=%d", x_dtype, out_dtype);
     const int E = w->hidden, H = w->H, D = w->D, K = w->K;
-    if (w->wdt != K3_WBF16 || !w->f_b2)
+    if (w->wdt != K3_WBF16)
         K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_layer_prefill: bf16 weights only (use k3hip_kda_layer_dev)");
+    if (!(w->parts & K3HIP_UPLOAD_PREFILL))
+        K3_FAIL(K3HIP_EINVAL, "k3hip_kda_layer_prefill: weights uploaded without K3HIP_UPLOAD_PREFILL");
     if (!w->o16)
         K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_layer_prefill: W_o has values beyond fp16 range (use k3hip_kda_layer_dev)");
     if (!chunk_gate_ok(w->gate_lb) || (D != 64 && D != 128) || K > 4)
@@ -401,14 +450,19 @@ extern "C" int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *
     hipStream_t st = as_stream(stream);
     const size_t P = (size_t)H * D, TP = (size_t)T * P;
     const size_t wsb = k3hip_kda_chunk_workspace(T, H, D, 64);
+    // the hand-written GEMM covers K % 64 == 0 (hidden, P and 2D); other widths take hipBLASLt
+    const bool own = mm_supported(E, E, E) && mm_supported((int)P, (long)P, (long)P) && mm_supported(2 * D, 2 * D, 2 * D);
+    int ncu = 256, rc;
+    if ((rc = cu_count(ncu))) return rc;
+    const int fab_s = own ? mm_splits(T, D + H, E, ncu) : 1;
     // scratch, 256-byte aligned pieces:
-    //   0 x bf16 | 1 q k v gate projections fp32 | 2 f_a and b fp32 [T][D + H] | 3 f_a hi/lo bf16 | 4 z fp32 |
-    //   5 b logits | 6 o fp32 | 7 y fp16 | 8 zero state | 9 chunk workspace |
-    //   10 fp32 o_proj result for a bf16 out (hipBLASLt has no fp16 x fp16 -> bf16 GEMM)
-    size_t sizes[] = {x_dtype == K3HIP_F32 ? (size_t)T * E * 2 : 0, 4 * TP * 4, (size_t)T * (D + H) * 4,
-                      (size_t)T * D * 4, TP * 4, (size_t)T * H * 4, TP * 4, TP * 2,
+    //   0 x bf16 | 1 q k v projections fp32 | 2 f_a and b fp32 (split-K planes) | 3 f_a hi/lo bf16 |
+    //   4 z fp32 | 5 b logits | 6 o fp32 | 7 gate fp16 | 8 y fp16 | 9 zero state | 10 chunk workspace |
+    //   11 fp32 o_proj result (fallback path with a bf16 out)
+    size_t sizes[] = {x_dtype == K3HIP_F32 ? (size_t)T * E * 2 : 0, 3 * TP * 4, (size_t)fab_s * T * (D + H) * 4,
+                      (size_t)T * D * 4, TP * 4, (size_t)T * H * 4, TP * 4, TP * 2, TP * 2,
                       state ? 0 : (size_t)H * D * D * 4, wsb,
-                      out_dtype == K3HIP_BF16 ? (size_t)T * E * 4 : 0};
+                      (!own && out_dtype == K3HIP_BF16) ? (size_t)T * E * 4 : 0};
     constexpr int NB = sizeof sizes / sizeof sizes[0];
     size_t off[NB], total = 0;
     for (int i = 0; i < NB; i++) {
@@ -416,8 +470,7 @@ extern "C" int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *
         total += (sizes[i] + 255) & ~(size_t)255;
     }
     StreamBuf buf;
-    int rc = stream_alloc(buf, total, st);
-    if (rc) return rc;
+    if ((rc = stream_alloc(buf, total, st))) return rc;
     char *base = (char *)buf.p;
     const void *xb = x;
     if (x_dtype == K3HIP_F32) {
@@ -427,53 +480,65 @@ extern "C" int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *
         K3_LAUNCHED();
         xb = base + off[0];
     }
-    float *qp = (float *)(base + off[1]), *kp = qp + TP, *vp = kp + TP, *gl = vp + TP;
+    float *qp = (float *)(base + off[1]), *kp = qp + TP, *vp = kp + TP;
     float *fa = (float *)(base + off[2]);
     uint16_t *fa2 = (uint16_t *)(base + off[3]);
     float *z = (float *)(base + off[4]), *bl = (float *)(base + off[5]);
     float *o = (float *)(base + off[6]);
-    uint16_t *y16 = (uint16_t *)(base + off[7]);
+    uint16_t *g16 = (uint16_t *)(base + off[7]), *y16 = (uint16_t *)(base + off[8]);
     float *S = state;
     if (!S) {
-        S = (float *)(base + off[8]);
+        S = (float *)(base + off[9]);
         if ((rc = zero_fill(S, (size_t)H * D * D, st))) return rc;
     }
     float *cs = state ? state + (size_t)H * D * D : nullptr;
+    const uint16_t *wq = (const uint16_t *)w->q;
+    if (w->k != wq + P * E || w->v != wq + 2 * P * E || (const char *)w->b != (const char *)w->f_a + (size_t)D * E * 2)
+        K3_FAIL(K3HIP_EINVAL, "kda layer: q, k, v (and f_a, b) weights are not one allocation");
 
-    // 1 projections on bf16 MFMA with fp32 accumulation and fp32 results; f_b takes f_a as a
-    //   bf16 hi/lo pair (K = 2D against [W_fb | W_fb]) so z keeps fp32 accuracy
-    //   q, k, v are consecutive row blocks of one weight allocation and qp, kp, vp consecutive
-    //   T x P results, so they run as one batched GEMM (batch stride 0 on x)
-    {
+    // 1 projections, fp32 results (a single bf16 rounding of q, k or v costs several times the
+    //   2e-3 bar): q, k, v as one GEMM over their consecutive weight rows, its three column
+    //   groups written to three [T][P] arrays; f_a and b as one split-K GEMM whose reduction
+    //   writes f_a as a bf16 hi/lo pair for z = [f_a_hi | f_a_lo] [W_fb | W_fb]^T (fp32 accuracy)
+    if (own) {
+        if ((rc = mm(T, 3 * (int)P, E, K3HIP_BF16, xb, E, wq, E, qp, K3HIP_F32, (long)P, st, (int)P, (long)TP)))
+            return rc;
+        if ((rc = mm_splitk(T, D + H, E, fab_s, K3HIP_BF16, xb, E, w->f_a, E, fa, st))) return rc;
+        const size_t n = (size_t)T * (D + H);
+        hipLaunchKernelGGL(fab_reduce_kernel, dim3(grid_for(n)), dim3(256), 0, st, fa, fab_s, fa2, bl, D, H, n);
+        K3_LAUNCHED();
+        if ((rc = mm(T, (int)P, 2 * D, K3HIP_BF16, fa2, 2 * D, w->f_b2, 2 * D, z, K3HIP_F32, (long)P, st))) return rc;
+    } else {
         GemmDesc g;
         g.M = T; g.N = (int)P; g.K = E;
         g.lda = E; g.ldb = E; g.ldc = (long)P;
         g.batch = 3; g.sa = 0; g.sb = (long)P * E; g.sc = (long)TP;
-        const uint16_t *wq = (const uint16_t *)w->q;
-        if (w->k != wq + P * E || w->v != wq + 2 * P * E)
-            K3_FAIL(K3HIP_EINVAL, "kda layer: q, k, v weights are not one allocation");
         if ((rc = gemm(g, xb, w->q, qp, st))) return rc;
+        if ((rc = gemm_bf16(T, D + H, E, xb, w->f_a, fa, K3HIP_F32, st))) return rc;
+        hipLaunchKernelGGL(split_fa_b_kernel, dim3(grid_for((size_t)T * (D + H))), dim3(256), 0, st, fa,
+                           fa2, bl, D, H, (size_t)T * (D + H));
+        K3_LAUNCHED();
+        if ((rc = gemm_bf16(T, (int)P, 2 * D, fa2, w->f_b2, z, K3HIP_F32, st))) return rc;
     }
-    if ((rc = gemm_bf16(T, (int)P, E, xb, w->g, gl, K3HIP_F32, st))) return rc;
-    //   f_a and b are consecutive row blocks too: one N = D + H GEMM, split apart below
-    if ((const char *)w->b != (const char *)w->f_a + (size_t)D * E * 2)
-        K3_FAIL(K3HIP_EINVAL, "kda layer: f_a, b weights are not one allocation");
-    if ((rc = gemm_bf16(T, D + H, E, xb, w->f_a, fa, K3HIP_F32, st))) return rc;
-    hipLaunchKernelGGL(split_fa_b_kernel, dim3(grid_for((size_t)T * (D + H))), dim3(256), 0, st, fa,
-                       fa2, bl, D, H, (size_t)T * (D + H));
-    K3_LAUNCHED();
-    if ((rc = gemm_bf16(T, (int)P, 2 * D, fa2, w->f_b2, z, K3HIP_F32, st))) return rc;
     // 2-5 K1 fused into 6 K2 (chunked): the prepared q, k, v, g never reach HBM
     if ((rc = k3hip_kda_prefill(T, H, D, K, w->gate_lb, K3HIP_F32, qp, kp, vp, z, bl, w->q_conv,
                                 w->k_conv, w->v_conv, w->A_log, w->dt_bias, cs,
-                                1.0f / sqrtf((float)D), S, o, base + off[9], wsb, stream)))
+                                1.0f / sqrtf((float)D), S, o, base + off[10], wsb, stream)))
         return rc;
-    // 7-8 head RMSNorm, then the gate; y in fp16 (11-bit significand: the o_proj product
-    //   keeps ~3e-4 relative error, inside the prefill tolerance, at bf16 MFMA speed)
+    // 7-8 the output gate's logits in fp16 (only sigmoid(gate) is used: fp16's 2^-11 costs ~0.1
+    //   of the bar, and an overflow to +-inf still gives the right limit 1 or 0), head RMSNorm,
+    //   then the gate; y in fp16 (RMS-normalised: |y| <= sqrt(D) max|o_norm|)
+    if (own) {
+        if ((rc = mm(T, (int)P, E, K3HIP_BF16, xb, E, w->g, E, g16, K3_DT_F16, (long)P, st))) return rc;
+        if ((rc = epilogue_split(T, H, D, w->rms_eps, o, g16, K3_DT_F16, w->o_norm, y16, st, true))) return rc;
+        // 9 o_proj on fp16 MFMA against the fp16 copy of W_o
+        return mm(T, E, (int)P, K3_DT_F16, y16, (long)P, w->o16, (long)P, out, out_dtype, E, st);
+    }
+    float *gl = z;   // the fallback keeps fp32 gate logits; z is consumed by now
+    if ((rc = gemm_bf16(T, (int)P, E, xb, w->g, gl, K3HIP_F32, st))) return rc;
     if ((rc = epilogue_split(T, H, D, w->rms_eps, o, gl, K3HIP_F32, w->o_norm, y16, st, true))) return rc;
-    // 9 o_proj on fp16 MFMA against the fp16 copy of W_o
     if (out_dtype == K3HIP_F32) return gemm_f16(T, E, (int)P, y16, w->o16, out, K3HIP_F32, st);
-    float *o32 = (float *)(base + off[10]);
+    float *o32 = (float *)(base + off[11]);
     if ((rc = gemm_f16(T, E, (int)P, y16, w->o16, o32, K3HIP_F32, st))) return rc;
     const size_t n = (size_t)T * E;
     hipLaunchKernelGGL(to_bf16_kernel, dim3(grid_for(n)), dim3(256), 0, st, o32, (uint16_t *)out, n);
@@ -491,6 +556,8 @@ extern "C" int k3hip_kda_layer_decode(const k3hip_kda_weights *w, int B, float *
     if (!w || !out || !x || !states) K3_FAIL(K3HIP_EINVAL, "k3hip_kda_layer_decode: NULL argument");
     if (B < 0) K3_FAIL(K3HIP_EINVAL, "k3hip_kda_layer_decode: B=%d", B);
     if (B == 0) return K3HIP_OK;
+    if (w->wdt == K3_WBF16 && !(w->parts & K3HIP_UPLOAD_DECODE))
+        K3_FAIL(K3HIP_EINVAL, "k3hip_kda_layer_decode: weights uploaded without K3HIP_UPLOAD_DECODE");
     if (w->wdt != K3_WBF16 || !w->xin_f)
         K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_layer_decode: bf16 weights with hidden and head dim multiples "
                                     "of 8 only (use k3hip_kda_layer_dev)");
@@ -570,8 +637,11 @@ extern "C" void k3_kda_layer(float *out, const float *x, const K3KdaW *w, const 
     const int E = c->hidden, H = c->kda_heads, D = c->kda_head_dim, K = c->conv_k;
     const size_t P = (size_t)H * D;
     const size_t nstate = P * D + 3 * P * (size_t)(K - 1);
+    g_dropin_h2d = g_dropin_d2h = 0;
+    g_in_dropin = true;
+    // only what k3hip_kda_layer_dev reads: the matrices in their own storage and the vectors
     k3hip_kda_weights *dw = nullptr;
-    if (k3hip_kda_upload(w, c, &dw)) fatal("k3_kda_layer (weight upload)");
+    if (k3hip_kda_upload_ex(w, c, K3HIP_UPLOAD_DEV, &dw)) fatal("k3_kda_layer (weight upload)");
     float *dx = nullptr, *dout = nullptr, *dst = nullptr;
     const size_t xb = (size_t)T * E * sizeof(float);
     if (hipMalloc((void **)&dx, xb) != hipSuccess || hipMalloc((void **)&dout, xb) != hipSuccess ||
@@ -584,12 +654,15 @@ extern "C" void k3_kda_layer(float *out, const float *x, const K3KdaW *w, const 
         set_error("host-to-device copy failed");
         fatal("k3_kda_layer");
     }
+    g_dropin_h2d += xb + (state ? nstate * 4 : 0);
     if (k3hip_kda_layer_dev(dw, T, dout, dx, dst, nullptr)) fatal("k3_kda_layer");
     if (hipMemcpy(out, dout, xb, hipMemcpyDeviceToHost) != hipSuccess ||
         (state && hipMemcpy(state, dst, nstate * 4, hipMemcpyDeviceToHost) != hipSuccess)) {
         set_error("device-to-host copy failed: %s", hipGetErrorString(hipGetLastError()));
         fatal("k3_kda_layer");
     }
+    g_dropin_d2h += xb + (state ? nstate * 4 : 0);
+    g_in_dropin = false;
     (void)hipFree(dx);
     (void)hipFree(dout);
     if (dst) (void)hipFree(dst);

@@ -353,7 +353,7 @@ extern "C" int k3hip_mla_decode(const k3hip_mla_weights *w, int B, int pos, int 
         gs.M = H; gs.N = Tn; gs.K = CW; gs.ab_dtype = K3HIP_F32; gs.c_dtype = K3HIP_F32; gs.b_trans = true;
         gs.lda = CW; gs.ldb = CW; gs.ldc = Tn; gs.batch = B;
         gs.sa = (long)H * CW; gs.sb = (long)cap * CW; gs.sc = (long)H * Tn;
-        gs.tune = false;   // a new length every step: take the heuristic's first choice
+        gs.cache = false;   // a new length every step: no plan kept
         if ((rc = gemm(gs, qcat, cache, S, st))) return rc;
         {
             const float scale = 1.0f / sqrtf((float)QH);
@@ -370,7 +370,7 @@ extern "C" int k3hip_mla_decode(const k3hip_mla_weights *w, int B, int pos, int 
         gp.M = H; gp.N = KL; gp.K = Tn; gp.ab_dtype = K3HIP_F32; gp.c_dtype = K3HIP_F32; gp.b_trans = false;
         gp.lda = Tn; gp.ldb = CW; gp.ldc = KL; gp.batch = B;
         gp.sa = (long)H * Tn; gp.sb = (long)cap * CW; gp.sc = (long)H * KL;
-        gp.tune = false;
+        gp.cache = false;
         if ((rc = gemm(gp, S, cache, chat, st))) return rc;
         if ((rc = split_rows2(chat, ch2, B, H * KL, st))) return rc;
     }

@@ -1,0 +1,319 @@
+// SPDX-License-Identifier: Apache-2.0
+// kda_mm.hip - the layer's projections as hand-written gfx950 MFMA GEMMs.
+//
+// Replaces the reference's per-token k3_mmw calls (include/k3/k3.h:290-296 ->
+// k3_matmul_bf16, src/core/k3_ops.c:1122-1227; call sites :879-886, :946, :948) for a
+// T-token prefill: every projection of a token is a row of one GEMM over all T tokens,
+//   C[M][N] = A[M][K] . B[N][K]^T      A = activations, B = the weight as stored (row n of
+//                                      the reference's [out][in] matrix), both K-contiguous
+// with bf16 or fp16 operands and fp32 accumulation.
+//
+// Workgroup tile 256 x 256, K in steps of 64, four waves in a 2 x 2 grid; each wave owns a
+// 128 x 128 block = 4 x 4 v_mfma_f32_32x32x16 tiles (256 accumulator registers, one wave per
+// SIMD). Per K-step the workgroup stages A[256][64] and B[256][64] (64 KiB) in LDS, double
+// buffered (128 KiB): each thread loads its 16-byte pieces of step ks+2 into registers while
+// step ks computes and writes them to the other LDS buffer during step ks+1. One barrier per
+// step, placed before the step's last 16-wide substep so the first fragments of the next
+// step load under that substep's MFMAs. Fragment reads are 16 bytes per lane; rows are 128
+// bytes and the 16-byte chunk index is XORed with (row & 7) ^ ((row >> 3) & 1), which keeps
+// every 16-lane group of a fragment read on distinct banks (no LDS bank conflicts, counter-
+// verified). The steady-state loop body is branch-free so the interleave hints (one MFMA,
+// one LDS read / LDS write / global load) apply to all of it.
+//
+// Tile order is XCD-aware: workgroup b runs on XCD b % 8, and consecutive tile ids (groups
+// of 8 M-tiles walked along N) are given to the same XCD, so the tiles running together on
+// one XCD share A rows and B rows through that XCD's L2.
+//
+// Split-K: for shapes with fewer tiles than compute units (the narrow f_a / b projection),
+// S workgroups per tile each take K/S and write fp32 partial planes P[s][M][N]; the consumer
+// adds them in increasing s, so results are bit-reproducible.
+#include "kda_internal.h"
+
+#include <type_traits>
+
+namespace k3kda {
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int BM = 256, BN = 256, BK = 64, NT = 256;
+constexpr int WM = 128, WN = 128, TI = WM / 32, TJ = WN / 32;
+constexpr int A_BYTES = BM * BK * 2, STAGE = (BM + BN) * BK * 2;
+constexpr int NL = (BM + BN) * (BK / 8) / NT;   // 16-byte pieces per thread per K-step
+constexpr int S = BK / 16;                       // 16-wide substeps per K-step
+constexpr int LDS_BYTES = 2 * STAGE;
+
+enum { OUT_F32 = 0, OUT_F16 = 1, OUT_BF16 = 2, OUT_PART = 3 };
+
+__device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+
+template <int AB>
+__device__ __forceinline__ f32x16 mfma(const u32x4 &a, const u32x4 &b, f32x16 c)
+{
+    if constexpr (AB == K3_DT_F16)
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                      0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                       0, 0, 0);
+}
+
+// Tile (tm, tn) and K-split s of workgroup b, XCD-aware grouped order.
+__device__ __forceinline__ void tile_of(int b, int nb, int tiles_m, int tiles_n, int splits, int &tm, int &tn, int &s)
+{
+    const int per = nb / 8, rem = nb % 8, x = b % 8, i = b / 8;
+    const int L = x * per + (x < rem ? x : rem) + i;
+    s = L % splits;
+    const int t = L / splits;
+    constexpr int GM = 8;
+    const int per_group = GM * tiles_n;
+    const int g = t / per_group, first_m = g * GM;
+    const int gsz = tiles_m - first_m < GM ? tiles_m - first_m : GM;
+    tm = first_m + (t % per_group) % gsz;
+    tn = (t % per_group) / gsz;
+}
+
+template <int AB, int OUT>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void mm_kernel(
+    int M, int N, int K, const uint16_t *__restrict__ A, long lda, const uint16_t *__restrict__ B, long ldb,
+    void *__restrict__ Cv, long ldc, int gcols, long gstride, int tiles_m, int tiles_n, int splits)
+{
+    extern __shared__ __attribute__((aligned(1024))) char smem[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    int tm, tn, sp;
+    tile_of(blockIdx.x, gridDim.x, tiles_m, tiles_n, splits, tm, tn, sp);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int nks = K / BK / splits, k_first = sp * nks * BK;
+
+    // this thread's 16-byte pieces: global row pointer (rows past M or N clamped to the last
+    // one: loaded, never stored) and LDS offset within a stage
+    const uint16_t *src[NL];
+    int ldo[NL];
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+        const int idx = i * NT + tid, row = idx >> 3, c = idx & 7;
+        if (row < BM) {
+            const int r = min(m0 + row, M - 1);
+            src[i] = A + (long)r * lda + k_first + c * 8;
+        } else {
+            const int r = min(n0 + row - BM, N - 1);
+            src[i] = B + (long)r * ldb + k_first + c * 8;
+        }
+        ldo[i] = row * 128 + ((c ^ swz(row)) << 4);
+    }
+    u32x4 stg[NL];
+    f32x16 acc[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; i++)
+#pragma unroll
+        for (int j = 0; j < TJ; j++) acc[i][j] = f32x16{};
+
+    // prologue: step 0 into LDS buffer 0, step 1 into registers
+#pragma unroll
+    for (int i = 0; i < NL; i++) stg[i] = *reinterpret_cast<const u32x4 *>(src[i]);
+#pragma unroll
+    for (int i = 0; i < NL; i++) *reinterpret_cast<u32x4 *>(smem + ldo[i]) = stg[i];
+    if (nks > 1) {
+#pragma unroll
+        for (int i = 0; i < NL; i++) stg[i] = *reinterpret_cast<const u32x4 *>(src[i] + BK);
+    }
+    __syncthreads();
+
+    const int r32 = lane & 31, kh = lane >> 5, sw = swz(r32);   // fragment rows start at multiples of 32
+    int aoff[TI], boff[TJ];
+#pragma unroll
+    for (int i = 0; i < TI; i++) aoff[i] = (wm * WM + i * 32 + r32) * 128;
+#pragma unroll
+    for (int j = 0; j < TJ; j++) boff[j] = A_BYTES + (wn * WN + j * 32 + r32) * 128;
+    u32x4 a[2][TI], b[2][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; i++) a[0][i] = *reinterpret_cast<const u32x4 *>(smem + aoff[i] + ((kh ^ sw) << 4));
+#pragma unroll
+    for (int j = 0; j < TJ; j++) b[0][j] = *reinterpret_cast<const u32x4 *>(smem + boff[j] + ((kh ^ sw) << 4));
+
+    // one K-step; NEXT: a step ks+1 exists (in registers), LOAD2: fetch step ks+2
+    auto step = [&](int ks, auto next_c, auto load2_c) {
+        constexpr bool NEXT = decltype(next_c)::value, LOAD2 = decltype(load2_c)::value;
+        const char *sa = smem + (ks & 1) * STAGE;
+        char *sn = smem + ((ks + 1) & 1) * STAGE;
+        constexpr int HALF = NL / 2;
+#pragma unroll
+        for (int s = 0; s < S; s++) {
+            const int cur = s & 1, nx = cur ^ 1;
+            if (NEXT && s < 2) {
+#pragma unroll
+                for (int i = s * HALF; i < (s + 1) * HALF; i++) {
+                    *reinterpret_cast<u32x4 *>(sn + ldo[i]) = stg[i];
+                    if (LOAD2) stg[i] = *reinterpret_cast<const u32x4 *>(src[i] + (long)(ks + 2) * BK);
+                }
+            }
+            if (s + 1 < S) {
+                const int c = 2 * (s + 1) + kh;
+#pragma unroll
+                for (int i = 0; i < TI; i++) a[nx][i] = *reinterpret_cast<const u32x4 *>(sa + aoff[i] + ((c ^ sw) << 4));
+#pragma unroll
+                for (int j = 0; j < TJ; j++) b[nx][j] = *reinterpret_cast<const u32x4 *>(sa + boff[j] + ((c ^ sw) << 4));
+            } else if (NEXT) {
+                // every read of this step is in registers; step ks+1 is in LDS once all waves
+                // pass this barrier
+                __syncthreads();
+#pragma unroll
+                for (int i = 0; i < TI; i++) a[nx][i] = *reinterpret_cast<const u32x4 *>(sn + aoff[i] + ((kh ^ sw) << 4));
+#pragma unroll
+                for (int j = 0; j < TJ; j++) b[nx][j] = *reinterpret_cast<const u32x4 *>(sn + boff[j] + ((kh ^ sw) << 4));
+            }
+#pragma unroll
+            for (int i = 0; i < TI; i++)
+#pragma unroll
+                for (int j = 0; j < TJ; j++) acc[i][j] = mfma<AB>(a[cur][i], b[cur][j], acc[i][j]);
+            if (s + 1 < S || NEXT) {
+#pragma unroll
+                for (int q = 0; q < TI + TJ; q++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // LDS read
+                }
+            }
+            if (NEXT && s < 2) {
+#pragma unroll
+                for (int q = 0; q < HALF; q++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);   // LDS write
+                    if (LOAD2) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // global load
+                }
+            }
+        }
+    };
+    int ks = 0;
+    for (; ks + 2 < nks; ks++) step(ks, std::true_type{}, std::true_type{});
+    if (ks + 1 < nks) step(ks++, std::true_type{}, std::false_type{});
+    step(ks, std::false_type{}, std::false_type{});
+
+    // epilogue: lane holds column r32 of each 32 x 32 tile, rows (r & 3) + 8 (r >> 2) + 4 kh
+#pragma unroll
+    for (int i = 0; i < TI; i++)
+#pragma unroll
+        for (int j = 0; j < TJ; j++) {
+            const int col = n0 + wn * WN + j * 32 + r32;
+            if (col >= N) continue;
+            // column groups: columns [g*gcols, (g+1)*gcols) go to the matrix at C + g*gstride
+            const int g = col / gcols;
+            const long cbase = g * gstride + (col - g * gcols);
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int row = m0 + wm * WM + i * 32 + (r & 3) + 8 * (r >> 2) + 4 * kh;
+                if (row >= M) continue;
+                const float v = acc[i][j][r];
+                if constexpr (OUT == OUT_F32) {
+                    reinterpret_cast<float *>(Cv)[(long)row * ldc + cbase] = v;
+                } else if constexpr (OUT == OUT_F16) {
+                    reinterpret_cast<_Float16 *>(Cv)[(long)row * ldc + cbase] = (_Float16)v;
+                } else if constexpr (OUT == OUT_BF16) {
+                    reinterpret_cast<uint16_t *>(Cv)[(long)row * ldc + cbase] = f2bf(v);
+                } else {
+                    reinterpret_cast<float *>(Cv)[((long)sp * M + row) * N + col] = v;
+                }
+            }
+        }
+}
+
+template <int AB, int OUT>
+int launch_mm(int M, int N, int K, const void *A, long lda, const void *B, long ldb, void *C, long ldc, int gcols,
+              long gstride, int splits, hipStream_t st)
+{
+    static bool lds_ok[64];
+    int dev = 0;
+    K3_HIP(hipGetDevice(&dev));
+    if (dev >= 0 && dev < 64 && !lds_ok[dev]) {
+        K3_HIP(hipFuncSetAttribute((const void *)mm_kernel<AB, OUT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   LDS_BYTES));
+        lds_ok[dev] = true;
+    }
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    const long grid = (long)tiles_m * tiles_n * splits;
+    if (grid > 0x7fffffffL) K3_FAIL(K3HIP_EUNSUPPORTED, "mm: %dx%d output needs too many workgroups", M, N);
+    hipLaunchKernelGGL((mm_kernel<AB, OUT>), dim3((unsigned)grid), dim3(NT), LDS_BYTES, st, M, N, K,
+                       (const uint16_t *)A, lda, (const uint16_t *)B, ldb, C, ldc, gcols, gstride, tiles_m, tiles_n,
+                       splits);
+    K3_LAUNCHED();
+    return K3HIP_OK;
+}
+
+int check_shape(const char *who, int M, int N, int K, int ab, const void *A, long lda, const void *B, long ldb)
+{
+    if (ab != K3HIP_BF16 && ab != K3_DT_F16) K3_FAIL(K3HIP_EINVAL, "%s: operand dtype %d", who, ab);
+    if (K % BK || (lda & 7) || (ldb & 7) || ((uintptr_t)A & 15) || ((uintptr_t)B & 15) || lda < K || ldb < K)
+        K3_FAIL(K3HIP_EUNSUPPORTED, "%s: K=%d (a multiple of %d), lda=%ld ldb=%ld (multiples of 8), 16-byte "
+                "aligned operands needed", who, K, BK, lda, ldb);
+    return K3HIP_OK;
+}
+
+}  // namespace
+
+bool mm_supported(int K, long lda, long ldb) { return K > 0 && K % BK == 0 && !(lda & 7) && !(ldb & 7); }
+
+int mm(int M, int N, int K, int ab, const void *A, long lda, const void *B, long ldb, void *C, int out, long ldc,
+       hipStream_t st, int gcols, long gstride)
+{
+    if (M <= 0 || N <= 0) return K3HIP_OK;
+    int rc;
+    if ((rc = check_shape("mm", M, N, K, ab, A, lda, B, ldb))) return rc;
+    if (gcols <= 0) {
+        gcols = N;
+        gstride = 0;
+    }
+#define K3_MM(AB_, OUT_) launch_mm<AB_, OUT_>(M, N, K, A, lda, B, ldb, C, ldc, gcols, gstride, 1, st)
+    if (ab == K3HIP_BF16) {
+        if (out == K3HIP_F32) return K3_MM(K3HIP_BF16, OUT_F32);
+        if (out == K3_DT_F16) return K3_MM(K3HIP_BF16, OUT_F16);
+        if (out == K3HIP_BF16) return K3_MM(K3HIP_BF16, OUT_BF16);
+    } else {
+        if (out == K3HIP_F32) return K3_MM(K3_DT_F16, OUT_F32);
+        if (out == K3_DT_F16) return K3_MM(K3_DT_F16, OUT_F16);
+        if (out == K3HIP_BF16) return K3_MM(K3_DT_F16, OUT_BF16);
+    }
+#undef K3_MM
+    K3_FAIL(K3HIP_EINVAL, "mm: output dtype %d", out);
+}
+
+int mm_splits(int M, int N, int K, int ncu)
+{
+    const long tiles = (long)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    const int steps = K / BK;
+    int s = 1;
+    // split while the grid is short of the CUs and each split keeps at least 8 K-steps
+    while (tiles * s * 2 <= ncu && steps % (s * 2) == 0 && steps / (s * 2) >= 8) s *= 2;
+    return s;
+}
+
+int mm_splitk(int M, int N, int K, int splits, int ab, const void *A, long lda, const void *B, long ldb, float *P,
+              hipStream_t st)
+{
+    if (M <= 0 || N <= 0) return K3HIP_OK;
+    int rc;
+    if ((rc = check_shape("mm_splitk", M, N, K, ab, A, lda, B, ldb))) return rc;
+    if (splits < 1 || (K / BK) % splits) K3_FAIL(K3HIP_EINVAL, "mm_splitk: %d splits of K=%d", splits, K);
+    if (ab == K3HIP_BF16) return launch_mm<K3HIP_BF16, OUT_PART>(M, N, K, A, lda, B, ldb, P, N, N, 0, splits, st);
+    return launch_mm<K3_DT_F16, OUT_PART>(M, N, K, A, lda, B, ldb, P, N, N, 0, splits, st);
+}
+
+}  // namespace k3kda
+
+using namespace k3kda;
+
+extern "C" int k3hip_proj_gemm(int M, int N, int K, int ab_dtype, const void *A, long lda, const void *B, long ldb,
+                               void *C, int c_dtype, long ldc, void *stream)
+{
+    clear_error();
+    if (M < 0 || N < 0 || K <= 0 || (M && N && (!A || !B || !C)) || ldc < N)
+        K3_FAIL(K3HIP_EINVAL, "k3hip_proj_gemm: M=%d N=%d K=%d ldc=%ld or NULL operand", M, N, K, ldc);
+    if (ab_dtype != K3HIP_BF16 && ab_dtype != K3HIP_F16)
+        K3_FAIL(K3HIP_EINVAL, "k3hip_proj_gemm: ab_dtype=%d (bf16 or fp16)", ab_dtype);
+    if (c_dtype != K3HIP_F32 && c_dtype != K3HIP_BF16 && c_dtype != K3HIP_F16)
+        K3_FAIL(K3HIP_EINVAL, "k3hip_proj_gemm: c_dtype=%d", c_dtype);
+    return mm(M, N, K, ab_dtype, A, lda, B, ldb, C, c_dtype, ldc, as_stream(stream));
+}

@@ -18,7 +18,8 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libk3kda_hip.so"
 
 K3_WF32, K3_WBF16, K3_WI8 = 0, 1, 2
-F32, BF16 = 0, 1
+F32, BF16, F16 = 0, 1, 3
+UPLOAD_DEV, UPLOAD_PREFILL, UPLOAD_DECODE, UPLOAD_ALL = 1, 2, 4, 7
 OK, EINVAL, EHIP, EUNSUPPORTED, ENOMEM = 0, 1, 2, 3, 4
 
 EXPORTS = (
@@ -30,7 +31,8 @@ EXPORTS = (
     "k3hip_kda_states_layer", "k3hip_kda_states_zero", "k3hip_kda_states_copy",
     "k3hip_kda_states_download", "k3hip_kda_states_upload",
     "k3hip_mla_upload", "k3hip_mla_release", "k3hip_mla_cache_floats", "k3hip_mla_decode",
-    "k3hip_kda_layer_decode",
+    "k3hip_kda_layer_decode", "k3hip_kda_upload_ex", "k3hip_kda_weights_bytes",
+    "k3hip_kda_dropin_bytes", "k3hip_proj_gemm",
 )
 
 
@@ -128,6 +130,10 @@ def lib() -> C.CDLL:
         "k3hip_mla_cache_floats": (sz, [C.POINTER(K3Cfg), i]),
         "k3hip_mla_decode": (i, [_P, i, i, i, _P, _P, _P, _P]),
         "k3hip_kda_layer_decode": (i, [_P, i, _P, _P, _P, C.c_long, _P]),
+        "k3hip_kda_upload_ex": (i, [C.POINTER(K3KdaW), C.POINTER(K3Cfg), i, C.POINTER(_P)]),
+        "k3hip_kda_weights_bytes": (sz, [_P]),
+        "k3hip_kda_dropin_bytes": (sz, []),
+        "k3hip_proj_gemm": (i, [i, i, i, i, _P, C.c_long, _P, C.c_long, _P, i, C.c_long, _P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -172,7 +178,22 @@ def _dt(t) -> int:
         return F32
     if t.dtype == torch.bfloat16:
         return BF16
-    raise ValueError(f"k3kda: dtype {t.dtype} not supported (float32 or bfloat16)")
+    if t.dtype == torch.float16:
+        return F16
+    raise ValueError(f"k3kda: dtype {t.dtype} not supported (float32, bfloat16 or float16)")
+
+
+def proj_gemm(a, b, c, stream=None) -> None:
+    """c[M,N] = a[M,K] . b[N,K]^T on the hand-written MFMA GEMM (a, b bf16 or fp16 alike;
+    c float32, bfloat16 or float16). Row strides are taken from the tensors."""
+    M, K = a.shape
+    N = b.shape[0]
+    for t in (a, b, c):
+        if not t.is_cuda or t.stride(-1) != 1:
+            raise ValueError("k3kda.proj_gemm: device tensors with unit column stride required")
+    _check(lib().k3hip_proj_gemm(M, N, K, _dt(a), C.c_void_p(a.data_ptr()), a.stride(0),
+                                 C.c_void_p(b.data_ptr()), b.stride(0), C.c_void_p(c.data_ptr()),
+                                 _dt(c), c.stride(0), _stream(stream)))
 
 
 def kda_decode(S, o, q, k, v, alpha, beta, q_scale: float, stream=None) -> None:
@@ -239,9 +260,13 @@ def kda_epilogue(o, gate, o_norm, y, H: int, D: int, rms_eps: float, stream=None
 class DeviceWeights:
     """k3hip_kda_upload / k3hip_kda_release around a K3KdaW of host pointers."""
 
-    def __init__(self, w: K3KdaW, cfg: K3Cfg):
+    def __init__(self, w: K3KdaW, cfg: K3Cfg, parts: int = UPLOAD_ALL):
         self.handle = C.c_void_p()
-        _check(lib().k3hip_kda_upload(C.byref(w), C.byref(cfg), C.byref(self.handle)))
+        _check(lib().k3hip_kda_upload_ex(C.byref(w), C.byref(cfg), parts, C.byref(self.handle)))
+
+    def nbytes(self) -> int:
+        """Device bytes the uploaded weight set holds."""
+        return int(lib().k3hip_kda_weights_bytes(self.handle))
 
     def layer(self, out, x, state, T: int, stream=None) -> None:
         _check(lib().k3hip_kda_layer_dev(self.handle, T, _ptr(out), _ptr(x), _ptr(state),
@@ -344,6 +369,11 @@ class MlaWeights:
             self.close()
         except Exception:
             pass
+
+
+def dropin_bytes() -> int:
+    """Host<->device bytes of the calling thread's last k3_kda_layer call."""
+    return int(lib().k3hip_kda_dropin_bytes())
 
 
 def kda_layer_host(out, x, w: K3KdaW, cfg: K3Cfg, T: int, state=None) -> None:

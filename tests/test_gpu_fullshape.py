@@ -1,0 +1,157 @@
+# SPDX-License-Identifier: Apache-2.0
+"""The benchmarked shapes under a check, the way the reference's scale_test runs one KDA
+layer at real dimensions (tests/unit/scale_test.c:161-208) because small shapes hide
+grid-size, indexing and overflow mistakes.
+
+1. The prefill core (k3hip_kda_prefill + k3hip_kda_epilogue) at H=32, D=128, T=8192 with bf16
+   conv inputs -- the exact launch shape of the benchmark (4096 phase-1 items over the
+   persistent grid, 256 phase-2 workgroups with the XCD mapping) -- against the oracle's
+   orc_kda_core on the same bf16-rounded inputs, at the chunked bar 2e-3.
+2. The bf16 full layer (k3hip_kda_layer_prefill: hand-written MFMA projections, fused core,
+   epilogue, o_proj) at hidden 4096, H=32, D=128, two prefills with the state carried,
+   against the oracle's k3_kda_layer on the same bf16 weights, at the chunked bar.
+3. The batched decode layer (k3hip_kda_layer_decode) at hidden 7168, H=32, D=128 for B=16
+   sequences (the hybrid slice's KDA layer), against the oracle's k3_kda_layer per
+   sequence, at the decode bar 1e-4, two steps.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import assert_close, worst_ratio
+from test_oracle_ref import bf16
+from test_gpu_layer_prefill import layer_weights, bf16_to_f32
+import k3_oracle as ko
+from k3_oracle import f32
+
+pytestmark = pytest.mark.gpu
+
+
+def rms(a):
+    return float(np.sqrt(np.mean(np.asarray(a, np.float64) ** 2)))
+
+
+def test_core_at_benchmark_shape(gpu):
+    import torch
+    H, D, T, K, LB, EPS = 32, 128, 8192, 4, -5.0, 1e-5
+    P = H * D
+    g = torch.Generator(device="cuda").manual_seed(0x4B334441 + 2)
+    bf = torch.bfloat16
+    q_in, k_in, v_in = (torch.randn((T, P), device="cuda", generator=g).to(bf) for _ in range(3))
+    z = torch.randn((T, P), device="cuda", generator=g) * 0.02
+    b_logit = torch.randn((T, H), device="cuda", generator=g)
+    gate = torch.randn((T, P), device="cuda", generator=g).to(bf)
+    conv = [torch.randn((P, K), device="cuda", generator=g) * 0.5 for _ in range(3)]
+    A_log = torch.rand((H,), device="cuda", generator=g) * 1.5
+    dt_bias = torch.randn((P,), device="cuda", generator=g)
+    o_norm = 1 + 0.1 * torch.randn((D,), device="cuda", generator=g)
+    S = torch.zeros((H, D, D), device="cuda")
+    cs = torch.zeros(3 * P * (K - 1), device="cuda")
+    o = torch.full((T, P), float("nan"), device="cuda")
+    y = torch.full((T, P), float("nan"), device="cuda")
+    ws = torch.empty(gpu.kda_chunk_workspace(T, H, D), dtype=torch.uint8, device="cuda")
+    qs = float(np.float32(1) / np.sqrt(np.float32(D)))
+    gpu.kda_prefill(q_in, k_in, v_in, z, b_logit, *conv, A_log, dt_bias, cs, S, o, H, D, K, LB, qs, ws)
+    gpu.kda_epilogue(o, gate, o_norm, y, H, D, EPS)
+    torch.cuda.synchronize()
+    h = lambda t: t.float().cpu().numpy()
+    arrays = {"q_conv": h(conv[0]), "k_conv": h(conv[1]), "v_conv": h(conv[2]), "A_log": h(A_log),
+              "dt_bias": h(dt_bias), "o_norm": h(o_norm)}
+    for n in ("q", "k", "v", "g", "f_a", "f_b", "b", "o"):
+        arrays[n] = np.zeros((1, 1), np.float32)
+    W = ko.Weights(arrays, 0)
+    cfg = ko.make_cfg(4096, H, D, K, LB, EPS)
+    st = np.zeros(P * D + 3 * P * (K - 1), np.float32)
+    want = ko.core(h(q_in), h(k_in), h(v_in), h(z), h(b_logit), h(gate), W, cfg, T, st, nthreads=16)
+    got, gS = h(y), h(S)
+    ry = assert_close(got, want, 2e-3 * rms(want), 2e-3, "core y at T=8192")
+    rs = assert_close(gS.ravel(), st[:P * D], 2e-3 * rms(st[:P * D]), 2e-3, "core S at T=8192")
+    t4 = worst_ratio(got, want, 1e-4 * rms(want), 1e-4)
+    print(f"c2 core H={H} D={D} T={T}: worst {ry:.4f}x (y) / {rs:.4f}x (S) of the 2e-3 bar, {t4:.3f}x of 1e-4")
+
+
+def test_layer_prefill_at_benchmark_width(gpu):
+    import torch
+    hidden, H, D, K = 4096, 32, 128, 4
+    rng = np.random.default_rng(0x4B334441 + 22)
+    W = layer_weights(rng, hidden, H, D, K)
+    cfg = ko.make_cfg(hidden, H, D, K, -5.0, 1e-5)
+    P = H * D
+    nst = P * D + 3 * P * (K - 1)
+    st_ref = np.zeros(nst, np.float32)
+    dw = gpu.DeviceWeights(W.w, cfg, gpu.UPLOAD_DEV | gpu.UPLOAD_PREFILL)
+    dst = torch.zeros(nst, device="cuda")
+    for i, T in enumerate((160, 64)):
+        x = bf16_to_f32(bf16(rng.standard_normal((T, hidden))))
+        want = ko.kda_layer(ko.orc(), x, W, cfg, T, st_ref)
+        out = torch.full((T, hidden), float("nan"), device="cuda")
+        dw.layer_prefill(out, torch.from_numpy(x).cuda().to(torch.bfloat16), dst, T)
+        torch.cuda.synchronize()
+        got, gst = out.cpu().numpy(), dst.cpu().numpy()
+        ro = assert_close(got, want, 2e-3 * rms(want), 2e-3, f"layer T={T} out")
+        rs = assert_close(gst[:P * D], st_ref[:P * D], 2e-3 * rms(st_ref[:P * D]), 2e-3, f"layer T={T} S")
+        assert_close(gst[P * D:], st_ref[P * D:], 1e-5 * rms(st_ref[P * D:]), 1e-5, f"layer T={T} conv history")
+        print(f"hidden={hidden} H={H} D={D} call {i} T={T}: worst {ro:.3f}x (out) / {rs:.3f}x (S) of the 2e-3 bar")
+    dw.close()
+
+
+def test_layer_decode_at_hybrid_width(gpu):
+    import torch
+    hidden, H, D, K, B = 7168, 32, 128, 4, 16
+    rng = np.random.default_rng(0x4B334441 + 44)
+    W = layer_weights(rng, hidden, H, D, K)
+    cfg = ko.make_cfg(hidden, H, D, K, -5.0, 1e-5)
+    P = H * D
+    kper = P * D + 3 * P * (K - 1)
+    stride = kper + 4
+    init = f32(rng.standard_normal((B, kper)) * 0.05)
+    refs = [init[b].copy() for b in range(B)]
+    dw = gpu.DeviceWeights(W.w, cfg, gpu.UPLOAD_DEV | gpu.UPLOAD_DECODE)
+    states = torch.zeros((B, stride), device="cuda")
+    states[:, :kper] = torch.from_numpy(init).cuda()
+    for step in range(2):
+        x = f32(rng.standard_normal((B, hidden)))
+        want = np.concatenate([ko.kda_layer(ko.orc(), x[b:b + 1], W, cfg, 1, refs[b]) for b in range(B)])
+        out = torch.full((B, hidden), float("nan"), device="cuda")
+        dw.layer_decode(out, torch.from_numpy(x).cuda(), states, stride)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        r = assert_close(got, want, 1e-4 * rms(want), 1e-4, f"decode step {step} out")
+        gs = states[:, :kper].cpu().numpy()
+        for b in range(B):
+            assert_close(gs[b], refs[b], 1e-4 * rms(refs[b]), 1e-4, f"decode step {step} seq {b} state")
+        print(f"hidden={hidden} H={H} D={D} B={B} step {step}: worst {r:.3f}x of the 1e-4 bar")
+    dw.close()
+
+
+def test_upload_parts_and_dropin_bytes(gpu):
+    """Each entry point's weight copies are made only when asked for, and the drop-in
+    k3_kda_layer moves exactly the layer's own weights + x + out + state per call."""
+    import torch
+    hidden, H, D, K, T = 256, 4, 64, 4, 9
+    rng = np.random.default_rng(31)
+    W = layer_weights(rng, hidden, H, D, K)
+    cfg = ko.make_cfg(hidden, H, D, K, -5.0, 1e-5)
+    P = H * D
+    mats = (4 * P * hidden + hidden * P + D * hidden + P * D + H * hidden) * 2
+    vecs = (3 * P * K + H + P + D) * 4
+    dev_only = gpu.DeviceWeights(W.w, cfg, gpu.UPLOAD_DEV)
+    assert dev_only.nbytes() == mats + vecs
+    everything = gpu.DeviceWeights(W.w, cfg)
+    assert everything.nbytes() > 2 * (mats + vecs)
+    x = f32(rng.standard_normal((T, hidden)))
+    with pytest.raises(gpu.K3HipError) as e:
+        dev_only.layer_prefill(torch.zeros((T, hidden), device="cuda"), torch.from_numpy(x).cuda(), None, T)
+    assert e.value.code == 1
+    with pytest.raises(gpu.K3HipError) as e:
+        dev_only.layer_decode(torch.zeros((2, hidden), device="cuda"), torch.zeros((2, hidden), device="cuda"),
+                              torch.zeros((2, P * D + 3 * P * (K - 1)), device="cuda"), P * D + 3 * P * (K - 1))
+    assert e.value.code == 1
+    dev_only.close()
+    everything.close()
+    nst = P * D + 3 * P * (K - 1)
+    st = np.zeros(nst, np.float32)
+    out = np.zeros((T, hidden), np.float32)
+    gpu.kda_layer_host(out, x, W.w, cfg, T, st)
+    assert gpu.dropin_bytes() == mats + vecs + 2 * T * hidden * 4 + 2 * nst * 4

@@ -79,3 +79,73 @@ def test_mla_refusals(gpu):
     with pytest.raises(gpu.K3HipError) as e:
         gpu.MlaWeights(W32.w, cfg)
     assert e.value.code == 3
+
+
+def seeded_caches(rng, W, H, kvl, qn, qr, vh, B, pos, cap, ncache=4):
+    """Positions 0..pos-1 filled with random (rmsnorm-scale) latents and rope slots: the GPU's
+    compressed rows [latent | rope] and the oracle's expanded rows kv_b . latent (float64
+    product rounded to fp32) for the same values; sequence b uses cache b % ncache."""
+    kvb = np.asarray(W.arrays["kv_b"]).astype(np.uint32) << 16
+    kvb = kvb.view(np.float32).astype(np.float64)                 # [H*(qn+vh)][kvl]
+    gcache = np.zeros((B, cap, kvl + qr), np.float32)
+    kvcs, ropecs = [], []
+    base = []
+    for c in range(ncache):
+        L = rng.standard_normal((pos, kvl)).astype(np.float32)
+        R = rng.standard_normal((pos, qr)).astype(np.float32)
+        kv = np.zeros((cap, H * (qn + vh)), np.float32)
+        kv[:pos] = (L.astype(np.float64) @ kvb.T).astype(np.float32)
+        rp = np.zeros((cap, qr), np.float32)
+        rp[:pos] = R
+        base.append((L, R, kv, rp))
+    for b in range(B):
+        L, R, kv, rp = base[b % ncache]
+        gcache[b, :pos, :kvl], gcache[b, :pos, kvl:] = L, R
+        kvcs.append(kv.copy())
+        ropecs.append(rp.copy())
+    return gcache, kvcs, ropecs
+
+
+def run_steps(gpu, rng, W, cfg, hidden, B, gcache, kvcs, ropecs, positions, cap):
+    import torch
+    mw = gpu.MlaWeights(W.w, cfg)
+    cache = torch.from_numpy(gcache).cuda()
+    worst = 0.0
+    for pos in positions:
+        x = rng.standard_normal((B, hidden)).astype(np.float32)
+        want = np.concatenate([ko.mla(x[b:b + 1], W, cfg, 1, kvcs[b], ropecs[b], pos, cap) for b in range(B)])
+        out = torch.full((B, hidden), float("nan"), device="cuda")
+        mw.decode(out, torch.from_numpy(x).cuda(), cache, pos, cap)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        worst = max(worst, assert_close(got, want, 1e-4 * rms(want), 1e-4, f"MLA pos {pos}"))
+    mw.close()
+    return worst
+
+
+def test_mla_fallback_heads_above_64(gpu):
+    """H = 96 (the reference's real MLA head count, src/cli/k3_run.c:105) is outside the fused
+    attention kernel: scores and P . cache as strided-batched fp32 GEMMs around the softmax.
+    Contexts 40, 2100 and 8300 cross its three softmax variants (<= 2048, <= 8192, longer)."""
+    rng = np.random.default_rng(0x4B334441 + 96)
+    hidden, H, ql, kvl, qn, qr, vh, B = 128, 96, 32, 32, 16, 8, 16, 2
+    cfg, W = mla_case(rng, hidden, H, ql, kvl, qn, qr, vh, 1)
+    positions, cap = (40, 2100, 8300), 8304
+    gcache, kvcs, ropecs = seeded_caches(rng, W, H, kvl, qn, qr, vh, B, positions[-1], cap, ncache=2)
+    # positions after the first seeded one are overwritten step by step on both sides
+    w = run_steps(gpu, rng, W, cfg, hidden, B, gcache, kvcs, ropecs, positions, cap)
+    print(f"H=96 fallback: worst {w:.3f}x of the 1e-4 bar")
+
+
+def test_mla_at_hybrid_width(gpu):
+    """The hybrid slice's MLA layer: hidden 7168, 64 heads, q_lora 1536, kv_lora 512, rope 64,
+    nope 128, v 128, B = 16 over ~600 cached positions, so the fused attention splits every
+    sequence into 16 position ranges (ragged, not multiples of its 16-position tile) and the
+    merge combines them."""
+    rng = np.random.default_rng(0x4B334441 + 77)
+    hidden, H, ql, kvl, qn, qr, vh, B = 7168, 64, 1536, 512, 128, 64, 128, 16
+    cfg, W = mla_case(rng, hidden, H, ql, kvl, qn, qr, vh, 1)
+    cap = 640
+    gcache, kvcs, ropecs = seeded_caches(rng, W, H, kvl, qn, qr, vh, B, 597, cap)
+    w = run_steps(gpu, rng, W, cfg, hidden, B, gcache, kvcs, ropecs, (597, 598), cap)
+    print(f"hybrid-width MLA B={B}: worst {w:.3f}x of the 1e-4 bar")
