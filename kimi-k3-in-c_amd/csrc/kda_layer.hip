@@ -450,8 +450,12 @@ extern "C" int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *
     hipStream_t st = as_stream(stream);
     const size_t P = (size_t)H * D, TP = (size_t)T * P;
     const size_t wsb = k3hip_kda_chunk_workspace(T, H, D, 64);
-    // the hand-written GEMM covers K % 64 == 0 (hidden, P and 2D); other widths take hipBLASLt
-    const bool own = mm_supported(E, E, E) && mm_supported((int)P, (long)P, (long)P) && mm_supported(2 * D, 2 * D, 2 * D);
+    // The projections are plain GEMMs and run on hipBLASLt: the hand-written MFMA GEMM
+    // (kda_mm.hip, k3hip_proj_gemm) measures 0.88-0.9x of its speed on these shapes (8192 x
+    // 4096 x 4096: 230 against 207 us; the whole layer 1.96 against 1.75 ms), the gap being
+    // the output write of each tile, which hipBLASLt's persistent stream-K kernels overlap
+    // with the next tile. `own` selects the hand-written kernels for every projection.
+    constexpr bool own = false;
     int ncu = 256, rc;
     if ((rc = cu_count(ncu))) return rc;
     const int fab_s = own ? mm_splits(T, D + H, E, ncu) : 1;
