@@ -271,6 +271,17 @@ int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *out, int ou
 int k3hip_kda_layer_decode(const k3hip_kda_weights *w, int B, float *out, const float *x,
                            float *states, long state_stride, void *stream);
 
+/* k3hip_kda_layer_decode that allocates nothing: for callers that cannot call hipMalloc
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid allocation). No
+ * counterpart in the reference. Same arguments, results bit-identical to
+ * k3hip_kda_layer_decode. Its scratch (projections, split-K partial planes, z, y) is a
+ * fixed 64 MiB device array inside this library, one per GPU, held until the process ends;
+ * a call whose B and layer width need more returns K3HIP_EINVAL (at hidden 7168 with 32 x 128
+ * heads that is beyond about 300 sequences). Every call on one GPU uses that GPU's array:
+ * calls that overlap on one GPU (other streams, other threads) race; serialise them. */
+int k3hip_kda_layer_decode_noalloc(const k3hip_kda_weights *w, int B, float *out, const float *x,
+                                   float *states, long state_stride, void *stream);
+
 /* Device-resident state for a decode loop: the reference's kstate[L * kper] array
  * (src/cli/k3_run.c:514-567), kper = H*D*D + 3*P*(conv_k-1) floats per layer
  * (k3_state_geom, src/cli/k3_state.c:23-29), in the same layout on the device. */

@@ -11,6 +11,7 @@
 //   9 o_proj                                            (:948)
 #include <algorithm>
 #include <math.h>
+#include <mutex>
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -553,30 +554,33 @@ extern "C" int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *
 // ------------------------------------------------------------- batched decode ----
 // One token for each of B sequences: projections on the fragment-ordered decode copies,
 // then the fused K1 + K3 + K4 step kernel, then o_proj. Five launches per layer step.
-extern "C" int k3hip_kda_layer_decode(const k3hip_kda_weights *w, int B, float *out, const float *x,
-                                      float *states, long state_stride, void *stream)
+// The batched decode step with its scratch either allocated per call on the stream (scr ==
+// nullptr) or taken from the caller's scr (scr_bytes, 256-byte aligned). Nothing in the
+// scratch has to start at zero: every element a kernel reads was written earlier in the
+// same call (the projections, the split-K partial planes, z, y).
+static int layer_decode_impl(const k3hip_kda_weights *w, int B, float *out, const float *x, float *states,
+                             long state_stride, void *stream, char *scr, size_t scr_bytes, const char *who)
 {
-    clear_error();
-    if (!w || !out || !x || !states) K3_FAIL(K3HIP_EINVAL, "k3hip_kda_layer_decode: NULL argument");
-    if (B < 0) K3_FAIL(K3HIP_EINVAL, "k3hip_kda_layer_decode: B=%d", B);
+    if (!w || !out || !x || !states) K3_FAIL(K3HIP_EINVAL, "%s: NULL argument", who);
+    if (B < 0) K3_FAIL(K3HIP_EINVAL, "%s: B=%d", who, B);
     if (B == 0) return K3HIP_OK;
     if (w->wdt == K3_WBF16 && !(w->parts & K3HIP_UPLOAD_DECODE))
-        K3_FAIL(K3HIP_EINVAL, "k3hip_kda_layer_decode: weights uploaded without K3HIP_UPLOAD_DECODE");
+        K3_FAIL(K3HIP_EINVAL, "%s: weights uploaded without K3HIP_UPLOAD_DECODE", who);
     if (w->wdt != K3_WBF16 || !w->xin_f)
-        K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_layer_decode: bf16 weights with hidden and head dim multiples "
-                                    "of 8 only (use k3hip_kda_layer_dev)");
+        K3_FAIL(K3HIP_EUNSUPPORTED, "%s: bf16 weights with hidden and head dim multiples "
+                                    "of 8 only (use k3hip_kda_layer_dev)", who);
     const int E = w->hidden, H = w->H, D = w->D, K = w->K;
     const size_t P = (size_t)H * D;
     const long kper = (long)(P * D + 3 * P * (size_t)(K - 1));
     if (!is_pow2_head(D) || K < 1 || K > 4)
-        K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_layer_decode: D=%d conv_k=%d", D, K);
+        K3_FAIL(K3HIP_EUNSUPPORTED, "%s: D=%d conv_k=%d", who, D, K);
     if (state_stride < kper || (state_stride & 3) || ((uintptr_t)states & 15))
-        K3_FAIL(K3HIP_EINVAL, "k3hip_kda_layer_decode: state stride %ld < %ld floats or misaligned",
+        K3_FAIL(K3HIP_EINVAL, "%s: state stride %ld < %ld floats or misaligned", who,
                 state_stride, kper);
     hipStream_t st = as_stream(stream);
     const size_t BP = (size_t)B * P;
     if ((E & 7) || (D & 7) || (P & 7) || ((uintptr_t)x & 15))
-        K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_layer_decode: hidden=%d D=%d need multiples of 8, x 16-byte aligned", E, D);
+        K3_FAIL(K3HIP_EUNSUPPORTED, "%s: hidden=%d D=%d need multiples of 8, x 16-byte aligned", who, E, D);
     // scratch: q k v f_a b projections [B][NI] | output-gate partial planes | z | y |
     //          split-K partials (shared by the projections, which run one after another)
     const int NI = 3 * (int)P + D + H;
@@ -592,9 +596,16 @@ extern "C" int k3hip_kda_layer_decode(const k3hip_kda_weights *w, int B, float *
         total += (sizes[i] + 255) & ~(size_t)255;
     }
     StreamBuf buf;
-    int rc = stream_alloc(buf, total, st);
-    if (rc) return rc;
-    char *bs = (char *)buf.p;
+    int rc;
+    char *bs = scr;
+    if (!scr) {
+        if ((rc = stream_alloc(buf, total, st))) return rc;
+        bs = (char *)buf.p;
+    } else if (total > scr_bytes) {
+        K3_FAIL(K3HIP_EINVAL, "%s: B=%d at hidden %d, %d heads x %d needs %zu bytes of scratch; the no-allocation "
+                "entry point has %zu (use k3hip_kda_layer_decode, or fewer sequences per call)", who, B, E, H, D,
+                total, scr_bytes);
+    }
     float *Cin = (float *)(bs + off[0]), *fa = Cin + 3 * P;
     float *glp = (float *)(bs + off[1]), *Cz = (float *)(bs + off[2]), *y = (float *)(bs + off[3]);
     float *ws = (float *)(bs + off[4]);
@@ -615,6 +626,55 @@ extern "C" int k3hip_kda_layer_decode(const k3hip_kda_weights *w, int B, float *
                          w->A_log, w->dt_bias, w->o_norm, states, state_stride, y, st)))
         return rc;
     return gemm_rows(B, E, (int)P, y, (long)P, Wo, out, E, st, ws, wsf);
+}
+
+extern "C" int k3hip_kda_layer_decode(const k3hip_kda_weights *w, int B, float *out, const float *x,
+                                      float *states, long state_stride, void *stream)
+{
+    clear_error();
+    return layer_decode_impl(w, B, out, x, states, state_stride, stream, nullptr, 0, "k3hip_kda_layer_decode");
+}
+
+// ------------------------------------------------------- no-allocation decode ----
+// Scratch of k3hip_kda_layer_decode_noalloc: a file-scope device array, one copy per GPU,
+// held until the process ends. Host code never passes `noalloc_scratch` itself (on the host
+// it only names the symbol); it takes the array's device address on each device from
+// hipGetSymbolAddress, once, with that device current, and passes that address on.
+constexpr size_t NOALLOC_SCRATCH_BYTES = 64ull << 20;
+static __device__ __align__(256) char noalloc_scratch[NOALLOC_SCRATCH_BYTES];
+
+static constexpr int NOALLOC_MAX_DEV = 64;
+static std::mutex g_noalloc_mu;
+static char *g_noalloc_ptr[NOALLOC_MAX_DEV];
+
+static int noalloc_scratch_ptr(char **out)
+{
+    int dev = 0;
+    K3_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= NOALLOC_MAX_DEV) K3_FAIL(K3HIP_EUNSUPPORTED, "no-allocation scratch: device %d", dev);
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (!g_noalloc_ptr[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(noalloc_scratch));
+        if (e != hipSuccess || !p) {
+            (void)hipGetLastError();
+            K3_FAIL(K3HIP_EHIP, "hipGetSymbolAddress(noalloc_scratch) on device %d: %s", dev, hipGetErrorString(e));
+        }
+        g_noalloc_ptr[dev] = (char *)p;
+    }
+    *out = g_noalloc_ptr[dev];
+    return K3HIP_OK;
+}
+
+extern "C" int k3hip_kda_layer_decode_noalloc(const k3hip_kda_weights *w, int B, float *out, const float *x,
+                                              float *states, long state_stride, void *stream)
+{
+    clear_error();
+    char *scr = nullptr;
+    int rc;
+    if ((rc = noalloc_scratch_ptr(&scr))) return rc;
+    return layer_decode_impl(w, B, out, x, states, state_stride, stream, scr, NOALLOC_SCRATCH_BYTES,
+                             "k3hip_kda_layer_decode_noalloc");
 }
 
 // ------------------------------------------------------------------ drop-in ----

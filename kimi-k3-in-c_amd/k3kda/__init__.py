@@ -32,7 +32,7 @@ EXPORTS = (
     "k3hip_kda_states_download", "k3hip_kda_states_upload",
     "k3hip_mla_upload", "k3hip_mla_release", "k3hip_mla_cache_floats", "k3hip_mla_decode",
     "k3hip_kda_layer_decode", "k3hip_kda_upload_ex", "k3hip_kda_weights_bytes",
-    "k3hip_kda_dropin_bytes", "k3hip_proj_gemm",
+    "k3hip_kda_dropin_bytes", "k3hip_proj_gemm", "k3hip_kda_layer_decode_noalloc",
 )
 
 
@@ -134,6 +134,7 @@ def lib() -> C.CDLL:
         "k3hip_kda_weights_bytes": (sz, [_P]),
         "k3hip_kda_dropin_bytes": (sz, []),
         "k3hip_proj_gemm": (i, [i, i, i, i, _P, C.c_long, _P, C.c_long, _P, i, C.c_long, _P]),
+        "k3hip_kda_layer_decode_noalloc": (i, [_P, i, _P, _P, _P, C.c_long, _P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -276,6 +277,11 @@ class DeviceWeights:
         """One token for each of B = x.shape[0] sequences; states: B slots `stride` floats apart."""
         _check(lib().k3hip_kda_layer_decode(self.handle, x.shape[0], _ptr(out), _ptr(x),
                                             _ptr(states), stride, _stream(stream)))
+
+    def layer_decode_noalloc(self, out, x, states, stride: int, stream=None) -> None:
+        """k3hip_kda_layer_decode_noalloc: the same step on the library's fixed scratch."""
+        _check(lib().k3hip_kda_layer_decode_noalloc(self.handle, x.shape[0], _ptr(out), _ptr(x),
+                                                    _ptr(states), stride, _stream(stream)))
 
     def layer_prefill(self, out, x, state, T: int, stream=None) -> None:
         """bf16 full-layer prefill: x, out [T, hidden] float32 or bfloat16 tensors."""
