@@ -22,6 +22,7 @@ import argparse
 import json
 import math
 import os
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -68,19 +69,48 @@ def prefill_core_bytes_per_token(H: int, D: int) -> int:
 
 
 def cpu_info() -> dict:
-    model, cores = "unknown", os.cpu_count() or 1
+    """The host CPU: lscpu model, physical cores (all, and those in this process's CPU
+    affinity share), and the OpenMP threads the baselines use: one per physical core of the
+    share, as the reference sizes its pool (src/cli/k3_run.c:1096-1106), capped by
+    OMP_NUM_THREADS when the environment sets it."""
+    model = "unknown"
     try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
                 model = line.split(":", 1)[1].strip()
-                break
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        allowed = sorted(os.sched_getaffinity(0))
+    except AttributeError:
+        allowed = list(range(os.cpu_count() or 1))
+
+    def core_of(cpu):
+        base = Path(f"/sys/devices/system/cpu/cpu{cpu}/topology")
+        try:
+            return (base / "physical_package_id").read_text().strip(), (base / "core_id").read_text().strip()
+        except OSError:
+            return ("cpu", str(cpu))
+    every = [c for c in range(os.cpu_count() or 1) if Path(f"/sys/devices/system/cpu/cpu{c}").exists()]
+    phys_total = len({core_of(c) for c in every}) or len(every)
+    phys_share = len({core_of(c) for c in allowed}) or len(allowed)
+    threads = phys_share
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        threads = min(threads, int(omp))
+    return {"model": model, "physical_cores": phys_total, "physical_cores_in_share": phys_share,
+            "threads": max(1, threads)}
+
+
+def set_omp_threads(n: int) -> None:
+    """OpenMP thread count of the calling thread for the CPU baselines (libgomp is shared by
+    the oracle and the reference libraries)."""
+    try:
+        import ctypes
+        ctypes.CDLL("libgomp.so.1").omp_set_num_threads(int(n))
     except OSError:
         pass
-    try:
-        cores = len(os.sched_getaffinity(0))
-    except AttributeError:
-        pass
-    return {"model": model, "threads_available": cores}
 
 
 def measured_traffic(*kernels: str):
@@ -174,8 +204,8 @@ def cpu_decode(torch, dset) -> dict:
     import k3_oracle as ko
     S, o, q, k, v, alpha, beta = (t.cpu().numpy() for t in dset)
     B, H, D = q.shape
-    nt = cpu_info()["threads_available"]
-    nt = max(1, min(nt, 16))
+    ci = cpu_info()
+    nt = ci["threads"]
     S = np.ascontiguousarray(S)
     ko.decode_batch(S, q, k, v, alpha, beta, 1.0 / math.sqrt(D), nt)   # warm
     n, t0 = 0, time.perf_counter()
@@ -183,12 +213,13 @@ def cpu_decode(torch, dset) -> dict:
         ko.decode_batch(S, q, k, v, alpha, beta, 1.0 / math.sqrt(D), nt)
         n += 1
         el = time.perf_counter() - t0
-        if el > 10.0 or n >= 200:
+        if el > 8.0 or n >= 5000:
             break
     step = el / n
     bytes_step = decode_bytes_per_token(H, D) * B
     return {"value": bytes_step / step / 1e9, "unit": "GB/s", "tokens_per_s": B / step,
-            "cores": nt, "kind": "port", "cpu": cpu_info()["model"],
+            "cores": nt, "kind": "port", "cpu": ci["model"], "physical_cores": ci["physical_cores"],
+            "physical_cores_in_share": ci["physical_cores_in_share"],
             "sample": f"{n} full decode steps (B={B}, H={H}, D={D}) of the C oracle, OpenMP over "
                       f"(sequence, head) pairs, {el:.1f} s"}
 
@@ -279,11 +310,16 @@ def bench_prefill(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
         "config": {"workload": "kda_prefill_core", "hidden": c["hidden"], "heads": H, "head_dim": D,
                    "T": T, "chunk": 64, "batch": 1, "conv_k": K, "activations": "bf16",
                    "state": "fp32", "core": kname},
-        "roofline": {"kernel": kname, "bound": "mfma", "achieved": flops_launch / kavg / 1e12,
-                     "peak": BF16_PEAK / 1e12, "unit": "TFLOP/s", "frac": flops_launch / kavg / BF16_PEAK,
+        # The core's algorithmic intensity (flops_per_launch / bytes_per_launch, ~101 FLOP/B)
+        # is below MI355X's ridge (2.5 PFLOP/s / 8 TB/s = 312 FLOP/B): the HBM roof binds, so
+        # frac is the HBM fraction; the MFMA fraction is kept beside it.
+        "roofline": {"kernel": kname, "bound": "hbm", "achieved": bytes_launch / kavg / 1e9,
+                     "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": bytes_launch / kavg / HBM_PEAK,
                      "traffic": traffic,
-                     "hbm_achieved_GBs": bytes_launch / kavg / 1e9,
-                     "hbm_frac": bytes_launch / kavg / HBM_PEAK,
+                     "intensity_flop_per_byte": flops_launch / bytes_launch,
+                     "ridge_flop_per_byte": BF16_PEAK / HBM_PEAK,
+                     "mfma_achieved_TFs": flops_launch / kavg / 1e12, "mfma_peak_TFs": BF16_PEAK / 1e12,
+                     "mfma_frac": flops_launch / kavg / BF16_PEAK,
                      "flops_per_launch": flops_launch, "bytes_per_launch": bytes_launch},
     }
     if cpu:   # timed after every GPU workload (its OpenMP threads would load the host)
@@ -324,6 +360,7 @@ def bench_layer(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
     x = torch.randn((T, E), device="cuda", generator=g).to(bf)
     out = torch.empty((T, E), device="cuda", dtype=torch.float32)
     state = torch.zeros(P * D + 3 * P * (K - 1), device="cuda")
+    x_host = x.float().cpu().numpy()
 
     def step():
         state.zero_()
@@ -357,7 +394,44 @@ def bench_layer(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
                      "unit": "TFLOP/s", "frac": flops / step_s / BF16_PEAK, "traffic": None,
                      "flops_per_step": flops},
     }
+    if cpu:   # timed after every GPU workload
+        out_d["_cpu"] = lambda: cpu_layer(host, x_host)
     return out_d
+
+
+def cpu_layer(host: dict, x) -> dict:
+    """The reference's own k3_kda_layer (src/core/k3_ops.c:864-951, compiled from its sources
+    into oracle/_ref; the C restatement where that is absent) on the same bf16 weights and
+    the first Ts tokens of the same input: a prefill of Ts tokens from a zero state, Ts
+    doubled until the call takes a few seconds."""
+    import numpy as np
+    sys.path.insert(0, str(REPO / "oracle"))
+    import k3_oracle as ko
+    c = PRE
+    ci = cpu_info()
+    nt = ci["threads"]
+    set_omp_threads(nt)
+    L, kind = ko.ref(), "reference"
+    if L is None:
+        L, kind = ko.orc(), "port"
+    arrays = {n: (a.view(np.uint16) if a.dtype == np.int16 else a) for n, a in host.items()}
+    W = ko.Weights(arrays, 1)
+    cfg = ko.make_cfg(c["hidden"], c["H"], c["D"], c["K"], c["gate_lb"], c["rms_eps"])
+    P = c["H"] * c["D"]
+    Ts = 8
+    while True:
+        st = np.zeros(P * c["D"] + 3 * P * (c["K"] - 1), np.float32)
+        t0 = time.perf_counter()
+        ko.kda_layer(L, np.ascontiguousarray(x[:Ts]), W, cfg, Ts, st)
+        el = time.perf_counter() - t0
+        if el > 8.0 or Ts >= len(x):
+            break
+        Ts = min(len(x), Ts * 2)
+    return {"value": Ts / el, "unit": "tokens/s", "cores": nt, "kind": kind, "cpu": ci["model"],
+            "physical_cores": ci["physical_cores"], "physical_cores_in_share": ci["physical_cores_in_share"],
+            "sample": f"k3_kda_layer ({'reference C from its own sources' if kind == 'reference' else 'C oracle'}) "
+                      f"prefill of the first {Ts} of {c['T']} tokens, hidden {c['hidden']}, H={c['H']}, "
+                      f"D={c['D']}, bf16 weights, zero state, OpenMP {nt} threads, {el:.2f} s"}
 
 
 def bench_hybrid(torch, k3, steps: int, warmup: int) -> dict:
@@ -474,7 +548,8 @@ def cpu_prefill(torch, q_in, k_in, v_in, z, b_logit, gate, conv, A_log, dt_bias,
     import k3_oracle as ko
     c = PRE
     H, D, K = c["H"], c["D"], c["K"]
-    nt = max(1, min(cpu_info()["threads_available"], 16))
+    ci = cpu_info()
+    nt = ci["threads"]
     cfg = ko.make_cfg(c["hidden"], H, D, K, c["gate_lb"], c["rms_eps"])
     arrays = {"q_conv": conv[0].cpu().numpy(), "k_conv": conv[1].cpu().numpy(),
               "v_conv": conv[2].cpu().numpy(), "A_log": A_log.cpu().numpy(),
@@ -495,10 +570,40 @@ def cpu_prefill(torch, q_in, k_in, v_in, z, b_logit, gate, conv, A_log, dt_bias,
         Ts = min(c["T"], Ts * 4)
     Ts, el = runs[-1]
     return {"value": Ts / el, "unit": "tokens/s", "cores": nt, "kind": "port",
-            "cpu": cpu_info()["model"],
+            "cpu": ci["model"], "physical_cores": ci["physical_cores"],
+            "physical_cores_in_share": ci["physical_cores_in_share"],
             "sample": f"C oracle orc_kda_core (conv+SiLU, L2, beta, decay, sequential recurrence, "
                       f"RMSNorm, gate) on the first {Ts} of {c['T']} tokens, H={H}, D={D}, "
                       f"OpenMP over heads, {el:.2f} s"}
+
+
+def bench_gemm(torch, k3, steps: int) -> dict:
+    """The layer's projection shapes at c2 (T=8192, hidden 4096) on the hand-written MFMA GEMM
+    (k3hip_proj_gemm) and on hipBLASLt (torch.mm, fp32 output), bf16 operands N(0,1), each
+    timed with HIP events over `steps` back-to-back calls after a clock ramp."""
+    g = torch.Generator(device="cuda").manual_seed(0x4B334441 + 5)
+    res = {}
+    for name, (M, N, K) in {"qkv": (8192, 12288, 4096), "gate_or_o_proj": (8192, 4096, 4096),
+                            "z": (8192, 4096, 256)}.items():
+        a = torch.randn((M, K), device="cuda", generator=g).to(torch.bfloat16)
+        b = torch.randn((N, K), device="cuda", generator=g).to(torch.bfloat16)
+        c = torch.empty((M, N), device="cuda")
+        row = {"M": M, "N": N, "K": K}
+        for impl, fn in (("hand_written_mfma", lambda: k3.proj_gemm(a, b, c)),
+                         ("hipblaslt", lambda: torch.mm(a, b.t(), out_dtype=torch.float32))):
+            fn()
+            ramp(torch, fn)
+            e0, e1 = ev_pair(torch)
+            e0.record()
+            for _ in range(steps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            s = e0.elapsed_time(e1) * 1e-3 / steps
+            row[impl] = {"us": s * 1e6, "TFLOP_s": 2.0 * M * N * K / s / 1e12,
+                         "frac_bf16_peak": 2.0 * M * N * K / s / BF16_PEAK}
+        res[name] = row
+    return res
 
 
 def bench_copy(torch, steps: int) -> dict:
@@ -525,8 +630,9 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["all", "prefill", "decode", "layer", "hybrid", "copy"], default="all",
-                    help="copy: the 1 GiB device copy used to calibrate HBM traffic counters")
+    ap.add_argument("--workload", choices=["all", "prefill", "decode", "layer", "hybrid", "copy", "gemm"],
+                    default="all", help="copy: the 1 GiB device copy used to calibrate HBM traffic counters; "
+                    "gemm: the layer's projection shapes on the hand-written GEMM and on hipBLASLt")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -540,6 +646,9 @@ def main() -> int:
     k3.lib()
     if a.workload == "copy":
         print(json.dumps({"workload": "copy_calibration", **bench_copy(torch, a.steps)}))
+        return 0
+    if a.workload == "gemm":
+        print(json.dumps({"workload": "projection_gemms", **bench_gemm(torch, k3, a.steps)}))
         return 0
     res = {}
     if a.workload in ("all", "decode"):
@@ -562,7 +671,8 @@ def main() -> int:
         "metric": "KDA prefill tokens/s (H=32,d=128,T=8k) + decode state-update GB/s, 1 GPU",
         "value": head["value"], "unit": head["unit"], "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": head["ms_per_step"], "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 in, split-bf16 MFMA (hi/lo pairs, fp32 accumulation), fp32 state",
         "data": "synthetic (torch Philox on device, distributions of the benchmark configs)",
         "config": head["config"], "roofline": head["roofline"],
         "cpu_baseline": head.get("cpu_baseline"),

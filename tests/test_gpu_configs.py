@@ -129,3 +129,58 @@ def test_c3_long_context_drift(gpu):
     r_state = worst_ratio(dS.cpu().numpy(), S_ref, 2e-3 * rms(S_ref), 2e-3)
     print(f"c3 decode tail (256 steps): worst {r_dec:.3f}x; final state {r_state:.3f}x of the 2e-3 bar")
     assert r_dec <= 1.0 and r_state <= 1.0
+
+
+def test_c3_drift_full_heads(gpu):
+    """c3 at the benchmark's full width: one prefill of T = 65,536 tokens at H = 32, D = 128
+    (1,024 chunks, the state carried through all of them) on fp32 conv inputs, against the
+    oracle's orc_kda_core (conv, L2, decay, sequential recurrence) on the same inputs. The
+    worst error of every 4,096-position window is the drift curve; with K3KDA_RECORD_DIR set
+    it is also written there as c3_drift_h32.json."""
+    import json
+    import os
+    import torch
+    H, D, K, T, LB = 32, 128, 4, 65536, -5.0
+    P = H * D
+    g = torch.Generator(device="cuda").manual_seed(0x4B334441 + 3)
+    q_in, k_in, v_in = (torch.randn((T, P), device="cuda", generator=g) for _ in range(3))
+    z = torch.randn((T, P), device="cuda", generator=g) * 0.5
+    bl = torch.randn((T, H), device="cuda", generator=g)
+    conv = [torch.randn((P, K), device="cuda", generator=g) * 0.5 for _ in range(3)]
+    A_log = torch.rand((H,), device="cuda", generator=g) * 1.5
+    dt_bias = torch.randn((P,), device="cuda", generator=g)
+    S = torch.zeros((H, D, D), device="cuda")
+    o = torch.full((T, P), float("nan"), device="cuda")
+    ws = torch.empty(gpu.kda_chunk_workspace(T, H, D), dtype=torch.uint8, device="cuda")
+    qs = float(np.float32(1) / np.sqrt(np.float32(D)))
+    gpu.kda_prefill(q_in, k_in, v_in, z, bl, *conv, A_log, dt_bias, None, S, o, H, D, K, LB, qs, ws)
+    torch.cuda.synchronize()
+    del ws
+    h = lambda t: t.cpu().numpy()
+    arrays = {"q_conv": h(conv[0]), "k_conv": h(conv[1]), "v_conv": h(conv[2]), "A_log": h(A_log),
+              "dt_bias": h(dt_bias), "o_norm": np.ones(D, np.float32)}
+    for n in ("q", "k", "v", "g", "f_a", "f_b", "b", "o"):
+        arrays[n] = np.zeros((1, 1), np.float32)
+    W = ko.Weights(arrays, 0)
+    cfg = ko.make_cfg(8, H, D, K, LB, 1e-5)
+    st = np.zeros(P * D + 3 * P * (K - 1), np.float32)
+    _, o_ref = ko.core(h(q_in), h(k_in), h(v_in), h(z), h(bl), np.zeros((T, P), np.float32), W, cfg, T, st,
+                       nthreads=16, want_rec=True)
+    got = h(o)
+    curve = []
+    for t in range(4095, T, 4096):
+        seg = slice(t - 4095, t + 1)
+        curve.append((t + 1, worst_ratio(got[seg], o_ref[seg], 2e-3 * rms(o_ref[seg]), 2e-3),
+                      worst_ratio(got[seg], o_ref[seg], 1e-4 * rms(o_ref[seg]), 1e-4)))
+    r_state = worst_ratio(h(S).ravel(), st[:P * D], 2e-3 * rms(st[:P * D]), 2e-3)
+    print("c3 H=32 drift (position, worst fraction of the 2e-3 bar):",
+          " ".join(f"{p}:{r:.4f}" for p, r, _ in curve), f"; final state {r_state:.4f}x")
+    rec = os.environ.get("K3KDA_RECORD_DIR")
+    if rec:
+        os.makedirs(rec, exist_ok=True)
+        with open(os.path.join(rec, "c3_drift_h32.json"), "w") as f:
+            json.dump({"T": T, "H": H, "D": D, "chunk": 64, "inputs": "fp32 conv inputs N(0,1), z N(0,0.25), "
+                       "b logits N(0,1), gate_lb -5, zero state", "window": 4096,
+                       "worst_2e-3_bar": [[p, r] for p, r, _ in curve],
+                       "worst_1e-4_bar": [[p, r4] for p, _, r4 in curve], "final_state_2e-3_bar": r_state}, f, indent=1)
+    assert max(r for _, r, _ in curve) <= 1.0 and r_state <= 1.0
