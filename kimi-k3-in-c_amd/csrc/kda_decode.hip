@@ -13,9 +13,11 @@
 // its whole state in registers between the read and the write: NT threads, each owning
 // NPASS float4s at rows rs, rs+RPP, ... of column group cg. A pass over the rows is one
 // contiguous D*RPP*4-byte span of S per instruction, so every wave issues full 64-byte
-// segments. The two reductions over rows (u, then o) go through LDS. The state write-back
-// is a nontemporal store: it streams out without being kept in the caches, which measured
-// 54.5 -> 45.5 us per B=64, H=32, D=128 step (5.0 -> 6.0 TB/s) on MI355X.
+// segments. The two reductions over rows (u, then o) go through LDS. The state is read
+// with nontemporal loads and written back with nontemporal stores: it streams through
+// without being kept in the caches. The stores measured 54.5 -> 45.5 us per B=64, H=32,
+// D=128 step (5.0 -> 6.0 TB/s) on MI355X; the loads a further ~0.6 us (48.6 -> 48.0 us
+// in the current build, alternating runs).
 // D = 128 uses 512 threads (8 float4s each, 60 VGPRs, 8 waves per SIMD): the 2,048 states
 // of a B=64 step then run as two full rounds of 1,024 workgroups; with 256 threads
 // (16 float4s, 90 VGPRs, 5 waves per SIMD) they ran as 1,280 + 768, about 1.5% slower.
@@ -58,7 +60,7 @@ __global__ __launch_bounds__(NT) void kda_decode_kernel(
     f4 *Sp = reinterpret_cast<f4 *>(S + (size_t)(pair / H) * s_stride + (size_t)(pair % H) * D * D);
     f4 s[NPASS];
 #pragma unroll
-    for (int m = 0; m < NPASS; m++) s[m] = Sp[(rs + m * RPP) * CPR + cg];
+    for (int m = 0; m < NPASS; m++) s[m] = __builtin_nontemporal_load(&Sp[(rs + m * RPP) * CPR + cg]);
     const f4 vv = reinterpret_cast<const f4 *>(v + vo)[cg];
     const float b = beta[pair];
     __syncthreads();

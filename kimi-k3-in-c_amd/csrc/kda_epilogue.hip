@@ -81,10 +81,12 @@ __global__ __launch_bounds__(256) void kda_epilogue2_kernel(long rows, int H, fl
         const long r = r0 + sub;
         const bool live = r < rows;
         const size_t base = (size_t)(live ? r : rows - 1) * D + 4 * cl;
-        const f4 x = *reinterpret_cast<const f4 *>(o + base);
+        const f4 x = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(o + base));   // read once: streamed
         f4 gt;
         if constexpr (GDT == K3HIP_BF16) {
-            const uint2 u = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(gate) + base);
+            typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+            const u32x2 uu = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(reinterpret_cast<const uint16_t *>(gate) + base));
+            const uint2 u = {uu.x, uu.y};
             gt = f4{__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
                     __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u)};
         } else if constexpr (GDT == K3_DT_F16) {
