@@ -34,10 +34,10 @@ HBM_PEAK = 8.0e12          # bytes/s, MI355X HBM3E
 BF16_PEAK = 2.5e15         # flop/s, dense bf16 MFMA
 FP32_PEAK = 157.3e12       # flop/s, dense fp32 MFMA
 
-# c2 / c1 shapes
+# prefill core / layer at T=8192, hidden 4096; batch-64 decode
 PRE = dict(hidden=4096, H=32, D=128, T=8192, chunk=64, K=4, gate_lb=-5.0, rms_eps=1e-5)
 DEC = dict(B=64, H=32, D=128)
-# c4 hybrid slice: 3 KDA layers + 1 gated MLA layer, decode at batch 16 over an 8192 context
+# hybrid decode slice: 3 KDA layers + 1 gated MLA layer, decode at batch 16 over an 8192 context
 HYB = dict(hidden=7168, B=16, ctx=8192, kda_layers=3, H=32, D=128, K=4, gate_lb=-5.0,
            mla_heads=64, q_lora=1536, kv_lora=512, qk_nope=128, qk_rope=64, v_head=128)
 
@@ -133,7 +133,7 @@ RAMP_S = 0.3
 def ramp(torch, step):
     """Untimed: repeat the workload's own step for RAMP_S seconds before its warm-up steps.
     From idle the GPU takes tens of milliseconds of sustained load to reach its working
-    clocks (c2 core: 0.63 ms per step after 3 warm-up steps, 0.585 after 20, 0.56 after
+    clocks (T=8192 prefill core: 0.63 ms per step after 3 warm-up steps, 0.585 after 20, 0.56 after
     ~60), so a few warm-up steps alone measure the ramp, not the kernels."""
     t0 = time.perf_counter()
     while time.perf_counter() - t0 < RAMP_S:
@@ -329,7 +329,7 @@ def bench_prefill(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
 
 
 def bench_layer(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
-    """The full k3_kda_layer prefill at c2 on bf16 weights: projections (bf16 MFMA GEMMs),
+    """The full k3_kda_layer prefill at T=8192, hidden 4096 on bf16 weights: projections (bf16 MFMA GEMMs),
     K1, K2, K4, o_proj -- k3hip_kda_layer_prefill, x bf16 in, fp32 out, zero initial state."""
     import ctypes as C
     c = PRE
@@ -435,7 +435,7 @@ def cpu_layer(host: dict, x) -> dict:
 
 
 def bench_hybrid(torch, k3, steps: int, warmup: int) -> dict:
-    """c4: one decode step of batch 16 through 3 KDA layers (k3hip_kda_layer_decode) and one
+    """Hybrid slice: one decode step of batch 16 through 3 KDA layers (k3hip_kda_layer_decode) and one
     gated MLA layer with absorbed weights over an 8192-position latent cache
     (k3hip_mla_decode), hidden 7168, bf16 weights N(0, 0.02). Each part is timed with HIP
     events over `steps` back-to-back steps. Bytes: each layer's weights once + its
@@ -578,7 +578,7 @@ def cpu_prefill(torch, q_in, k_in, v_in, z, b_logit, gate, conv, A_log, dt_bias,
 
 
 def bench_gemm(torch, k3, steps: int) -> dict:
-    """The layer's projection shapes at c2 (T=8192, hidden 4096) on the hand-written MFMA GEMM
+    """The layer's projection shapes at T=8192, hidden 4096 on the hand-written MFMA GEMM
     (k3hip_proj_gemm) and on hipBLASLt (torch.mm, fp32 output), bf16 operands N(0,1), each
     timed with HIP events over `steps` back-to-back calls after a clock ramp."""
     g = torch.Generator(device="cuda").manual_seed(0x4B334441 + 5)

@@ -131,7 +131,7 @@ __device__ __forceinline__ void store_cpl(float *p, const float (&v)[CPL])
 
 // Split x and store it as lane `lane` of the fragment block at `blk`. Workspace stores are
 // nontemporal: the block is read back by the next kernel from HBM (its L2 warm-up touches),
-// so keeping it in this kernel's L2 only displaces the inputs (c2 phase 1: -5 us).
+// so keeping it in this kernel's L2 only displaces the inputs (phase 1 at T=8192, H=32, D=128: -5 us).
 __device__ __forceinline__ void store_frag(char *blk, int lane, const float (&x)[8])
 {
     bf16x8 hi, lo;
@@ -768,7 +768,7 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra_act(
 // windows where it does not hold up the other role: state waves between the two barriers
 // (they wait for Vn there), row waves spread over their products (P2_MID). A step's O rows
 // are stored at the start of the next step, before its loads, so the stores do not queue
-// behind a full vector-memory path (c2 prefill kernels 598 -> 565 us).
+// behind a full vector-memory path (T=8192, H=32 prefill kernels 598 -> 565 us).
 template <int D, int NW> struct RowOps {
     static constexpr int KSI = D / 32;
     Frag wf[KSI], qf[KSI], af[2];
@@ -785,7 +785,7 @@ template <int D> struct StateOps {
 // barrier (2), so its loads share the CU's vector-memory path with the state waves' loads
 // (issued between the two barriers) instead of all queueing at the start of the step. At
 // D = 128 all W and Q e^G K-steps go between the products and A_qk and U after barrier (2)
-// (c2: 6 us faster than 3 K-steps before it, 10 us faster than everything before it).
+// (T=8192, H=32: 6 us faster than 3 K-steps before it, 10 us faster than everything before it).
 constexpr int P2_MID = 4;
 
 // Row wave w's operands of one chunk: W, Q e^G and A_qk fragments of its 16 token rows
@@ -1036,7 +1036,7 @@ __global__ __launch_bounds__(512) void kda_chunk_state(int T, int H, const char 
         // item PF chunks ahead (one dword each); when the operand loads of that chunk come,
         // they hit L2 instead of waiting on HBM once per step. A touch is consumed (waited
         // for) two steps after it is issued, just before its register is reused. PF = 2 (the
-        // touch one step before the operand loads) measured best: c2 phase 2 is 7 us faster
+        // touch one step before the operand loads) measured best: phase 2 at T=8192, H=32 is 7 us faster
         // than at PF = 4 and 50 us faster than without touches; farther touches are evicted
         // from the XCD's L2 before use more often (one touch per 64 bytes cost 6 us more).
         constexpr int PF = 2;

@@ -1,7 +1,7 @@
 # SPDX-License-Identifier: Apache-2.0
-"""The benchmark configurations that are parity cases, on the GPU against the CPU oracle.
+"""Parity cases at the benchmarks' configurations, on the GPU against the CPU oracle.
 
-c0  one KDA layer, hidden 256, H=4, D=64, conv 4, T=32 prefill then 8 single-token decode
+Small layer: one KDA layer, hidden 256, H=4, D=64, conv 4, T=32 prefill then 8 single-token decode
     steps carrying the state, fp32, weights N(0,0.02), x N(0,1), A_log U(0,1.5), dt_bias
     N(0,1); every output element of every step and the full state compared. Both gates:
     the reference's bounded gate (gate_lb = -5) and the unbounded softplus gate
@@ -9,7 +9,7 @@ c0  one KDA layer, hidden 256, H=4, D=64, conv 4, T=32 prefill then 8 single-tok
     closed form in tests/test_oracle_invariants.py).
     Tolerance: rtol 1e-4, atol 1e-4 * rms (fp32 path; the T=32 prefill runs the chunked
     kernel for the bounded gate).
-c3  long-context drift: D=128, a 65,536-token chunked prefill (state carried across 1024
+Long-context drift: D=128, a 65,536-token chunked prefill (state carried across 1024
     chunks) then 256 decode steps at batch 1, against the sequential oracle over the same
     65,792 tokens; the error is recorded at every 4096th position and may not grow past the
     chunked bar (rtol 2e-3, atol 2e-3 * rms). Heads are independent, so 4 of the 32 heads
@@ -31,7 +31,7 @@ def rms(a):
     return float(np.sqrt(np.mean(np.asarray(a, np.float64) ** 2)))
 
 
-def c0_weights(rng, hidden=256, H=4, D=64, K=4):
+def small_layer_weights(rng, hidden=256, H=4, D=64, K=4):
     P = H * D
     nrm = lambda *s: f32(rng.standard_normal(s) * 0.02)
     arrays = {"q": nrm(P, hidden), "k": nrm(P, hidden), "v": nrm(P, hidden), "g": nrm(P, hidden),
@@ -43,12 +43,12 @@ def c0_weights(rng, hidden=256, H=4, D=64, K=4):
 
 
 @pytest.mark.parametrize("gate_lb", [-5.0, 0.0])
-def test_c0_prefill_then_decode(gpu, gate_lb):
+def test_small_layer_prefill_then_decode(gpu, gate_lb):
     import torch
     rng = np.random.default_rng(0x4B334441 + 0)
     hidden, H, D, K = 256, 4, 64, 4
     P = H * D
-    W = c0_weights(rng, hidden, H, D, K)
+    W = small_layer_weights(rng, hidden, H, D, K)
     cfg = ko.make_cfg(hidden, H, D, K, gate_lb, 1e-5)
     nst = P * D + 3 * P * (K - 1)
     st_ref = np.zeros(nst, np.float32)
@@ -61,24 +61,24 @@ def test_c0_prefill_then_decode(gpu, gate_lb):
         out = torch.zeros((T, hidden), device="cuda")
         dw.layer(out, torch.from_numpy(x).cuda(), dst, T)
         torch.cuda.synchronize()
-        assert_close(out.cpu().numpy(), want, 1e-4 * rms(want), 1e-4, f"c0 lb={gate_lb} step {step} out")
-        assert_close(dst.cpu().numpy(), st_ref, 1e-4 * rms(st_ref), 1e-4, f"c0 lb={gate_lb} step {step} state")
+        assert_close(out.cpu().numpy(), want, 1e-4 * rms(want), 1e-4, f"small layer lb={gate_lb} step {step} out")
+        assert_close(dst.cpu().numpy(), st_ref, 1e-4 * rms(st_ref), 1e-4, f"small layer lb={gate_lb} step {step} state")
         if gate_lb != 0.0:   # the host drop-in on the same sequence
             out_h = np.zeros((T, hidden), np.float32)
             gpu.kda_layer_host(out_h, x, W.w, cfg, T, st_host)
-            assert_close(out_h, want, 1e-4 * rms(want), 1e-4, f"c0 drop-in step {step} out")
-            assert_close(st_host, st_ref, 1e-4 * rms(st_ref), 1e-4, f"c0 drop-in step {step} state")
+            assert_close(out_h, want, 1e-4 * rms(want), 1e-4, f"small layer drop-in step {step} out")
+            assert_close(st_host, st_ref, 1e-4 * rms(st_ref), 1e-4, f"small layer drop-in step {step} state")
     dw.close()
 
 
-def test_c3_long_context_drift(gpu):
+def test_long_context_drift(gpu):
     import torch
     rng = np.random.default_rng(0x4B334441 + 3)
     H, D, K = 4, 128, 4
     P = H * D
     T, NDEC = 65536, 256
     Tall = T + NDEC
-    # raw activations N(0,1) through the oracle's conv + SiLU + L2 + decay (c0 gate spread)
+    # raw activations N(0,1) through the oracle's conv + SiLU + L2 + decay (the small layer's gate spread)
     arrays = {"q_conv": f32(rng.standard_normal((P, K)) * 0.5), "k_conv": f32(rng.standard_normal((P, K)) * 0.5),
               "v_conv": f32(rng.standard_normal((P, K)) * 0.5), "A_log": f32(rng.uniform(0, 1.5, H)),
               "dt_bias": f32(rng.standard_normal(P)), "o_norm": f32(np.ones(D))}
@@ -104,7 +104,7 @@ def test_c3_long_context_drift(gpu):
     for t in range(4095, T, 4096):
         seg = slice(t - 4095, t + 1)
         curve.append((t + 1, worst_ratio(got[seg], o_ref[seg], 2e-3 * rms(o_ref[seg]), 2e-3)))
-    print("c3 drift (position, worst fraction of the 2e-3 bar):",
+    print("long-context drift (position, worst fraction of the 2e-3 bar):",
           " ".join(f"{p}:{r:.3f}" for p, r in curve))
     assert max(r for _, r in curve) <= 1.0
     # decode tail at batch 1 from the GPU's own state
@@ -121,22 +121,22 @@ def test_c3_long_context_drift(gpu):
             w1 = ko.decode_batch(S_chk[None].copy(), q[t:t + 1].reshape(1, H, D),
                                  k[t:t + 1].reshape(1, H, D), v[t:t + 1].reshape(1, H, D),
                                  al[t:t + 1].reshape(1, H, D), beta[t:t + 1], qs, 1)
-            assert_close(o1.cpu().numpy(), w1, 1e-4 * rms(w1), 1e-4, "c3 first decode step, same state")
+            assert_close(o1.cpu().numpy(), w1, 1e-4 * rms(w1), 1e-4, "long-context first decode step, same state")
         dec.append(o1)
     torch.cuda.synchronize()
     got_dec = torch.cat(dec).cpu().numpy().reshape(NDEC, P)
     r_dec = worst_ratio(got_dec, o_ref[T:], 2e-3 * rms(o_ref[T:]), 2e-3)
     r_state = worst_ratio(dS.cpu().numpy(), S_ref, 2e-3 * rms(S_ref), 2e-3)
-    print(f"c3 decode tail (256 steps): worst {r_dec:.3f}x; final state {r_state:.3f}x of the 2e-3 bar")
+    print(f"long-context decode tail (256 steps): worst {r_dec:.3f}x; final state {r_state:.3f}x of the 2e-3 bar")
     assert r_dec <= 1.0 and r_state <= 1.0
 
 
-def test_c3_drift_full_heads(gpu):
-    """c3 at the benchmark's full width: one prefill of T = 65,536 tokens at H = 32, D = 128
+def test_long_context_drift_full_heads(gpu):
+    """The long-context drift at the benchmark's full width: one prefill of T = 65,536 tokens at H = 32, D = 128
     (1,024 chunks, the state carried through all of them) on fp32 conv inputs, against the
     oracle's orc_kda_core (conv, L2, decay, sequential recurrence) on the same inputs. The
     worst error of every 4,096-position window is the drift curve; with K3KDA_RECORD_DIR set
-    it is also written there as c3_drift_h32.json."""
+    it is also written there as long_context_drift_h32.json."""
     import json
     import os
     import torch
@@ -173,12 +173,12 @@ def test_c3_drift_full_heads(gpu):
         curve.append((t + 1, worst_ratio(got[seg], o_ref[seg], 2e-3 * rms(o_ref[seg]), 2e-3),
                       worst_ratio(got[seg], o_ref[seg], 1e-4 * rms(o_ref[seg]), 1e-4)))
     r_state = worst_ratio(h(S).ravel(), st[:P * D], 2e-3 * rms(st[:P * D]), 2e-3)
-    print("c3 H=32 drift (position, worst fraction of the 2e-3 bar):",
+    print("long-context H=32 drift (position, worst fraction of the 2e-3 bar):",
           " ".join(f"{p}:{r:.4f}" for p, r, _ in curve), f"; final state {r_state:.4f}x")
     rec = os.environ.get("K3KDA_RECORD_DIR")
     if rec:
         os.makedirs(rec, exist_ok=True)
-        with open(os.path.join(rec, "c3_drift_h32.json"), "w") as f:
+        with open(os.path.join(rec, "long_context_drift_h32.json"), "w") as f:
             json.dump({"T": T, "H": H, "D": D, "chunk": 64, "inputs": "fp32 conv inputs N(0,1), z N(0,0.25), "
                        "b logits N(0,1), gate_lb -5, zero state", "window": 4096,
                        "worst_2e-3_bar": [[p, r] for p, r, _ in curve],

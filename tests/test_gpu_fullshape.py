@@ -68,7 +68,7 @@ def test_core_at_benchmark_shape(gpu):
     ry = assert_close(got, want, 2e-3 * rms(want), 2e-3, "core y at T=8192")
     rs = assert_close(gS.ravel(), st[:P * D], 2e-3 * rms(st[:P * D]), 2e-3, "core S at T=8192")
     t4 = worst_ratio(got, want, 1e-4 * rms(want), 1e-4)
-    print(f"c2 core H={H} D={D} T={T}: worst {ry:.4f}x (y) / {rs:.4f}x (S) of the 2e-3 bar, {t4:.3f}x of 1e-4")
+    print(f"core H={H} D={D} T={T}: worst {ry:.4f}x (y) / {rs:.4f}x (S) of the 2e-3 bar, {t4:.3f}x of 1e-4")
 
 
 def test_layer_prefill_at_benchmark_width(gpu):
