@@ -109,11 +109,13 @@ int mla_attention(int B, int H, int KL, int CW, int Tn, int cap, float scale, co
 
 // One decode token of a KDA layer between its projections (kda_step.hip): K1 + K3 + K4 per
 // (head, sequence). Cin rows (stride ldc) hold q | k | v at columns 0, P, 2P and the beta
-// logits at bcol; Cz [B][P] the decay logits (f_b output); gl the output-gate logits as
+// logits at bcol, f_a (D wide) at facol; Wfb the f_b weight [P][D] in the decode GEMV's
+// fragment order (rows_frag_pack), from which the kernel forms the decay logits z = f_a W_fb^T;
+// gl the output-gate logits as
 // gsplit planes of gplane floats. states: per sequence (stride floats apart) the H D x D
 // state, then the [3][P][conv_k-1] conv history; both updated in place. y [B][P] out.
 int layer_step(int B, int H, int D, int K, float lb, float eps, float q_scale, const float *Cin,
-               long ldc, int bcol, const float *Cz, const float *gl, int gsplit, long gplane,
+               long ldc, int bcol, int facol, const uint16_t *Wfb, const float *gl, int gsplit, long gplane,
                const float *q_conv, const float *k_conv, const float *v_conv, const float *A_log,
                const float *dt_bias, const float *o_norm, float *states, long stride, float *y,
                hipStream_t st);

@@ -581,14 +581,13 @@ static int layer_decode_impl(const k3hip_kda_weights *w, int B, float *out, cons
     const size_t BP = (size_t)B * P;
     if ((E & 7) || (D & 7) || (P & 7) || ((uintptr_t)x & 15))
         K3_FAIL(K3HIP_EUNSUPPORTED, "%s: hidden=%d D=%d need multiples of 8, x 16-byte aligned", who, E, D);
-    // scratch: q k v f_a b projections [B][NI] | output-gate partial planes | z | y |
+    // scratch: q k v f_a b projections [B][NI] | output-gate partial planes | y |
     //          split-K partials (shared by the projections, which run one after another)
     const int NI = 3 * (int)P + D + H;
     const long ldi = (NI + 3) & ~3;   // a multiple of 4: f_a is read in place as an x operand
     const int gs = gemm_rows_splits((int)P, E);
-    const size_t wsf = std::max({gemm_rows_ws_floats(B, NI, E), gemm_rows_ws_floats(B, (int)P, D),
-                                 gemm_rows_ws_floats(B, E, (int)P)});
-    size_t sizes[] = {(size_t)B * ldi * 4, (size_t)gs * BP * 4, BP * 4, BP * 4, wsf * 4};
+    const size_t wsf = std::max(gemm_rows_ws_floats(B, NI, E), gemm_rows_ws_floats(B, E, (int)P));
+    size_t sizes[] = {(size_t)B * ldi * 4, (size_t)gs * BP * 4, BP * 4, wsf * 4};
     constexpr int NB = sizeof sizes / sizeof sizes[0];
     size_t off[NB], total = 0;
     for (int i = 0; i < NB; i++) {
@@ -606,9 +605,9 @@ static int layer_decode_impl(const k3hip_kda_weights *w, int B, float *out, cons
                 "entry point has %zu (use k3hip_kda_layer_decode, or fewer sequences per call)", who, B, E, H, D,
                 total, scr_bytes);
     }
-    float *Cin = (float *)(bs + off[0]), *fa = Cin + 3 * P;
-    float *glp = (float *)(bs + off[1]), *Cz = (float *)(bs + off[2]), *y = (float *)(bs + off[3]);
-    float *ws = (float *)(bs + off[4]);
+    float *Cin = (float *)(bs + off[0]);
+    float *glp = (float *)(bs + off[1]), *y = (float *)(bs + off[2]);
+    float *ws = (float *)(bs + off[3]);
     const uint16_t *Win = (const uint16_t *)w->xin_f, *Wg = (const uint16_t *)w->g_f,
                    *Wfb = (const uint16_t *)w->f_b_f, *Wo = (const uint16_t *)w->o_f;
 
@@ -618,11 +617,10 @@ static int layer_decode_impl(const k3hip_kda_weights *w, int B, float *out, cons
     //   planes that the step kernel adds
     if ((rc = gemm_rows(B, NI, E, x, E, Win, Cin, ldi, st, ws, wsf))) return rc;
     if ((rc = gemm_rows_part(B, (int)P, E, x, E, Wg, glp, st))) return rc;
-    if ((rc = gemm_rows(B, (int)P, D, fa, ldi, Wfb, Cz, (long)P, st, ws, wsf))) return rc;
-    // 2-8 K1, K3 and K4 on one token per sequence (kda_step.hip), conv history and state in
-    //   each slot, then 9 o_proj
+    // 2-8 the f_b product, K1, K3 and K4 on one token per sequence (kda_step.hip), conv
+    //   history and state in each slot, then 9 o_proj
     if ((rc = layer_step(B, H, D, K, w->gate_lb, w->rms_eps, 1.0f / sqrtf((float)D), Cin, ldi,
-                         3 * (int)P + D, Cz, glp, gs, (long)BP, w->q_conv, w->k_conv, w->v_conv,
+                         3 * (int)P + D, 3 * (int)P, Wfb, glp, gs, (long)BP, w->q_conv, w->k_conv, w->v_conv,
                          w->A_log, w->dt_bias, w->o_norm, states, state_stride, y, st)))
         return rc;
     return gemm_rows(B, E, (int)P, y, (long)P, Wo, out, E, st, ws, wsf);

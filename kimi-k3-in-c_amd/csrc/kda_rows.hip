@@ -29,33 +29,19 @@
 #include <algorithm>
 
 #include "kda_internal.h"
+#include "kda_split.h"
 
 namespace k3kda {
 
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+using bsplit::bf16x8;
+using bsplit::split_row8;
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int RT_WAVES = 8;   // waves per workgroup
 constexpr int RT_NT = 4;      // 16-column groups per workgroup
 constexpr int RT_SMAX = 16;   // most K-ranges per column block
-
-// x = hi + lo, both bf16 (round to nearest even; lo carries the rounding error of hi)
-__device__ __forceinline__ void split_row8(const f4 &a, const f4 &b, bf16x8 &hi, bf16x8 &lo)
-{
-    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-    for (int e = 0; e < 8; e += 2) {
-        const bf16x2 h = __builtin_convertvector(f2{v[e], v[e + 1]}, bf16x2);
-        const uint32_t u = __builtin_bit_cast(uint32_t, h);
-        const float h0 = __uint_as_float(u << 16), h1 = __uint_as_float(u & 0xffff0000u);
-        const bf16x2 l = __builtin_convertvector(f2{v[e] - h0, v[e + 1] - h1}, bf16x2);
-        hi[e] = h[0]; hi[e + 1] = h[1];
-        lo[e] = l[0]; lo[e + 1] = l[1];
-    }
-}
 
 // out[u] (16 B) for u = (g KT + t) 64 + lane: W[16 g + (lane & 15)][32 t + 8 (lane >> 4) .. + 7],
 // zero past N and K (K % 8 == 0, so a slice is wholly inside or outside)

@@ -21,15 +21,24 @@
 // kda_epilogue2_kernel (fp32 per-lane squares, double across the row's lanes, hardware
 // sigmoid). The output-gate logits may arrive as split-K partial planes of the gate
 // projection; they are added in plane order, which is what the split-K reduction does.
+//
+// The decay logits z = f_a . W_fb^T (the f_b projection, k3_ops.c:886, D outputs of the
+// head from the D-wide f_a row) are computed here too, one 16-channel group of W_fb per
+// wave, in the arithmetic of the decode GEMV (kda_rows.hip): f_a split into bf16 hi + lo
+// against the bf16 weight fragments, each 32-wide K-step's product an fp32 partial of its
+// own, the partials added in K-step order. z gets the bits the stand-alone GEMV gives it,
+// without its launch and its round trip through memory (batch-16 decode layer at hidden
+// 7168: one launch of ~5 us fewer per layer).
 #include "kda_internal.h"
 #include "kda_prep_math.h"
+#include "kda_split.h"
 
 namespace k3kda {
 
 template <int D, int K>
 __global__ __launch_bounds__(4 * D) void kda_layer_step_kernel(
     int H, float lb, float eps, float q_scale, const float *__restrict__ Cin, long ldc, int bcol,
-    const float *__restrict__ Cz, const float *__restrict__ gl, int gsplit, long gplane,
+    int facol, const uint16_t *__restrict__ Wfb, const float *__restrict__ gl, int gsplit, long gplane,
     const float *__restrict__ q_conv, const float *__restrict__ k_conv,
     const float *__restrict__ v_conv, const float *__restrict__ A_log,
     const float *__restrict__ dt_bias, const float *__restrict__ o_norm,
@@ -44,7 +53,7 @@ __global__ __launch_bounds__(4 * D) void kda_layer_step_kernel(
     constexpr int CPL = D >= 32 ? D / 32 : 1;   // K1 channels per lane of a half-wave
     constexpr int NH = K - 1;
 
-    __shared__ float s_q[D], s_k[D], s_v[D], s_a[D];
+    __shared__ float s_q[D], s_k[D], s_v[D], s_a[D], s_z[D];
     __shared__ f4 s_red[RPP][CPR];
     __shared__ f4 s_u[CPR];
     __shared__ float s_beta;
@@ -53,11 +62,49 @@ __global__ __launch_bounds__(4 * D) void kda_layer_step_kernel(
     const int cg = tid % CPR, rs = tid / CPR;
     const size_t P = (size_t)H * D;
 
-    // state first: its latency overlaps the K1 arithmetic below
+    // z: wave wv takes the head's 16-channel group wv of W_fb (D / 16 groups = NT / 64
+    // waves); A-operand row 0 is this sequence's f_a, rows 1..15 zero. The weight and f_a
+    // loads go out before the state's, so the MFMAs below wait for them only.
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    constexpr int KT = (D + 31) / 32;   // K-steps over the D-wide f_a
+    const int ln = tid & 63, r16 = ln & 15, kq = ln >> 4, wv = tid >> 6;
+    bsplit::bf16x8 wfr[KT];
+    f4 fxa[KT], fxb[KT];
+    {
+        const bsplit::bf16x8 *wf = reinterpret_cast<const bsplit::bf16x8 *>(Wfb) +
+                                   ((size_t)h * (D / 16) + wv) * KT * 64 + ln;
+        const float *fa = Cin + (size_t)b * ldc + facol;
+#pragma unroll
+        for (int t = 0; t < KT; t++) {
+            wfr[t] = wf[(size_t)t * 64];
+            const int k = 32 * t + 8 * kq;   // D % 8 == 0: the 8-slice is wholly inside or outside
+            fxa[t] = fxb[t] = f4(0.0f);
+            if (r16 == 0 && k < D) {
+                fxa[t] = f4{fa[k], fa[k + 1], fa[k + 2], fa[k + 3]};
+                fxb[t] = f4{fa[k + 4], fa[k + 5], fa[k + 6], fa[k + 7]};
+            }
+        }
+    }
+
+    // then the state: its latency overlaps the z product and the K1 arithmetic below
     f4 *Sp = reinterpret_cast<f4 *>(states + (size_t)b * stride + (size_t)h * D * D);
     f4 s[NPASS];
 #pragma unroll
     for (int m = 0; m < NPASS; m++) s[m] = __builtin_nontemporal_load(&Sp[(rs + m * RPP) * CPR + cg]);
+
+    {
+        f32x4 zs = 0.0f;
+#pragma unroll
+        for (int t = 0; t < KT; t++) {
+            bsplit::bf16x8 xh, xl;
+            bsplit::split_row8(fxa[t], fxb[t], xh, xl);
+            f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, wfr[t], f32x4(0.0f), 0, 0, 0);
+            p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, wfr[t], p, 0, 0, 0);
+            zs = t == 0 ? p : zs + p;
+        }
+        if (ln < 16) s_z[16 * wv + ln] = zs[0];   // C layout: lane n < 16 holds row 0, column n
+    }
+    __syncthreads();
 
     // K1: task 0..3 = q, k, v, decay gate; half-wave hw takes tasks hw, hw + NT/32, ...
     const int hw = tid >> 5, l32 = tid & 31;
@@ -96,7 +143,7 @@ __global__ __launch_bounds__(4 * D) void kda_layer_step_kernel(
 #pragma unroll
             for (int e = 0; e < CPL; e++) {
                 const size_t ch = c0 + e;
-                const float z = Cz[(size_t)b * P + ch];
+                const float z = s_z[cl + e];
                 const float g = lb != 0.0f ? gate_bounded(lb, gate_a2(a), z, dt_bias[ch])
                                            : -a * softplus_ref(z + dt_bias[ch]);   // softplus gate
                 s_a[cl + e] = fast_exp(g);
@@ -163,14 +210,14 @@ __global__ __launch_bounds__(4 * D) void kda_layer_step_kernel(
 
 template <int D>
 static int launch_step(int K, int B, int H, float lb, float eps, float qs, const float *Cin, long ldc,
-                       int bcol, const float *Cz, const float *gl, int gsplit, long gplane,
+                       int bcol, int facol, const uint16_t *Wfb, const float *gl, int gsplit, long gplane,
                        const float *q_conv, const float *k_conv, const float *v_conv,
                        const float *A_log, const float *dt_bias, const float *o_norm, float *states,
                        long stride, float *y, hipStream_t st)
 {
 #define K3_STEP(KK)                                                                              \
     hipLaunchKernelGGL((kda_layer_step_kernel<D, KK>), dim3(H, B), dim3(4 * D), 0, st, H, lb, eps, qs, \
-                       Cin, ldc, bcol, Cz, gl, gsplit, gplane, q_conv, k_conv, v_conv, A_log,    \
+                       Cin, ldc, bcol, facol, Wfb, gl, gsplit, gplane, q_conv, k_conv, v_conv, A_log, \
                        dt_bias, o_norm, states, stride, y)
     switch (K) {
     case 1: K3_STEP(1); break;
@@ -185,20 +232,20 @@ static int launch_step(int K, int B, int H, float lb, float eps, float qs, const
 }
 
 int layer_step(int B, int H, int D, int K, float lb, float eps, float q_scale, const float *Cin,
-               long ldc, int bcol, const float *Cz, const float *gl, int gsplit, long gplane,
+               long ldc, int bcol, int facol, const uint16_t *Wfb, const float *gl, int gsplit, long gplane,
                const float *q_conv, const float *k_conv, const float *v_conv, const float *A_log,
                const float *dt_bias, const float *o_norm, float *states, long stride, float *y,
                hipStream_t st)
 {
     if (B <= 0 || H <= 0) return K3HIP_OK;
     if (gsplit < 1 || ((uintptr_t)gl & 15) || (gplane & 3) || ((uintptr_t)y & 15) || ((uintptr_t)states & 15) ||
-        (stride & 3))
-        K3_FAIL(K3HIP_EINVAL, "layer step: gate planes, y or states misaligned");
+        (stride & 3) || ((uintptr_t)Wfb & 15) || (D & 7))
+        K3_FAIL(K3HIP_EINVAL, "layer step: gate planes, y, states or W_fb misaligned");
     switch (D) {
-    case 16: return launch_step<16>(K, B, H, lb, eps, q_scale, Cin, ldc, bcol, Cz, gl, gsplit, gplane, q_conv, k_conv, v_conv, A_log, dt_bias, o_norm, states, stride, y, st);
-    case 32: return launch_step<32>(K, B, H, lb, eps, q_scale, Cin, ldc, bcol, Cz, gl, gsplit, gplane, q_conv, k_conv, v_conv, A_log, dt_bias, o_norm, states, stride, y, st);
-    case 64: return launch_step<64>(K, B, H, lb, eps, q_scale, Cin, ldc, bcol, Cz, gl, gsplit, gplane, q_conv, k_conv, v_conv, A_log, dt_bias, o_norm, states, stride, y, st);
-    case 128: return launch_step<128>(K, B, H, lb, eps, q_scale, Cin, ldc, bcol, Cz, gl, gsplit, gplane, q_conv, k_conv, v_conv, A_log, dt_bias, o_norm, states, stride, y, st);
+    case 16: return launch_step<16>(K, B, H, lb, eps, q_scale, Cin, ldc, bcol, facol, Wfb, gl, gsplit, gplane, q_conv, k_conv, v_conv, A_log, dt_bias, o_norm, states, stride, y, st);
+    case 32: return launch_step<32>(K, B, H, lb, eps, q_scale, Cin, ldc, bcol, facol, Wfb, gl, gsplit, gplane, q_conv, k_conv, v_conv, A_log, dt_bias, o_norm, states, stride, y, st);
+    case 64: return launch_step<64>(K, B, H, lb, eps, q_scale, Cin, ldc, bcol, facol, Wfb, gl, gsplit, gplane, q_conv, k_conv, v_conv, A_log, dt_bias, o_norm, states, stride, y, st);
+    case 128: return launch_step<128>(K, B, H, lb, eps, q_scale, Cin, ldc, bcol, facol, Wfb, gl, gsplit, gplane, q_conv, k_conv, v_conv, A_log, dt_bias, o_norm, states, stride, y, st);
     default: K3_FAIL(K3HIP_EUNSUPPORTED, "layer step: D=%d not in {16,32,64,128}", D);
     }
 }
