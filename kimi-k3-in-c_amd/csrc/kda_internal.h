@@ -86,10 +86,13 @@ int rows_frag_pack(const uint16_t *W, int N, int K, uint16_t *Wf, hipStream_t st
 // registers so products keep fp32 accuracy; built for few rows (decode batches), bound by
 // reading W once. K % 8 == 0, ldx % 4 == 0, x and Wf 16-byte aligned. Stream-ordered.
 // Split-K partials go to ws (16-byte aligned, at least gemm_rows_ws_floats(B, N, K) floats);
-// with ws == nullptr or too small they are allocated on `st` for the call.
+// with ws == nullptr or too small they are allocated on `st` for the call. c_zeroed: C
+// already holds zeros; with exactly two K-ranges they are then added into C by atomics (the
+// same bits: a two-term sum does not depend on order) instead of a workspace and a second
+// launch.
 size_t gemm_rows_ws_floats(int B, int N, int K);
 int gemm_rows(int B, int N, int K, const float *x, long ldx, const uint16_t *Wf, float *C, long ldc,
-              hipStream_t st, float *ws = nullptr, size_t ws_floats = 0);
+              hipStream_t st, float *ws = nullptr, size_t ws_floats = 0, bool c_zeroed = false);
 // The same product left as its S = gemm_rows_splits(N, K) K-range partials: planes
 // P[s][B][N], whose sum in increasing s is C bit for bit, for a consumer that adds them
 // itself instead of a reduction launch.
@@ -114,11 +117,12 @@ int mla_attention(int B, int H, int KL, int CW, int Tn, int cap, float scale, co
 // gl the output-gate logits as
 // gsplit planes of gplane floats. states: per sequence (stride floats apart) the H D x D
 // state, then the [3][P][conv_k-1] conv history; both updated in place. y [B][P] out.
+// zout (may be nullptr): zn floats the kernel sets to zero on the way.
 int layer_step(int B, int H, int D, int K, float lb, float eps, float q_scale, const float *Cin,
                long ldc, int bcol, int facol, const uint16_t *Wfb, const float *gl, int gsplit, long gplane,
                const float *q_conv, const float *k_conv, const float *v_conv, const float *A_log,
                const float *dt_bias, const float *o_norm, float *states, long stride, float *y,
-               hipStream_t st);
+               float *zout, long zn, hipStream_t st);
 
 // p[0..n) = 0 on `st` with a kernel (never a memset node).
 int zero_fill(float *p, size_t n, hipStream_t st);

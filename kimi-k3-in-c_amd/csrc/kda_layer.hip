@@ -618,12 +618,15 @@ static int layer_decode_impl(const k3hip_kda_weights *w, int B, float *out, cons
     if ((rc = gemm_rows(B, NI, E, x, E, Win, Cin, ldi, st, ws, wsf))) return rc;
     if ((rc = gemm_rows_part(B, (int)P, E, x, E, Wg, glp, st))) return rc;
     // 2-8 the f_b product, K1, K3 and K4 on one token per sequence (kda_step.hip), conv
-    //   history and state in each slot, then 9 o_proj
+    //   history and state in each slot, then 9 o_proj: when it runs as two K-ranges, the
+    //   step kernel zeroes `out` and both ranges add into it (no reduction launch)
+    const bool oz = gemm_rows_splits(E, (int)P) == 2;
     if ((rc = layer_step(B, H, D, K, w->gate_lb, w->rms_eps, 1.0f / sqrtf((float)D), Cin, ldi,
                          3 * (int)P + D, 3 * (int)P, Wfb, glp, gs, (long)BP, w->q_conv, w->k_conv, w->v_conv,
-                         w->A_log, w->dt_bias, w->o_norm, states, state_stride, y, st)))
+                         w->A_log, w->dt_bias, w->o_norm, states, state_stride, y, oz ? out : nullptr,
+                         oz ? (long)B * E : 0, st)))
         return rc;
-    return gemm_rows(B, E, (int)P, y, (long)P, Wo, out, E, st, ws, wsf);
+    return gemm_rows(B, E, (int)P, y, (long)P, Wo, out, E, st, ws, wsf, oz);
 }
 
 extern "C" int k3hip_kda_layer_decode(const k3hip_kda_weights *w, int B, float *out, const float *x,

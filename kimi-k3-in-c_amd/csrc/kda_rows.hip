@@ -25,7 +25,9 @@
 // column block (split-K) is chosen so that a launch has about one workgroup per CU: wide N
 // runs unsplit, narrow N splits K. The eight wave partials meet in LDS and are summed in a
 // fixed order; K-range partials go to a workspace and a second kernel sums them in range
-// order. Results are therefore reproducible bit for bit.
+// order. Results are therefore reproducible bit for bit. A caller that has zeroed C may let
+// two K-range partials be added into C with atomics instead (no workspace, no second
+// launch): a + b = b + a exactly, so the bits do not depend on which range lands first.
 #include <algorithm>
 
 #include "kda_internal.h"
@@ -64,7 +66,7 @@ __global__ void rows_frag_pack_kernel(const uint16_t *__restrict__ W, int N, int
 // MT = 16-row tiles of x (B <= 16 MT). Wave w takes K-steps tbeg + w, tbeg + w + 8, ...;
 // each step loads the 4 groups' fragments (4 x 1 KB) and the x slice, then runs the hi and
 // lo MFMAs. Out = P + s * split_stride, row stride ldp.
-template <int MT>
+template <int MT, bool ATOM>
 __global__ __launch_bounds__(64 * RT_WAVES) void rows_gemm_kernel(
     int B, int N, int K, int tchunk, const float *__restrict__ x, long ldx,
     const uint16_t *__restrict__ Wf, float *__restrict__ P, long ldp, long split_stride)
@@ -128,7 +130,7 @@ __global__ __launch_bounds__(64 * RT_WAVES) void rows_gemm_kernel(
         for (int mt = 0; mt < MT; mt++) red[w][j][mt][lane] = acc[j][mt];
     __syncthreads();
     if (w >= RT_NT) return;
-    float *out = P + (size_t)s * split_stride;
+    float *out = ATOM ? P : P + (size_t)s * split_stride;
     const int n = 16 * (RT_NT * nb + w) + r16;
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
@@ -138,7 +140,10 @@ __global__ __launch_bounds__(64 * RT_WAVES) void rows_gemm_kernel(
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const int m = 16 * mt + 4 * kg + e;   // MFMA C layout: lane n + 16 j holds rows 4j..4j+3
-            if (m < B && n < N) out[(size_t)m * ldp + n] = t[e];
+            if (m < B && n < N) {
+                if constexpr (ATOM) unsafeAtomicAdd(&out[(size_t)m * ldp + n], t[e]);
+                else out[(size_t)m * ldp + n] = t[e];
+            }
         }
     }
 }
@@ -179,11 +184,11 @@ __global__ void rows_reduce1_kernel(int B, int N, int S, const float *__restrict
     }
 }
 
-template <int MT>
+template <int MT, bool ATOM = false>
 int launch_rows(int B, int N, int K, int tchunk, int S, const float *x, long ldx, const uint16_t *Wf,
                 float *P, long ldp, long split_stride, hipStream_t st)
 {
-    hipLaunchKernelGGL((rows_gemm_kernel<MT>), dim3((N + 16 * RT_NT - 1) / (16 * RT_NT), S),
+    hipLaunchKernelGGL((rows_gemm_kernel<MT, ATOM>), dim3((N + 16 * RT_NT - 1) / (16 * RT_NT), S),
                        dim3(64 * RT_WAVES), 0, st, B, N, K, tchunk, x, ldx, Wf, P, ldp, split_stride);
     K3_LAUNCHED();
     return K3HIP_OK;
@@ -281,13 +286,26 @@ int gemm_rows_part(int B, int N, int K, const float *x, long ldx, const uint16_t
 }
 
 int gemm_rows(int B, int N, int K, const float *x, long ldx, const uint16_t *Wf, float *C, long ldc,
-              hipStream_t st, float *ws, size_t ws_floats)
+              hipStream_t st, float *ws, size_t ws_floats, bool c_zeroed)
 {
     if (B <= 0 || N <= 0 || K <= 0) return K3HIP_OK;
     if ((K & 7) || (ldx & 3) || (((uintptr_t)x | (uintptr_t)Wf) & 15))
         K3_FAIL(K3HIP_EINVAL, "gemm_rows: K=%d ldx=%ld need multiples of 8 / 4 and 16-byte aligned x, W", K, ldx);
     const RowsPlan pl = rows_plan(N, K);
     const int S = pl.S, tchunk = pl.tchunk;
+    if (c_zeroed && S == 2) {   // the two K-range partials are added into C in place
+        for (int b0 = 0; b0 < B; b0 += 64) {
+            const int bb = std::min(64, B - b0);
+            const float *xb = x + (size_t)b0 * ldx;
+            float *Cb = C + (size_t)b0 * ldc;
+            int rc;
+            if (bb <= 16) rc = launch_rows<1, true>(bb, N, K, tchunk, S, xb, ldx, Wf, Cb, ldc, 0, st);
+            else if (bb <= 32) rc = launch_rows<2, true>(bb, N, K, tchunk, S, xb, ldx, Wf, Cb, ldc, 0, st);
+            else rc = launch_rows<4, true>(bb, N, K, tchunk, S, xb, ldx, Wf, Cb, ldc, 0, st);
+            if (rc) return rc;
+        }
+        return K3HIP_OK;
+    }
     const size_t need = gemm_rows_ws_floats(B, N, K);
     StreamBuf own;
     if (need && (!ws || ws_floats < need || ((uintptr_t)ws & 15))) {

@@ -42,7 +42,7 @@ __global__ __launch_bounds__(4 * D) void kda_layer_step_kernel(
     const float *__restrict__ q_conv, const float *__restrict__ k_conv,
     const float *__restrict__ v_conv, const float *__restrict__ A_log,
     const float *__restrict__ dt_bias, const float *__restrict__ o_norm,
-    float *__restrict__ states, long stride, float *__restrict__ y)
+    float *__restrict__ states, long stride, float *__restrict__ y, float *__restrict__ zout, long zn)
 {
 #pragma clang fp contract(off)
     constexpr int NT = 4 * D;
@@ -84,6 +84,14 @@ __global__ __launch_bounds__(4 * D) void kda_layer_step_kernel(
                 fxb[t] = f4{fa[k + 4], fa[k + 5], fa[k + 6], fa[k + 7]};
             }
         }
+    }
+
+    // zout[0 .. zn) = 0 for the o_proj product that adds its two K-range partials there
+    // (stream-ordered after every reader of the layer input), spread over the grid
+    if (zout) {
+        const long nwg = (long)gridDim.x * gridDim.y, id = (long)b * gridDim.x + h;
+        const long per = (zn + nwg - 1) / nwg, z0 = id * per, z1 = min(zn, z0 + per);
+        for (long i = z0 + tid; i < z1; i += NT) zout[i] = 0.0f;
     }
 
     // then the state: its latency overlaps the z product and the K1 arithmetic below
@@ -213,12 +221,12 @@ static int launch_step(int K, int B, int H, float lb, float eps, float qs, const
                        int bcol, int facol, const uint16_t *Wfb, const float *gl, int gsplit, long gplane,
                        const float *q_conv, const float *k_conv, const float *v_conv,
                        const float *A_log, const float *dt_bias, const float *o_norm, float *states,
-                       long stride, float *y, hipStream_t st)
+                       long stride, float *y, float *zout, long zn, hipStream_t st)
 {
 #define K3_STEP(KK)                                                                              \
     hipLaunchKernelGGL((kda_layer_step_kernel<D, KK>), dim3(H, B), dim3(4 * D), 0, st, H, lb, eps, qs, \
                        Cin, ldc, bcol, facol, Wfb, gl, gsplit, gplane, q_conv, k_conv, v_conv, A_log, \
-                       dt_bias, o_norm, states, stride, y)
+                       dt_bias, o_norm, states, stride, y, zout, zn)
     switch (K) {
     case 1: K3_STEP(1); break;
     case 2: K3_STEP(2); break;
@@ -235,17 +243,17 @@ int layer_step(int B, int H, int D, int K, float lb, float eps, float q_scale, c
                long ldc, int bcol, int facol, const uint16_t *Wfb, const float *gl, int gsplit, long gplane,
                const float *q_conv, const float *k_conv, const float *v_conv, const float *A_log,
                const float *dt_bias, const float *o_norm, float *states, long stride, float *y,
-               hipStream_t st)
+               float *zout, long zn, hipStream_t st)
 {
     if (B <= 0 || H <= 0) return K3HIP_OK;
     if (gsplit < 1 || ((uintptr_t)gl & 15) || (gplane & 3) || ((uintptr_t)y & 15) || ((uintptr_t)states & 15) ||
         (stride & 3) || ((uintptr_t)Wfb & 15) || (D & 7))
         K3_FAIL(K3HIP_EINVAL, "layer step: gate planes, y, states or W_fb misaligned");
     switch (D) {
-    case 16: return launch_step<16>(K, B, H, lb, eps, q_scale, Cin, ldc, bcol, facol, Wfb, gl, gsplit, gplane, q_conv, k_conv, v_conv, A_log, dt_bias, o_norm, states, stride, y, st);
-    case 32: return launch_step<32>(K, B, H, lb, eps, q_scale, Cin, ldc, bcol, facol, Wfb, gl, gsplit, gplane, q_conv, k_conv, v_conv, A_log, dt_bias, o_norm, states, stride, y, st);
-    case 64: return launch_step<64>(K, B, H, lb, eps, q_scale, Cin, ldc, bcol, facol, Wfb, gl, gsplit, gplane, q_conv, k_conv, v_conv, A_log, dt_bias, o_norm, states, stride, y, st);
-    case 128: return launch_step<128>(K, B, H, lb, eps, q_scale, Cin, ldc, bcol, facol, Wfb, gl, gsplit, gplane, q_conv, k_conv, v_conv, A_log, dt_bias, o_norm, states, stride, y, st);
+    case 16: return launch_step<16>(K, B, H, lb, eps, q_scale, Cin, ldc, bcol, facol, Wfb, gl, gsplit, gplane, q_conv, k_conv, v_conv, A_log, dt_bias, o_norm, states, stride, y, zout, zn, st);
+    case 32: return launch_step<32>(K, B, H, lb, eps, q_scale, Cin, ldc, bcol, facol, Wfb, gl, gsplit, gplane, q_conv, k_conv, v_conv, A_log, dt_bias, o_norm, states, stride, y, zout, zn, st);
+    case 64: return launch_step<64>(K, B, H, lb, eps, q_scale, Cin, ldc, bcol, facol, Wfb, gl, gsplit, gplane, q_conv, k_conv, v_conv, A_log, dt_bias, o_norm, states, stride, y, zout, zn, st);
+    case 128: return launch_step<128>(K, B, H, lb, eps, q_scale, Cin, ldc, bcol, facol, Wfb, gl, gsplit, gplane, q_conv, k_conv, v_conv, A_log, dt_bias, o_norm, states, stride, y, zout, zn, st);
     default: K3_FAIL(K3HIP_EUNSUPPORTED, "layer step: D=%d not in {16,32,64,128}", D);
     }
 }
