@@ -120,17 +120,19 @@ __global__ void mla_softmax_kernel(float *__restrict__ S, int n, int ld, float s
 }
 
 // o = O2[b] + O2[B+b] (the halves of the batched W_UV GEMM), times sigmoid(g) when gated
-// (g row b at stride ldg), as fp32 rows of o [B][H*VH] for o_proj.
+// (g row b at stride ldg), as fp32 rows of o [B][H*VH] for o_proj; zout[0 .. zn) = 0 on the
+// way (may be nullptr) for an o_proj that adds its two K-range partials there.
 __global__ void mla_gate_kernel(const float *__restrict__ O2, const float *__restrict__ g, long ldg,
-                                int B, size_t HV, float *__restrict__ o)
+                                int B, size_t HV, float *__restrict__ o, float *__restrict__ zout, size_t zn)
 {
-    const size_t n = (size_t)B * HV;
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-         i += (size_t)gridDim.x * blockDim.x) {
+    const size_t n = (size_t)B * HV, step = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step) {
         float v = O2[i] + O2[n + i];
         if (g) v *= 1.0f / (1.0f + expf(-g[(i / HV) * ldg + i % HV]));
         o[i] = v;
     }
+    if (zout)
+        for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < zn; i += step) zout[i] = 0.0f;
 }
 
 // mla_softmax_kernel for rows of n <= 256 * RPT scores held in registers: one read and one
@@ -380,8 +382,11 @@ extern "C" int k3hip_mla_decode(const k3hip_mla_weights *w, int B, int pos, int 
     gu.lda = (long)H * KL; gu.ldb = KL; gu.ldc = HV; gu.batch = H;
     gu.sa = KL; gu.sb = (long)(QN + VH) * KL; gu.sc = VH;
     if ((rc = gemm(gu, ch2, kvb + (size_t)QN * KL, O2, st))) return rc;
+    // o_proj as two K-ranges adds into `out`, which the gate kernel zeroes (no reduction launch)
+    const bool oz = gemm_rows_splits(E, HV) == 2;
     hipLaunchKernelGGL(mla_gate_kernel, dim3(mla_grid((size_t)B * HV)), dim3(256), 0, st, O2,
-                       w->gate ? C1 + QL + CW : nullptr, ld1, B, (size_t)HV, o);
+                       w->gate ? C1 + QL + CW : nullptr, ld1, B, (size_t)HV, o, oz ? out : nullptr,
+                       oz ? (size_t)B * E : (size_t)0);
     K3_LAUNCHED();
-    return gemm_rows(B, E, HV, o, HV, (const uint16_t *)w->o, out, E, st, ws, wsf);
+    return gemm_rows(B, E, HV, o, HV, (const uint16_t *)w->o, out, E, st, ws, wsf, oz);
 }
