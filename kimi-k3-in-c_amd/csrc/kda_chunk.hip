@@ -611,7 +611,8 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra_act(
     extern __shared__ __attribute__((aligned(16))) float lds[];
     float *sG = lds + L::G, *sK = lds + L::K, *sX = lds + L::X, *sA = lds + L::A, *sB = lds + L::B;
     float *sV = lds + L::A;                    // v staging [CH][PD], aliases A and Tm
-    float *sW = lds + L::FLOATS;               // conv taps [3][D][4]
+    float *sW = lds + L::FLOATS;               // conv taps [3][4][D], tap-major: a lane's CPL
+                                               // channels of one tap are one conflict-free read
     float *sDT = sW + 3 * D * 4;               // dt_bias [D]
     float *sHist = lds + L::NS;                // incoming conv history [3][D][K-1] at chunk 0
 
@@ -666,8 +667,8 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra_act(
         const int m = lane & 15, kg = lane >> 4;
         const int c0 = (tid & 31) * CPL, r0 = (tid >> 5) * RL;
         if (h != head) {   // uniform: a new head's conv taps and dt_bias into LDS
-            for (int i = tid; i < 3 * D * 4; i += P1_THREADS) {
-                const int b = i / (D * 4), ch = (i / 4) % D, j = i % 4;
+            for (int i = tid; i < 3 * 4 * D; i += P1_THREADS) {
+                const int b = i / (4 * D), j = (i / D) % 4, ch = i % D;
                 sW[i] = j < K ? convw[b][((size_t)h * D + ch) * K + j] : 0.0f;
             }
             for (int i = tid; i < D; i += P1_THREADS) sDT[i] = dt_bias[(size_t)h * D + i];
@@ -686,12 +687,23 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra_act(
         // (1) prepare this half-wave's RL tokens from the prefetched raw rows
         float y[3][RL][CPL];
 #pragma unroll
-        for (int b = 0; b < 3; b++)
+        for (int b = 0; b < 3; b++) {
+            float wq[K][CPL];   // this lane's CPL channels of each tap
+#pragma unroll
+            for (int j = 0; j < K; j++) {
+                if constexpr (CPL == 4) {
+                    const f4 t4 = *reinterpret_cast<const f4 *>(&sW[(b * 4 + j) * D + c0]);
+                    wq[j][0] = t4.x; wq[j][1] = t4.y; wq[j][2] = t4.z; wq[j][3] = t4.w;
+                } else {
+                    const f2 t2 = *reinterpret_cast<const f2 *>(&sW[(b * 4 + j) * D + c0]);
+                    wq[j][0] = t2.x; wq[j][1] = t2.y;
+                }
+            }
 #pragma unroll
             for (int e = 0; e < CPL; e++) {
                 float wt[K], xs[NR];
 #pragma unroll
-                for (int j = 0; j < K; j++) wt[j] = sW[(b * D + c0 + e) * 4 + j];
+                for (int j = 0; j < K; j++) wt[j] = wq[j][e];
 #pragma unroll
                 for (int j = 0; j < NR; j++) {
                     if constexpr (DT == K3HIP_BF16) {
@@ -715,6 +727,7 @@ __global__ __launch_bounds__(P1_THREADS) void kda_chunk_intra_act(
 #pragma unroll
                 for (int r = 0; r < RL; r++) y[b][r][e] = conv_silu<K>(wt, &xs[r], xs[NH + r]);
             }
+        }
 #pragma unroll
         for (int r = 0; r < RL; r++) {
             l2norm_half<CPL>(y[0][r]);
