@@ -981,11 +981,21 @@ __device__ __forceinline__ void state_update(const StateOps<D> &op, f32x4 (&accS
     }
 }
 
+// The outgoing short-conv history of the fused prefill (conv_state_update's result), formed
+// by phase 2's state waves: each of the first 3 P of them loads one channel's K-1 newest
+// inputs (or, for T < K-1, the older history slots that shift down) before its loop and
+// stores them after it, off the critical path. Phase 1 has read the incoming history by then.
+struct ConvOut {
+    const void *qi, *ki, *vi;   // raw conv inputs [T][P] (bf16 or fp32, dt)
+    float *cs;                  // [3][P][K-1], nullptr: nothing to do
+    int K, dt;
+};
+
 // --- phase 2 kernel: one workgroup per (head, NW consecutive 16-column tiles of S) ---
 template <int D, int NW>
 __global__ __launch_bounds__(512) void kda_chunk_state(int T, int H, const char *__restrict__ ws,
                                                        float *__restrict__ S,
-                                                       float *__restrict__ o)
+                                                       float *__restrict__ o, ConvOut co)
 {
     using WL = Ws<D>;
     constexpr int NG = D / 16 / NW;      // workgroups per head
@@ -1068,6 +1078,23 @@ __global__ __launch_bounds__(512) void kda_chunk_state(int T, int H, const char 
             for (int i = 0; i < TPL; i++) asm volatile("" ::"v"(t[i]));
         };
         int tA[TPL], tB[TPL];
+        // this thread's channel of the outgoing conv history (one per state-wave thread
+        // suffices: 3 H D <= 256 H D / 16)
+        const int NHc = co.K - 1;
+        const long chbc = (long)blockIdx.x * 256 + (threadIdx.x - 256);
+        const bool chdo = co.cs && NHc > 0 && chbc < 3L * (long)P;
+        float chv[3] = {0.0f, 0.0f, 0.0f};
+        if (chdo) {
+            const int cb = (int)(chbc / (long)P);
+            const size_t cc = (size_t)(chbc % (long)P);
+            const void *src = cb == 0 ? co.qi : (cb == 1 ? co.ki : co.vi);
+            for (int j = 0; j < NHc; j++) {
+                const int p = T - NHc + j;
+                chv[j] = p >= 0 ? (co.dt == K3HIP_BF16 ? load_act<K3HIP_BF16>(src, (size_t)p * P + cc)
+                                                       : load_act<K3HIP_F32>(src, (size_t)p * P + cc))
+                                : co.cs[chbc * NHc + j + T];   // T < K-1: an older slot shifts down
+            }
+        }
         f32x4 accS[RTW][NW];
 #pragma unroll
         for (int j = 0; j < NW; j++)
@@ -1111,6 +1138,8 @@ __global__ __launch_bounds__(512) void kda_chunk_state(int T, int H, const char 
 #pragma unroll
                 for (int e = 0; e < 4; e++)
                     Sh[(size_t)(16 * (RTW * sw + r) + 4 * kg + e) * D + j0 + 16 * j + m] = accS[r][j][e];
+        if (chdo)
+            for (int j = 0; j < NHc; j++) co.cs[chbc * NHc + j] = chv[j];
     }
 }
 
@@ -1146,13 +1175,13 @@ static int allow_lds(const void *fn, size_t bytes, bool &done)
 }
 
 template <int D, int NW>
-static int launch_state_nw(int T, int H, const char *ws, float *S, float *o, hipStream_t st)
+static int launch_state_nw(int T, int H, const char *ws, float *S, float *o, const ConvOut &co, hipStream_t st)
 {
     const size_t lds = (size_t)NW * (P2Lds<D>::SF + P2Lds<D>::VF);
     static bool lds_ok = false;
     int rc;
     if ((rc = allow_lds((const void *)kda_chunk_state<D, NW>, lds, lds_ok))) return rc;
-    hipLaunchKernelGGL((kda_chunk_state<D, NW>), dim3(H * (D / 16 / NW)), dim3(512), lds, st, T, H, ws, S, o);
+    hipLaunchKernelGGL((kda_chunk_state<D, NW>), dim3(H * (D / 16 / NW)), dim3(512), lds, st, T, H, ws, S, o, co);
     K3_LAUNCHED();
     return K3HIP_OK;
 }
@@ -1162,9 +1191,10 @@ static int launch_state_nw(int T, int H, const char *ws, float *S, float *o, hip
 // operands of the whole head are needed by every tile), not by the redundant copies that
 // the head's other workgroups load from the same L2.
 template <int D>
-static int launch_state(int T, int H, const char *ws, float *S, float *o, hipStream_t st)
+static int launch_state(int T, int H, const char *ws, float *S, float *o, hipStream_t st,
+                        const ConvOut &co = ConvOut{nullptr, nullptr, nullptr, nullptr, 0, 0})
 {
-    return launch_state_nw<D, 1>(T, H, ws, S, o, st);
+    return launch_state_nw<D, 1>(T, H, ws, S, o, co, st);
 }
 
 template <int D>
@@ -1209,9 +1239,8 @@ static int launch_prefill(const PrefillArgs &a, hipStream_t st)
                        a.H, a.qs, a.lb, a.qi, a.ki, a.vi, a.z, a.bl, a.qc, a.kc, a.vc, a.A, a.dt,
                        a.cs, a.ws);
     K3_LAUNCHED();
-    // the outgoing conv history, after the kernel above has read the incoming one
-    if ((rc = conv_state_update(a.T, a.H * D, K, DT, a.qi, a.ki, a.vi, a.cs, st))) return rc;
-    return launch_state<D>(a.T, a.H, a.ws, a.S, a.o, st);
+    // phase 2 also writes the outgoing conv history (the kernel above has read the incoming one)
+    return launch_state<D>(a.T, a.H, a.ws, a.S, a.o, st, ConvOut{a.qi, a.ki, a.vi, a.cs, K, DT});
 }
 
 template <int D, int DT>
