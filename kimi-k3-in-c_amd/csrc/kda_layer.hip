@@ -553,11 +553,12 @@ extern "C" int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *
 
 // ------------------------------------------------------------- batched decode ----
 // One token for each of B sequences: projections on the fragment-ordered decode copies,
-// then the fused K1 + K3 + K4 step kernel, then o_proj. Five launches per layer step.
+// then the fused f_b + K1 + K3 + K4 step kernel, then o_proj. Four launches per layer step.
 // The batched decode step with its scratch either allocated per call on the stream (scr ==
 // nullptr) or taken from the caller's scr (scr_bytes, 256-byte aligned). Nothing in the
 // scratch has to start at zero: every element a kernel reads was written earlier in the
-// same call (the projections, the split-K partial planes, z, y).
+// same call (the projections, the split-K partial planes, y). The layer output is zeroed by
+// the step kernel when o_proj adds its two K-ranges into it.
 static int layer_decode_impl(const k3hip_kda_weights *w, int B, float *out, const float *x, float *states,
                              long state_stride, void *stream, char *scr, size_t scr_bytes, const char *who)
 {
