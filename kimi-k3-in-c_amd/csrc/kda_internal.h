@@ -87,9 +87,10 @@ int rows_frag_pack(const uint16_t *W, int N, int K, uint16_t *Wf, hipStream_t st
 // reading W once. K % 8 == 0, ldx % 4 == 0, x and Wf 16-byte aligned. Stream-ordered.
 // Split-K partials go to ws (16-byte aligned, at least gemm_rows_ws_floats(B, N, K) floats);
 // with ws == nullptr or too small they are allocated on `st` for the call. c_zeroed: C
-// already holds zeros; with exactly two K-ranges they are then added into C by atomics (the
-// same bits: a two-term sum does not depend on order) instead of a workspace and a second
-// launch.
+// already holds zeros; with exactly two K-ranges they are then added into C by atomics
+// instead of a workspace and a second launch. Reproducible: a two-term sum does not depend
+// on which range lands first (and equals the reduction kernel's a + b unless a partial is
+// denormal, which the atomic unit may flush).
 size_t gemm_rows_ws_floats(int B, int N, int K);
 int gemm_rows(int B, int N, int K, const float *x, long ldx, const uint16_t *Wf, float *C, long ldc,
               hipStream_t st, float *ws = nullptr, size_t ws_floats = 0, bool c_zeroed = false);
