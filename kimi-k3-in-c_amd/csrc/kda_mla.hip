@@ -57,14 +57,23 @@ __device__ __forceinline__ double block_sum(double v, double *red)
 // Row b of C (row stride ldc): rmsnorm over the first nn of its N entries (weight w,
 // src/core/k3_ops.c:94-102; double mean of squares, eps inside), the rest copied; written
 // as fp32 row b of y [B][N] (y != nullptr) or to cache row b at position pos
-// (cache [B][cap][N]).
-__global__ void mla_norm_kernel(const float *__restrict__ C, long ldc, int N, int nn,
-                                const float *__restrict__ w, float eps, float *__restrict__ y,
-                                float *__restrict__ cache, long cap, int pos)
+// (cache [B][cap][N]). Two independent norms share one launch: blockIdx.y picks the job.
+struct NormJob {
+    const float *C;
+    int N, nn;
+    const float *w;
+    float *y, *cache;
+};
+__global__ void mla_norm_kernel(long ldc, float eps, NormJob j0, NormJob j1, long cap, int pos)
 {
     __shared__ double red[16];
+    const NormJob &jb = blockIdx.y == 0 ? j0 : j1;
+    const float *__restrict__ w = jb.w;
+    float *__restrict__ y = jb.y;
+    float *__restrict__ cache = jb.cache;
+    const int N = jb.N, nn = jb.nn;
     const int b = blockIdx.x;
-    const float *r0 = C + (size_t)b * ldc;
+    const float *r0 = jb.C + (size_t)b * ldc;
     double ss = 0.0;
     for (int n = threadIdx.x; n < nn; n += blockDim.x) {
         const double v = (double)r0[n];
@@ -326,14 +335,13 @@ extern "C" int k3hip_mla_decode(const k3hip_mla_weights *w, int B, int pos, int 
     // q_a, kv_a and g in one pass over their weights (fp32 x split hi/lo in registers);
     // q = q_b(rmsnorm(q_a x)); latent + rope = kv_a x, the latent rmsnorm'd into the cache
     if ((rc = gemm_rows(B, N1, E, x, E, (const uint16_t *)w->xin, C1, ld1, st, ws, wsf))) return rc;
-    hipLaunchKernelGGL(mla_norm_kernel, dim3(B), dim3(256), 0, st, C1, ld1, QL, QL, w->q_a_norm, w->eps,
-                       qn, (float *)nullptr, 0L, 0);
+    // the q_a rmsnorm into qn and the latent rmsnorm into the cache, one launch
+    hipLaunchKernelGGL(mla_norm_kernel, dim3(B, 2), dim3(256), 0, st, ld1, w->eps,
+                       NormJob{C1, QL, QL, w->q_a_norm, qn, nullptr},
+                       NormJob{C1 + QL, CW, KL, w->kv_a_norm, nullptr, cache}, (long)cap, pos);
     K3_LAUNCHED();
     if ((rc = gemm_rows(B, H * QH, QL, qn, QL, (const uint16_t *)w->q_b, q, (long)H * QH, st, ws, wsf)))
         return rc;
-    hipLaunchKernelGGL(mla_norm_kernel, dim3(B), dim3(256), 0, st, C1 + QL, ld1, CW, KL, w->kv_a_norm,
-                       w->eps, (float *)nullptr, cache, (long)cap, pos);
-    K3_LAUNCHED();
     // absorb: per head h, [q hi; lo] (2B x QN) . W_UK_h (QN x KL), batched over heads
     if ((rc = split_rows2(q, qs2, B, H * QH, st))) return rc;
     GemmDesc ga;
