@@ -101,15 +101,17 @@ int gemm_rows_splits(int N, int K);
 int gemm_rows_part(int B, int N, int K, const float *x, long ldx, const uint16_t *Wf, float *P, hipStream_t st);
 
 // Attention of an absorbed MLA decode step (kda_mla_attn.hip) in one pass over the cache:
-// qcat [B][H][CW] fp32, cache [B][cap][CW] fp32 (latent = channels 0..KL-1), positions
-// 0..Tn-1; writes chat = softmax(scale qcat . cache^T) . latent as bf16 hi (rows 0..B-1)
-// and lo (rows B..2B-1) of ch2 [2B][H KL]. Shapes: mla_attention_supported (H <= 64, KL a
-// multiple of 16 up to 512, CW a multiple of 4 up to 576). ws: mla_attention_ws_bytes
-// bytes, 256-byte aligned; qcat and cache 16-byte aligned.
+// the query rows qcat[b][h] = [A2[b][h] + A2[B+b][h] | q_rope(b, h)] are formed in the kernel
+// from the absorb GEMM's hi/lo halves A2 [2B][H CW] (first KL of each head's CW columns) and
+// q [B][H][QN + CW - KL] (rope at column QN); cache [B][cap][CW] fp32 (latent = channels
+// 0..KL-1), positions 0..Tn-1; writes chat = softmax(scale qcat . cache^T) . latent as bf16
+// hi (rows 0..B-1) and lo (rows B..2B-1) of ch2 [2B][H KL]. Shapes: mla_attention_supported
+// (H <= 64, KL a multiple of 16 up to 512, CW a multiple of 4 up to 576) and QN % 4 == 0.
+// ws: mla_attention_ws_bytes bytes, 256-byte aligned; A2, q and cache 16-byte aligned.
 bool mla_attention_supported(int H, int KL, int CW);
 size_t mla_attention_ws_bytes(int B, int H, int KL, int Tn);
-int mla_attention(int B, int H, int KL, int CW, int Tn, int cap, float scale, const float *qcat,
-                  const float *cache, uint16_t *ch2, void *ws, size_t ws_bytes, hipStream_t st);
+int mla_attention(int B, int H, int KL, int CW, int Tn, int cap, float scale, const float *A2, const float *q,
+                  int QN, const float *cache, uint16_t *ch2, void *ws, size_t ws_bytes, hipStream_t st);
 
 // One decode token of a KDA layer between its projections (kda_step.hip): K1 + K3 + K4 per
 // (head, sequence). Cin rows (stride ldc) hold q | k | v at columns 0, P, 2P and the beta

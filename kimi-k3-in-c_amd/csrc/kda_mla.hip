@@ -301,7 +301,7 @@ extern "C" int k3hip_mla_decode(const k3hip_mla_weights *w, int B, int pos, int 
         K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_mla_decode: q_lora=%d, heads*v_head=%d not multiples of 8", QL, HV);
     // attention in one pass over the cache (kda_mla_attn.hip) where the shape fits it, else
     // as two strided-batched fp32 GEMMs around the softmax
-    const bool fused = mla_attention_supported(H, KL, CW) && !((uintptr_t)cache & 15);
+    const bool fused = mla_attention_supported(H, KL, CW) && !((uintptr_t)cache & 15) && !(QN & 3);
     // scratch: q_a kv_a g projections [B][ld1] | q_a normed | q | q hi/lo | absorb halves | qcat |
     //          scores or the fused attention's workspace | chat | chat hi/lo | W_UV halves | o |
     //          split-K partials
@@ -349,15 +349,16 @@ extern "C" int k3hip_mla_decode(const k3hip_mla_weights *w, int B, int pos, int 
     ga.lda = (long)H * QH; ga.ldb = KL; ga.ldc = (long)H * CW; ga.batch = H;
     ga.sa = QH; ga.sb = (long)(QN + VH) * KL; ga.sc = CW;
     if ((rc = gemm(ga, qs2, kvb, A2, st))) return rc;
-    hipLaunchKernelGGL(mla_qcat_kernel, dim3(mla_grid((size_t)B * H * CW)), dim3(256), 0, st, A2, q, B, H,
-                       QN, QR, KL, qcat);
-    K3_LAUNCHED();
     if (fused) {
-        // chat as the bf16 hi/lo rows of the W_UV GEMM, straight from the attention
-        if ((rc = mla_attention(B, H, KL, CW, Tn, cap, 1.0f / sqrtf((float)QH), qcat, cache, ch2, S,
+        // the query rows formed inside the attention from A2 and q; chat as the bf16 hi/lo
+        // rows of the W_UV GEMM, straight from the attention
+        if ((rc = mla_attention(B, H, KL, CW, Tn, cap, 1.0f / sqrtf((float)QH), A2, q, QN, cache, ch2, S,
                                 mla_attention_ws_bytes(B, H, KL, Tn), st)))
             return rc;
     } else {
+        hipLaunchKernelGGL(mla_qcat_kernel, dim3(mla_grid((size_t)B * H * CW)), dim3(256), 0, st, A2, q, B, H,
+                           QN, QR, KL, qcat);
+        K3_LAUNCHED();
         // scores S_b [H][Tn] = qcat_b [H][CW] . cache_b[0..Tn)^T, per sequence
         GemmDesc gs;
         gs.M = H; gs.N = Tn; gs.K = CW; gs.ab_dtype = K3HIP_F32; gs.c_dtype = K3HIP_F32; gs.b_trans = true;

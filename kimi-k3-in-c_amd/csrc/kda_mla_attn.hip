@@ -70,6 +70,14 @@ struct AtGeom {
     int H, CW, KL;
 };
 
+// Where the query rows come from: qcat[b][h] = [A2[b][h] + A2[B+b][h] (the hi and lo halves
+// of the batched absorb GEMM, KL floats) | q_rope(b, h) (q [B][H][QH] at column QN)], formed
+// while the q fragments are loaded (the same fp32 sums a separate qcat pass would store).
+struct AtQ {
+    const float *A2, *q;
+    int B, QN, QH;
+};
+
 __device__ __forceinline__ void split2(float a, float b, bf16x2 &hi, bf16x2 &lo)
 {
     hi = __builtin_convertvector(f2{a, b}, bf16x2);
@@ -105,7 +113,7 @@ __device__ __forceinline__ f32x4 mma3_16(f32x4 acc, const s16x4 &ah, const s16x4
 // FULL: kv_lora + rope = 576, every staging unit of a row exists.
 template <bool FULL>
 __global__ __launch_bounds__(AT_NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void mla_attn_kernel(
-    AtGeom g, int Tn, int cap, int nsplit, float scale2, const float *__restrict__ qcat,
+    AtGeom g, int Tn, int cap, int nsplit, float scale2, AtQ qs,
     const float *__restrict__ cache, float *__restrict__ pctx, float *__restrict__ pm, float *__restrict__ pl)
 {
     extern __shared__ __attribute__((aligned(16))) uint16_t at_smem[];
@@ -127,10 +135,17 @@ __global__ __launch_bounds__(AT_NT) __attribute__((amdgpu_waves_per_eu(2, 2))) v
         float x[8];
         const int c = 32 * (AT_KSW * hf + i) + 8 * kg;
         const bool ok = h < H;
-        const float *src = qcat + ((size_t)b * H + (ok ? h : 0)) * CW;
+        const size_t bh = (size_t)b * H + (ok ? h : 0);
+        const float *a2 = qs.A2 + bh * CW, *a2lo = a2 + (size_t)qs.B * H * CW;
+        const float *qr = qs.q + bh * qs.QH + qs.QN - KL;   // q_rope(b, h) at channels KL ..
 #pragma unroll
         for (int e = 0; e < 8; e += 4) {
-            const f4 v = ok && c + e < CW ? *reinterpret_cast<const f4 *>(src + c + e) : f4{0.0f, 0.0f, 0.0f, 0.0f};
+            const int cc = c + e;   // KL % 16 == 0: a 4-channel group is wholly latent or rope
+            f4 v = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (ok && cc < CW) {
+                if (cc < KL) v = *reinterpret_cast<const f4 *>(a2 + cc) + *reinterpret_cast<const f4 *>(a2lo + cc);
+                else v = *reinterpret_cast<const f4 *>(qr + cc);
+            }
             x[e] = v.x; x[e + 1] = v.y; x[e + 2] = v.z; x[e + 3] = v.w;
         }
 #pragma unroll
@@ -370,8 +385,8 @@ bool mla_attention_supported(int H, int KL, int CW)
     return at_geom(H, KL, CW, g);
 }
 
-int mla_attention(int B, int H, int KL, int CW, int Tn, int cap, float scale, const float *qcat,
-                  const float *cache, uint16_t *ch2, void *ws, size_t ws_bytes, hipStream_t st)
+int mla_attention(int B, int H, int KL, int CW, int Tn, int cap, float scale, const float *A2, const float *q,
+                  int QN, const float *cache, uint16_t *ch2, void *ws, size_t ws_bytes, hipStream_t st)
 {
     AtGeom g;
     if (!at_geom(H, KL, CW, g))
@@ -379,8 +394,11 @@ int mla_attention(int B, int H, int KL, int CW, int Tn, int cap, float scale, co
     if (B <= 0 || Tn <= 0 || Tn > cap) K3_FAIL(K3HIP_EINVAL, "mla attention: B=%d Tn=%d cap=%d", B, Tn, cap);
     const int nsplit = at_nsplit(B, Tn);
     const size_t need = mla_attention_ws_bytes(B, H, KL, Tn);
-    if (!ws || ws_bytes < need || ((uintptr_t)ws & 255) || ((uintptr_t)cache & 15) || ((uintptr_t)qcat & 15))
+    const int QH = QN + (CW - KL);
+    if (!ws || ws_bytes < need || ((uintptr_t)ws & 255) || ((uintptr_t)cache & 15) || ((uintptr_t)A2 & 15) ||
+        ((uintptr_t)q & 15) || (QN & 3))
         K3_FAIL(K3HIP_EINVAL, "mla attention: workspace %zu < %zu bytes, or a misaligned buffer", ws_bytes, need);
+    const AtQ qs{A2, q, B, QN, QH};
     const size_t r = (size_t)B * nsplit * H;
     float *pctx = (float *)ws;
     float *pm = (float *)((char *)ws + ((r * KL * 4 + 255) & ~(size_t)255));
@@ -395,10 +413,10 @@ int mla_attention(int B, int H, int KL, int CW, int Tn, int cap, float scale, co
     }
     if (CW == 32 * AT_MAXKS)
         hipLaunchKernelGGL(mla_attn_kernel<true>, dim3(nsplit, B), dim3(AT_NT), AT_LDS, st, g, Tn, cap, nsplit,
-                           scale * AT_LOG2E, qcat, cache, pctx, pm, pl);
+                           scale * AT_LOG2E, qs, cache, pctx, pm, pl);
     else
         hipLaunchKernelGGL(mla_attn_kernel<false>, dim3(nsplit, B), dim3(AT_NT), AT_LDS, st, g, Tn, cap, nsplit,
-                           scale * AT_LOG2E, qcat, cache, pctx, pm, pl);
+                           scale * AT_LOG2E, qs, cache, pctx, pm, pl);
     K3_LAUNCHED();
     hipLaunchKernelGGL(mla_attn_merge_kernel, dim3(H, B), dim3(128), 0, st, B, H, KL, nsplit, pctx, pm, pl, ch2);
     K3_LAUNCHED();
