@@ -99,6 +99,13 @@ int gemm_rows(int B, int N, int K, const float *x, long ldx, const uint16_t *Wf,
 // itself instead of a reduction launch.
 int gemm_rows_splits(int N, int K);
 int gemm_rows_part(int B, int N, int K, const float *x, long ldx, const uint16_t *Wf, float *P, hipStream_t st);
+// gemm_rows of W1 (N1 columns into C1, row stride ldc1) and gemm_rows_part of W2 (N2 columns,
+// planes P2) over the same x in one launch when W1 runs unsplit: the two weights' workgroups
+// fill the GPU together and x is read by both in the same pass. The same bits as the two
+// calls; when W1 would split K, it is those two calls.
+int gemm_rows_with_part(int B, int K, const float *x, long ldx, int N1, const uint16_t *Wf1, float *C1, long ldc1,
+                        int N2, const uint16_t *Wf2, float *P2, hipStream_t st, float *ws = nullptr,
+                        size_t ws_floats = 0);
 
 // Attention of an absorbed MLA decode step (kda_mla_attn.hip) in one pass over the cache:
 // the query rows qcat[b][h] = [A2[b][h] + A2[B+b][h] | q_rope(b, h)] are formed in the kernel

@@ -552,8 +552,9 @@ extern "C" int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *
 }
 
 // ------------------------------------------------------------- batched decode ----
-// One token for each of B sequences: projections on the fragment-ordered decode copies,
-// then the fused f_b + K1 + K3 + K4 step kernel, then o_proj. Four launches per layer step.
+// One token for each of B sequences: the q/k/v/f_a/beta and output-gate projections in one
+// launch on the fragment-ordered decode copies, then the fused f_b + K1 + K3 + K4 step
+// kernel, then o_proj. Three launches per layer step (B <= 64).
 // The batched decode step with its scratch either allocated per call on the stream (scr ==
 // nullptr) or taken from the caller's scr (scr_bytes, 256-byte aligned). Nothing in the
 // scratch has to start at zero: every element a kernel reads was written earlier in the
@@ -616,8 +617,7 @@ static int layer_decode_impl(const k3hip_kda_weights *w, int B, float *out, cons
     //   (kda_rows.hip: x split into bf16 hi + lo in registers); q, k, v, f_a and the beta
     //   logits in one pass over their concatenated weights; the output gate left as split-K
     //   planes that the step kernel adds
-    if ((rc = gemm_rows(B, NI, E, x, E, Win, Cin, ldi, st, ws, wsf))) return rc;
-    if ((rc = gemm_rows_part(B, (int)P, E, x, E, Wg, glp, st))) return rc;
+    if ((rc = gemm_rows_with_part(B, E, x, E, NI, Win, Cin, ldi, (int)P, Wg, glp, st, ws, wsf))) return rc;
     // 2-8 the f_b product, K1, K3 and K4 on one token per sequence (kda_step.hip), conv
     //   history and state in each slot, then 9 o_proj: when it runs as two K-ranges, the
     //   step kernel zeroes `out` and both ranges add into it (no reduction launch)

@@ -62,19 +62,36 @@ __global__ void rows_frag_pack_kernel(const uint16_t *__restrict__ W, int N, int
     }
 }
 
-// Block (nb, s): column groups 4 nb .. 4 nb + 3, K-steps [s tchunk, min(KT, (s + 1) tchunk)).
-// MT = 16-row tiles of x (B <= 16 MT). Wave w takes K-steps tbeg + w, tbeg + w + 8, ...;
-// each step loads the 4 groups' fragments (4 x 1 KB) and the x slice, then runs the hi and
-// lo MFMAs. Out = P + s * split_stride, row stride ldp.
+// One weight's product in a launch: nb column blocks x S K-ranges of tchunk K-steps; the
+// outputs go to P + s * split_stride (row stride ldp).
+struct RowsJob {
+    int N, nb, S, tchunk;
+    const uint16_t *Wf;
+    float *P;
+    long ldp, split_stride;
+};
+
+// Block (nb, s) of a job: column groups 4 nb .. 4 nb + 3, K-steps [s tchunk, min(KT, (s + 1)
+// tchunk)). One launch may carry two jobs over the same x (the first j0.nb * j0.S blocks
+// are j0's). MT = 16-row tiles of x (B <= 16 MT). Wave w takes K-steps tbeg + w, tbeg + w +
+// 8, ...; each step loads the 4 groups' fragments (4 x 1 KB) and the x slice, then runs the
+// hi and lo MFMAs.
 template <int MT, bool ATOM>
-__global__ __launch_bounds__(64 * RT_WAVES) void rows_gemm_kernel(
-    int B, int N, int K, int tchunk, const float *__restrict__ x, long ldx,
-    const uint16_t *__restrict__ Wf, float *__restrict__ P, long ldp, long split_stride)
+__global__ __launch_bounds__(64 * RT_WAVES) void rows_gemm_kernel(int B, int K, const float *__restrict__ x,
+                                                                  long ldx, RowsJob j0, RowsJob j1)
 {
     __shared__ f32x4 red[RT_WAVES][RT_NT][MT][64];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int r16 = lane & 15, kg = lane >> 4;
-    const int nb = blockIdx.x, s = blockIdx.y;
+    const int n0 = j0.nb * j0.S;
+    const bool second = (int)blockIdx.x >= n0;
+    const RowsJob &jb = second ? j1 : j0;
+    const int lb = second ? (int)blockIdx.x - n0 : (int)blockIdx.x;
+    const int nb = lb % jb.nb, s = lb / jb.nb;
+    const int N = jb.N, tchunk = jb.tchunk;
+    const uint16_t *__restrict__ Wf = jb.Wf;
+    float *__restrict__ P = jb.P;
+    const long ldp = jb.ldp, split_stride = jb.split_stride;
     const int KT = (K + 31) / 32, NG = (N + 15) / 16;
     const int tbeg = s * tchunk, tend = min(KT, tbeg + tchunk);
 
@@ -184,14 +201,35 @@ __global__ void rows_reduce1_kernel(int B, int N, int S, const float *__restrict
     }
 }
 
+RowsJob rows_job(int N, int tchunk, int S, const uint16_t *Wf, float *P, long ldp, long split_stride)
+{
+    return RowsJob{N, (N + 16 * RT_NT - 1) / (16 * RT_NT), S, tchunk, Wf, P, ldp, split_stride};
+}
+
+template <int MT, bool ATOM = false>
+int launch_jobs(int B, int K, const float *x, long ldx, const RowsJob &j0, const RowsJob &j1, hipStream_t st)
+{
+    const long nblk = (long)j0.nb * j0.S + (long)j1.nb * j1.S;
+    hipLaunchKernelGGL((rows_gemm_kernel<MT, ATOM>), dim3((unsigned)nblk), dim3(64 * RT_WAVES), 0, st, B, K, x,
+                       ldx, j0, j1);
+    K3_LAUNCHED();
+    return K3HIP_OK;
+}
+
 template <int MT, bool ATOM = false>
 int launch_rows(int B, int N, int K, int tchunk, int S, const float *x, long ldx, const uint16_t *Wf,
                 float *P, long ldp, long split_stride, hipStream_t st)
 {
-    hipLaunchKernelGGL((rows_gemm_kernel<MT, ATOM>), dim3((N + 16 * RT_NT - 1) / (16 * RT_NT), S),
-                       dim3(64 * RT_WAVES), 0, st, B, N, K, tchunk, x, ldx, Wf, P, ldp, split_stride);
-    K3_LAUNCHED();
-    return K3HIP_OK;
+    const RowsJob none{1, 1, 0, 1, Wf, P, 0, 0};   // no blocks
+    return launch_jobs<MT, ATOM>(B, K, x, ldx, rows_job(N, tchunk, S, Wf, P, ldp, split_stride), none, st);
+}
+
+// rows for one launch of up to 64 rows (MT = 1, 2 or 4 16-row tiles)
+int launch_jobs_b(int bb, int K, const float *x, long ldx, const RowsJob &j0, const RowsJob &j1, hipStream_t st)
+{
+    if (bb <= 16) return launch_jobs<1>(bb, K, x, ldx, j0, j1, st);
+    if (bb <= 32) return launch_jobs<2>(bb, K, x, ldx, j0, j1, st);
+    return launch_jobs<4>(bb, K, x, ldx, j0, j1, st);
 }
 
 int cu_total()
@@ -280,6 +318,28 @@ int gemm_rows_part(int B, int N, int K, const float *x, long ldx, const uint16_t
         if (bb <= 16) rc = launch_rows<1>(bb, N, K, pl.tchunk, pl.S, xb, ldx, Wf, Pb, N, plane, st);
         else if (bb <= 32) rc = launch_rows<2>(bb, N, K, pl.tchunk, pl.S, xb, ldx, Wf, Pb, N, plane, st);
         else rc = launch_rows<4>(bb, N, K, pl.tchunk, pl.S, xb, ldx, Wf, Pb, N, plane, st);
+        if (rc) return rc;
+    }
+    return K3HIP_OK;
+}
+
+int gemm_rows_with_part(int B, int K, const float *x, long ldx, int N1, const uint16_t *Wf1, float *C1, long ldc1,
+                        int N2, const uint16_t *Wf2, float *P2, hipStream_t st, float *ws, size_t ws_floats)
+{
+    if (B <= 0 || K <= 0) return K3HIP_OK;
+    const RowsPlan p1 = rows_plan(N1, K), p2 = rows_plan(N2, K);
+    if (N1 <= 0 || N2 <= 0 || p1.S != 1) {   // the first product needs its reduction: two launches
+        int rc = gemm_rows(B, N1, K, x, ldx, Wf1, C1, ldc1, st, ws, ws_floats);
+        return rc ? rc : gemm_rows_part(B, N2, K, x, ldx, Wf2, P2, st);
+    }
+    if ((K & 7) || (ldx & 3) || (((uintptr_t)x | (uintptr_t)Wf1 | (uintptr_t)Wf2) & 15))
+        K3_FAIL(K3HIP_EINVAL, "gemm_rows_with_part: K=%d ldx=%ld need multiples of 8 / 4 and 16-byte aligned x, W", K, ldx);
+    const long plane = (long)B * N2;
+    for (int b0 = 0; b0 < B; b0 += 64) {
+        const int bb = std::min(64, B - b0);
+        const RowsJob j0 = rows_job(N1, p1.tchunk, 1, Wf1, C1 + (size_t)b0 * ldc1, ldc1, 0);
+        const RowsJob j1 = rows_job(N2, p2.tchunk, p2.S, Wf2, P2 + (size_t)b0 * N2, N2, plane);
+        int rc = launch_jobs_b(bb, K, x + (size_t)b0 * ldx, ldx, j0, j1, st);
         if (rc) return rc;
     }
     return K3HIP_OK;
