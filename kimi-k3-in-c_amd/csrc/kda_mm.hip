@@ -17,8 +17,12 @@
 // step load under that substep's MFMAs. Fragment reads are 16 bytes per lane; rows are 128
 // bytes and the 16-byte chunk index is XORed with (row & 7) ^ ((row >> 3) & 1), which keeps
 // every 16-lane group of a fragment read on distinct banks (no LDS bank conflicts, counter-
-// verified). The steady-state loop body is branch-free so the interleave hints (one MFMA,
-// one LDS read / LDS write / global load) apply to all of it.
+// verified). Global loads are buffer loads: a thread's 16 pieces differ only by wave-uniform
+// offsets, so one per-lane offset register per operand addresses all of them, and every LDS
+// offset is one per-lane base plus an immediate; the loop body stays at ~150 VGPRs. Each
+// substep is 16 MFMA slots in a fixed order (sched_barrier between slots), each slot also
+// carrying one fragment read or one LDS write + global load, and the same branch-free body
+// runs every K-step (the last steps reload clamped copies that nothing reads).
 //
 // Tile order is XCD-aware: workgroup b runs on XCD b % 8, and consecutive tile ids (groups
 // of 8 M-tiles walked along N) are given to the same XCD, so the tiles running together on
@@ -29,6 +33,7 @@
 // adds them in increasing s, so results are bit-reproducible.
 #include "kda_internal.h"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace k3kda {
@@ -77,7 +82,11 @@ __device__ __forceinline__ void tile_of(int b, int nb, int tiles_m, int tiles_n,
     tn = (t % per_group) / gsz;
 }
 
-template <int AB, int OUT>
+// EDGE: M or N below one tile (or leading dimensions beyond 32-bit buffer offsets), rows
+// past M / N clamped to the last one in every load (the general form). Otherwise a last partial tile is moved back to end at M (or N): the rows it
+// shares with the tile before are computed again, with the same bits, and every load of a
+// thread is a wave-uniform base plus one fixed per-lane offset.
+template <int AB, int OUT, bool EDGE>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void mm_kernel(
     int M, int N, int K, const uint16_t *__restrict__ A, long lda, const uint16_t *__restrict__ B, long ldb,
     void *__restrict__ Cv, long ldc, int gcols, long gstride, int tiles_m, int tiles_n, int splits)
@@ -87,25 +96,48 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     const int wm = wave >> 1, wn = wave & 1;
     int tm, tn, sp;
     tile_of(blockIdx.x, gridDim.x, tiles_m, tiles_n, splits, tm, tn, sp);
-    const int m0 = tm * BM, n0 = tn * BN;
+    int m0 = tm * BM, n0 = tn * BN;
+    if constexpr (!EDGE) {
+        m0 = min(m0, M - BM);
+        n0 = min(n0, N - BN);
+    }
     const int nks = K / BK / splits, k_first = sp * nks * BK;
 
-    // this thread's 16-byte pieces: global row pointer (rows past M or N clamped to the last
-    // one: loaded, never stored) and LDS offset within a stage
-    const uint16_t *src[NL];
-    int ldo[NL];
-#pragma unroll
-    for (int i = 0; i < NL; i++) {
-        const int idx = i * NT + tid, row = idx >> 3, c = idx & 7;
-        if (row < BM) {
-            const int r = min(m0 + row, M - 1);
-            src[i] = A + (long)r * lda + k_first + c * 8;
+    // this thread's 16-byte pieces of a K-step: piece i is row 32 i + prow of the stage's
+    // A rows (0-255) then B rows (256-511), 16-byte chunk pc; in LDS at wo + 4096 i (the
+    // swizzle of row 32 i + prow equals that of prow)
+    const int prow = tid >> 3, pc = tid & 7;
+    const int va = (prow * (int)lda + pc * 8) * 2, vb = (prow * (int)ldb + pc * 8) * 2;
+    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(A + (long)m0 * lda + k_first), (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(B + (long)n0 * ldb + k_first), (short)0, 0x7fffffff, 0x00020000);
+    auto gload = [&](int i, int ks) -> u32x4 {
+        if constexpr (EDGE) {
+            const int row = i * 32 + prow;
+            const uint16_t *p = row < BM ? A + (long)min(m0 + row, M - 1) * lda
+                                         : B + (long)min(n0 + row - BM, N - 1) * ldb;
+            return *reinterpret_cast<const u32x4 *>(p + k_first + ks * BK + pc * 8);
+        } else if (i < NL / 2) {
+            return __builtin_amdgcn_raw_buffer_load_b128(rA, va, i * 64 * (int)lda + ks * BK * 2, 0);
         } else {
-            const int r = min(n0 + row - BM, N - 1);
-            src[i] = B + (long)r * ldb + k_first + c * 8;
+            return __builtin_amdgcn_raw_buffer_load_b128(rB, vb, (i - NL / 2) * 64 * (int)ldb + ks * BK * 2, 0);
         }
-        ldo[i] = row * 128 + ((c ^ swz(row)) << 4);
+    };
+    const uint32_t wo = prow * 128 + ((pc ^ swz(prow)) << 4);
+
+    // fragment reads: lane row r32 of a 32-row tile, 16-byte chunk 2 s + kh in substep s;
+    // ra / rb hold the per-lane offset of each substep in stage 0, the tile adds 4096 i
+    const int r32 = lane & 31, kh = lane >> 5, sw = swz(r32);
+    uint32_t ra[S], rb[S];
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+        const uint32_t x = r32 * 128 + (((2 * s + kh) ^ sw) << 4);
+        ra[s] = x + wm * WM * 128;
+        rb[s] = x + A_BYTES + wn * WN * 128;
     }
+    auto lds16 = [&](uint32_t off) { return *reinterpret_cast<const u32x4 *>(smem + off); };
+
     u32x4 stg[NL];
     f32x16 acc[TI][TJ];
 #pragma unroll
@@ -113,85 +145,60 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
 #pragma unroll
         for (int j = 0; j < TJ; j++) acc[i][j] = f32x16{};
 
-    // prologue: step 0 into LDS buffer 0, step 1 into registers
+    // prologue: step 0 into LDS stage 0, step 1 (or step 0 again) into registers
 #pragma unroll
-    for (int i = 0; i < NL; i++) stg[i] = *reinterpret_cast<const u32x4 *>(src[i]);
+    for (int i = 0; i < NL; i++) stg[i] = gload(i, 0);
 #pragma unroll
-    for (int i = 0; i < NL; i++) *reinterpret_cast<u32x4 *>(smem + ldo[i]) = stg[i];
-    if (nks > 1) {
+    for (int i = 0; i < NL; i++) *reinterpret_cast<u32x4 *>(smem + wo + 4096 * i) = stg[i];
 #pragma unroll
-        for (int i = 0; i < NL; i++) stg[i] = *reinterpret_cast<const u32x4 *>(src[i] + BK);
-    }
+    for (int i = 0; i < NL; i++) stg[i] = gload(i, min(1, nks - 1));
     __syncthreads();
 
-    const int r32 = lane & 31, kh = lane >> 5, sw = swz(r32);   // fragment rows start at multiples of 32
-    int aoff[TI], boff[TJ];
-#pragma unroll
-    for (int i = 0; i < TI; i++) aoff[i] = (wm * WM + i * 32 + r32) * 128;
-#pragma unroll
-    for (int j = 0; j < TJ; j++) boff[j] = A_BYTES + (wn * WN + j * 32 + r32) * 128;
     u32x4 a[2][TI], b[2][TJ];
 #pragma unroll
-    for (int i = 0; i < TI; i++) a[0][i] = *reinterpret_cast<const u32x4 *>(smem + aoff[i] + ((kh ^ sw) << 4));
+    for (int i = 0; i < TI; i++) a[0][i] = lds16(ra[0] + 4096 * i);
 #pragma unroll
-    for (int j = 0; j < TJ; j++) b[0][j] = *reinterpret_cast<const u32x4 *>(smem + boff[j] + ((kh ^ sw) << 4));
+    for (int j = 0; j < TJ; j++) b[0][j] = lds16(rb[0] + 4096 * j);
 
-    // one K-step; NEXT: a step ks+1 exists (in registers), LOAD2: fetch step ks+2
-    auto step = [&](int ks, auto next_c, auto load2_c) {
-        constexpr bool NEXT = decltype(next_c)::value, LOAD2 = decltype(load2_c)::value;
-        const char *sa = smem + (ks & 1) * STAGE;
-        char *sn = smem + ((ks + 1) & 1) * STAGE;
-        constexpr int HALF = NL / 2;
+    // K-step ks from LDS stage ks & 1. Each substep is 16 MFMA slots in a fixed order:
+    // slots 0-7 also read one fragment of the next substep (in the order the next
+    // substep's MFMAs use them), slots 8-13 write one piece of step ks+1 (held in
+    // registers) to the other stage and load step ks+2 in its place. The barrier that
+    // publishes step ks+1 opens the last substep, whose slots read step ks+1's first
+    // fragments. The last steps load and store clamped copies that nothing reads, so
+    // every step runs the same branch-free code.
+    for (int ks = 0; ks < nks; ks++) {
+        const uint32_t so = (ks & 1) * STAGE, wbase = (so ^ STAGE) + wo;
+        const int kl = min(ks + 2, nks - 1);
 #pragma unroll
         for (int s = 0; s < S; s++) {
             const int cur = s & 1, nx = cur ^ 1;
-            if (NEXT && s < 2) {
+            constexpr int W0[4] = {0, 6, 11, 16};
+            const int wb = s < 3 ? W0[s] : NL, we = s < 3 ? W0[s + 1] : NL;
+            const uint32_t rso = s + 1 < S ? so : so ^ STAGE;
+            const uint32_t xa = ra[(s + 1) % S] + rso, xb = rb[(s + 1) % S] + rso;
+            if (s + 1 == S) __syncthreads();
 #pragma unroll
-                for (int i = s * HALF; i < (s + 1) * HALF; i++) {
-                    *reinterpret_cast<u32x4 *>(sn + ldo[i]) = stg[i];
-                    if (LOAD2) stg[i] = *reinterpret_cast<const u32x4 *>(src[i] + (long)(ks + 2) * BK);
+            for (int q = 0; q < TI * TJ; q++) {
+                const int i = q / TJ, j = q % TJ;
+                acc[i][j] = mfma<AB>(a[cur][i], b[cur][j], acc[i][j]);
+                if (q < TI + TJ) {
+                    // read order a0 b0 b1 b2 b3 a1 a2 a3
+                    if (q == 0) a[nx][0] = lds16(xa);
+                    else if (q <= TJ) b[nx][q - 1] = lds16(xb + 4096 * (q - 1));
+                    else a[nx][q - TJ] = lds16(xa + 4096 * (q - TJ));
                 }
-            }
-            if (s + 1 < S) {
-                const int c = 2 * (s + 1) + kh;
-#pragma unroll
-                for (int i = 0; i < TI; i++) a[nx][i] = *reinterpret_cast<const u32x4 *>(sa + aoff[i] + ((c ^ sw) << 4));
-#pragma unroll
-                for (int j = 0; j < TJ; j++) b[nx][j] = *reinterpret_cast<const u32x4 *>(sa + boff[j] + ((c ^ sw) << 4));
-            } else if (NEXT) {
-                // every read of this step is in registers; step ks+1 is in LDS once all waves
-                // pass this barrier
-                __syncthreads();
-#pragma unroll
-                for (int i = 0; i < TI; i++) a[nx][i] = *reinterpret_cast<const u32x4 *>(sn + aoff[i] + ((kh ^ sw) << 4));
-#pragma unroll
-                for (int j = 0; j < TJ; j++) b[nx][j] = *reinterpret_cast<const u32x4 *>(sn + boff[j] + ((kh ^ sw) << 4));
-            }
-#pragma unroll
-            for (int i = 0; i < TI; i++)
-#pragma unroll
-                for (int j = 0; j < TJ; j++) acc[i][j] = mfma<AB>(a[cur][i], b[cur][j], acc[i][j]);
-            if (s + 1 < S || NEXT) {
-#pragma unroll
-                for (int q = 0; q < TI + TJ; q++) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // LDS read
+                if (q >= TI + TJ && wb + q - (TI + TJ) < we) {
+                    const int w = wb + q - (TI + TJ);
+                    *reinterpret_cast<u32x4 *>(smem + wbase + 4096 * w) = stg[w];
+                    // the reload may not move above the write: stg[w] keeps its registers
+                    __builtin_amdgcn_sched_barrier(0);
+                    stg[w] = gload(w, kl);
                 }
-            }
-            if (NEXT && s < 2) {
-#pragma unroll
-                for (int q = 0; q < HALF; q++) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);   // LDS write
-                    if (LOAD2) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // global load
-                }
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
-    };
-    int ks = 0;
-    for (; ks + 2 < nks; ks++) step(ks, std::true_type{}, std::true_type{});
-    if (ks + 1 < nks) step(ks++, std::true_type{}, std::false_type{});
-    step(ks, std::false_type{}, std::false_type{});
+    }
 
     // epilogue: lane holds column r32 of each 32 x 32 tile, rows (r & 3) + 8 (r >> 2) + 4 kh
 #pragma unroll
@@ -221,26 +228,36 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
         }
 }
 
-template <int AB, int OUT>
-int launch_mm(int M, int N, int K, const void *A, long lda, const void *B, long ldb, void *C, long ldc, int gcols,
-              long gstride, int splits, hipStream_t st)
+template <int AB, int OUT, bool EDGE>
+int launch_mm_e(int M, int N, int K, const void *A, long lda, const void *B, long ldb, void *C, long ldc, int gcols,
+                long gstride, int splits, hipStream_t st)
 {
     static bool lds_ok[64];
     int dev = 0;
     K3_HIP(hipGetDevice(&dev));
     if (dev >= 0 && dev < 64 && !lds_ok[dev]) {
-        K3_HIP(hipFuncSetAttribute((const void *)mm_kernel<AB, OUT>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                   LDS_BYTES));
+        K3_HIP(hipFuncSetAttribute((const void *)mm_kernel<AB, OUT, EDGE>,
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES));
         lds_ok[dev] = true;
     }
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     const long grid = (long)tiles_m * tiles_n * splits;
     if (grid > 0x7fffffffL) K3_FAIL(K3HIP_EUNSUPPORTED, "mm: %dx%d output needs too many workgroups", M, N);
-    hipLaunchKernelGGL((mm_kernel<AB, OUT>), dim3((unsigned)grid), dim3(NT), LDS_BYTES, st, M, N, K,
+    hipLaunchKernelGGL((mm_kernel<AB, OUT, EDGE>), dim3((unsigned)grid), dim3(NT), LDS_BYTES, st, M, N, K,
                        (const uint16_t *)A, lda, (const uint16_t *)B, ldb, C, ldc, gcols, gstride, tiles_m, tiles_n,
                        splits);
     K3_LAUNCHED();
     return K3HIP_OK;
+}
+
+template <int AB, int OUT>
+int launch_mm(int M, int N, int K, const void *A, long lda, const void *B, long ldb, void *C, long ldc, int gcols,
+              long gstride, int splits, hipStream_t st)
+{
+    // the uniform-offset form needs whole tiles and 32-bit buffer offsets
+    if (M < BM || N < BN || (long)BM * 2 * std::max(lda, ldb) + 2L * K >= (1L << 31))
+        return launch_mm_e<AB, OUT, true>(M, N, K, A, lda, B, ldb, C, ldc, gcols, gstride, splits, st);
+    return launch_mm_e<AB, OUT, false>(M, N, K, A, lda, B, ldb, C, ldc, gcols, gstride, splits, st);
 }
 
 int check_shape(const char *who, int M, int N, int K, int ab, const void *A, long lda, const void *B, long ldb)
