@@ -12,23 +12,26 @@
 //
 //  * A workgroup (8 waves, two per SIMD) owns one sequence and a contiguous range of
 //    positions (~CUs/B ranges per sequence) and walks it in tiles of 16 positions (16
-//    contiguous cache rows). A tile is loaded one tile ahead into registers with 16-byte
-//    loads, split into bf16 hi/lo and staged row-major in LDS (double-buffered).
-//  * Wave w works for head tile w % 4 (16 heads) and lane l always for head 16 (w % 4) +
-//    (l & 15), so a head's softmax state and its weighted sums sit in the same lanes:
-//      scores^T (positions x heads) = cache tile (16 x CW) . qcat^T on split-bf16 MFMA
-//        (16x16x32, cache rows read from LDS, q fragments held in registers for the whole
-//        range); the two waves of a head tile take half of the channels each and add their
-//        partial scores in the same order through LDS, so lane l of both ends with the same
-//        scores of its head at 4 of the tile's positions;
-//      online softmax in base 2: running max M (exchanged between the 4 lanes of a head),
-//        per-lane partial sums, the weighted sums rescaled by 2^(M_old - M_new) only when
-//        some max of the wave grew;
-//      chat^T (latent channels x heads) += latent tile^T . P on split-bf16 MFMA (16x16x16),
-//        256 of the latent channels per wave: the transposed latent fragments come straight
-//        from the row-major tile through ds_read_b64_tr_b16, and P is the score product's
-//        output without leaving the lanes.
-//    Two barriers per tile: partial scores published, tile consumed.
+//    contiguous cache rows). Every thread loads its 16-byte units of a tile two tiles
+//    ahead into registers, splits them into bf16 hi/lo and stages them row-major in LDS
+//    (four tile buffers).
+//  * The two waves of a SIMD take different roles on consecutive tiles, so one score
+//    product and one weighted sum share the SIMD's MFMA pipe instead of both waves running
+//    the same phase. Lane l of wave w works for head 16 (w % 4) + (l & 15) in both roles:
+//      S waves (0-3), tile it: scores^T (positions x heads) = cache tile (16 x CW) . qcat^T
+//        on split-bf16 MFMA (16x16x32, cache rows read from LDS, the q fragments of all 18
+//        K-steps held in registers for the whole range; the channel halves summed
+//        separately and then added), then the online softmax in base 2: running max M
+//        (exchanged between the 4 lanes of a head), per-lane partial sums; P (bf16 hi/lo)
+//        and the rescale factor 2^(M_old - M_new) go to LDS;
+//      U waves (4-7), tile it - 1: the weighted sums, all 32 latent channel tiles, rescaled
+//        only when some max of the wave grew, then chat^T (latent channels x heads) +=
+//        latent tile^T . P on split-bf16 MFMA (16x16x16); the transposed latent fragments
+//        come straight from the row-major tile through ds_read_b64_tr_b16, and P is read in
+//        the score product's output layout (the lanes that hold a head's scores are the
+//        lanes that need its weights).
+//    One barrier per tile: P of tile it and the staging of tile it + 2 are published, tiles
+//    it and it - 1 consumed.
 //  * Each workgroup writes its unnormalised sums with (M, l); a second kernel merges the
 //    ranges of a sequence (weights 2^(M_s - M*), the sums in a fixed order), divides by the
 //    merged sum and writes chat directly as the bf16 hi/lo rows of the W_UV GEMM.
@@ -51,20 +54,23 @@ typedef s16x4 __attribute__((address_space(3))) *lds_s16x4_ptr;
 constexpr int AT_T = 16;             // positions per tile
 constexpr int AT_NT = 512;           // threads per workgroup: 8 waves, two per SIMD
 constexpr int AT_MAXKS = 18;         // 32-channel K-steps of the scores (kv_lora + rope <= 576)
-constexpr int AT_KSW = AT_MAXKS / 2; // K-steps per wave
+constexpr int AT_KSW = AT_MAXKS / 2; // K-steps per channel half of the score product
 constexpr int AT_MAXCT = 32;         // 16-channel tiles of the latent (kv_lora <= 512)
-constexpr int AT_CTW = AT_MAXCT / 2; // latent channel tiles per wave
 constexpr int AT_MAXU = 5;           // 16-byte cache loads per thread per tile (kv_lora + rope <= 576)
+constexpr int AT_NB = 4;             // staged tile buffers
 constexpr int AT_MAXSPLIT = 64;      // position ranges per sequence
 constexpr float AT_LOG2E = 1.4426950408889634f;
 
-// LDS: 2 buffers x {hi, lo} x [AT_T][AT_PR] bf16. Rows hold the 576 channels of the largest
+// LDS: AT_NB buffers x {hi, lo} x [AT_T][AT_PR] bf16 (150 KB), then P and the rescale
+// factors of two tiles (10 KB). Rows hold the 576 channels of the largest
 // shape (smaller shapes are zero past their kv_lora + rope, so every shape runs the same
 // products). The row pitch in dwords is 4 (4 AT_MAXKS + 1): the 16 rows of one 16-byte
 // fragment read start in 16 different 4-bank groups.
 constexpr int AT_PR = 32 * AT_MAXKS + 8;
 constexpr size_t AT_PLANE = (size_t)AT_T * AT_PR;   // bf16
-constexpr size_t AT_LDS = 4 * AT_PLANE * 2 + 8 * 64 * 16;   // bytes: tiles, partial scores
+constexpr size_t AT_P = (size_t)AT_NB * 2 * AT_PLANE * 2;  // bytes: tiles; then P [2][4][64] x 16 B
+constexpr size_t AT_A = AT_P + 2 * 4 * 64 * 16;              // rescale factors [2][4][64] fp32
+constexpr size_t AT_LDS = AT_A + 2 * 4 * 64 * 4;
 
 struct AtGeom {
     int H, CW, KL;
@@ -104,22 +110,21 @@ __device__ __forceinline__ f32x4 mma3_16(f32x4 acc, const s16x4 &ah, const s16x4
 }
 
 // Workgroup (sp, b): positions [Tn sp / nsplit, Tn (sp + 1) / nsplit) of sequence b.
-// Wave w: head tile ht = w % 4 (heads 16 ht .. 16 ht + 15), half hf = w / 4. Lane l works for
-// head h = 16 ht + (l & 15); kg = l >> 4 picks its K slice in the score product and its 4
-// positions of each tile (4 kg .. 4 kg + 3) in the softmax. The two waves of a head tile
-// split the score product's channels (K-steps 9 hf .. 9 hf + 8) and the weighted sum's latent
-// channels (256 hf .. 256 hf + 255); they add their partial scores in the same order through
-// LDS, so both run the identical softmax.
-// FULL: kv_lora + rope = 576, every staging unit of a row exists.
+// Wave w: head tile ht = w % 4 (heads 16 ht .. 16 ht + 15), S role for w < 4, U role
+// otherwise. Lane l works for head h = 16 ht + (l & 15); kg = l >> 4 picks its K slice in
+// the score product and its 4 positions of each tile (4 kg .. 4 kg + 3). The S wave sums
+// the score product as K-steps 0-8 and 9-17, each into two alternating accumulators, then
+// the two halves. FULL: kv_lora + rope = 576, every staging unit of a row exists.
 template <bool FULL>
 __global__ __launch_bounds__(AT_NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void mla_attn_kernel(
     AtGeom g, int Tn, int cap, int nsplit, float scale2, AtQ qs,
     const float *__restrict__ cache, float *__restrict__ pctx, float *__restrict__ pm, float *__restrict__ pl)
 {
     extern __shared__ __attribute__((aligned(16))) uint16_t at_smem[];
-    f32x4 *sS = reinterpret_cast<f32x4 *>(at_smem + 4 * AT_PLANE);   // partial scores [2][4][64]
+    char *sbase = reinterpret_cast<char *>(at_smem);
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int m = lane & 15, kg = lane >> 4, ht = w & 3, hf = w >> 2;
+    const int m = lane & 15, kg = lane >> 4, ht = w & 3;
+    const bool isS = w < 4;
     const int sp = blockIdx.x, b = blockIdx.y;
     const int p0 = (int)((long)Tn * sp / nsplit), p1 = (int)((long)Tn * (sp + 1) / nsplit);
     const int ntile = (p1 - p0 + AT_T - 1) / AT_T;
@@ -127,55 +132,21 @@ __global__ __launch_bounds__(AT_NT) __attribute__((amdgpu_waves_per_eu(2, 2))) v
     const int h = 16 * ht + m;
     const bool act = 16 * ht < H;   // wave-uniform: this wave has heads
 
-    // q B-fragments of this wave's K-steps (K = channels 32 ks + 8 kg .. +7, column = head h),
-    // hi/lo, zero past CW and for heads past H
-    bf16x8 qh[AT_KSW], ql[AT_KSW];
-#pragma unroll
-    for (int i = 0; i < AT_KSW; i++) {
-        float x[8];
-        const int c = 32 * (AT_KSW * hf + i) + 8 * kg;
-        const bool ok = h < H;
-        const size_t bh = (size_t)b * H + (ok ? h : 0);
-        const float *a2 = qs.A2 + bh * CW, *a2lo = a2 + (size_t)qs.B * H * CW;
-        const float *qr = qs.q + bh * qs.QH + qs.QN - KL;   // q_rope(b, h) at channels KL ..
-#pragma unroll
-        for (int e = 0; e < 8; e += 4) {
-            const int cc = c + e;   // KL % 16 == 0: a 4-channel group is wholly latent or rope
-            f4 v = f4{0.0f, 0.0f, 0.0f, 0.0f};
-            if (ok && cc < CW) {
-                if (cc < KL) v = *reinterpret_cast<const f4 *>(a2 + cc) + *reinterpret_cast<const f4 *>(a2lo + cc);
-                else v = *reinterpret_cast<const f4 *>(qr + cc);
-            }
-            x[e] = v.x; x[e + 1] = v.y; x[e + 2] = v.z; x[e + 3] = v.w;
-        }
-#pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-            bf16x2 hh, ll;
-            split2(x[e], x[e + 1], hh, ll);
-            qh[i][e] = hh[0]; qh[i][e + 1] = hh[1];
-            ql[i][e] = ll[0]; ql[i][e + 1] = ll[1];
-        }
-    }
-    // channels CW .. 575 of every staged row stay zero (both buffers, hi and lo)
     if (!FULL) {
         const int padw = 32 * AT_MAXKS - CW;
-        for (int i = tid; i < 4 * AT_T * padw; i += AT_NT) {
+        for (int i = tid; i < 2 * AT_NB * AT_T * padw; i += AT_NT) {
             const int pl4 = i / (AT_T * padw), r = (i / padw) % AT_T, c = CW + i % padw;
             at_smem[pl4 * AT_PLANE + (size_t)r * AT_PR + c] = 0;
         }
     }
 
-    // staging: thread (r = tid / 32, q = tid % 32) owns row r of a tile and its 16-byte units
-    // q + 32 k (floats 4 q + 128 k .. +3), so 32 threads read 512 contiguous bytes. Each
-    // cache row is read once per step: nontemporal loads stream it past the caches (the
-    // batch-16 MLA layer over 8192 positions measured 205.7 -> 198.4 us with them).
     const int sr = tid >> 5, sq = 4 * (tid & 31);
     f4 R[AT_MAXU];
 #pragma unroll
     for (int k = 0; k < AT_MAXU; k++) R[k] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     auto load_tile = [&](int tile) {
         const int tl = min(tile, ntile - 1);
-        const int pos = min(p0 + AT_T * tl + sr, p1 - 1);   // past the range: a valid row, masked later
+        const int pos = min(p0 + AT_T * tl + sr, p1 - 1);
         const float *row = cache + ((size_t)b * cap + pos) * CW + sq;
 #pragma unroll
         for (int k = 0; k < AT_MAXU; k++)
@@ -194,99 +165,137 @@ __global__ __launch_bounds__(AT_NT) __attribute__((amdgpu_waves_per_eu(2, 2))) v
             }
     };
 
-    f32x4 acc[AT_CTW];
-#pragma unroll
-    for (int j = 0; j < AT_CTW; j++) acc[j] = 0.0f;
-    float M = -INFINITY, lsum = 0.0f;
-
-    // scores^T partial over this wave's K-steps: D[position 4 kg + e][head m]
-    auto scores = [&](int buf) {
-        const uint16_t *hi = at_smem + (size_t)(2 * buf) * AT_PLANE + m * AT_PR + 32 * AT_KSW * hf + 8 * kg;
-        const uint16_t *lo = hi + AT_PLANE;
-        f32x4 s0 = 0.0f, s1 = 0.0f;
-#pragma unroll
-        for (int i = 0; i < AT_KSW; i++) {
-            const bf16x8 ah = *reinterpret_cast<const bf16x8 *>(hi + 32 * i);
-            const bf16x8 al = *reinterpret_cast<const bf16x8 *>(lo + 32 * i);
-            if (i & 1) s1 = mma3_32(s1, ah, al, qh[i], ql[i]);
-            else s0 = mma3_32(s0, ah, al, qh[i], ql[i]);
-        }
-        return s0 + s1;
-    };
-    // online softmax of the tile's scores s (this lane: head h, positions p0 + 16 it + 4 kg + e)
-    // and the weighted sum over this wave's latent channel tiles
-    auto update = [&](int buf, int it, f32x4 s) {
-        const uint16_t *hi = at_smem + (size_t)(2 * buf) * AT_PLANE, *lo = hi + AT_PLANE;
-        const int t0 = p0 + AT_T * it + 4 * kg;
-        float x[4], mt = -INFINITY;
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            x[e] = t0 + e < p1 ? s[e] * scale2 : -INFINITY;
-            mt = fmaxf(mt, x[e]);
-        }
-        mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-        const float mn = fmaxf(M, mt);
-        const float alpha = __builtin_amdgcn_exp2f(M - mn);   // 0 on the first tile (M = -inf)
-        float p[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++) p[e] = __builtin_amdgcn_exp2f(x[e] - mn);   // 0 where masked
-        lsum = lsum * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
-        M = mn;
-        if (__ballot(alpha != 1.0f)) {   // some max of the wave grew
-#pragma unroll
-            for (int j = 0; j < AT_CTW; j++) acc[j] *= alpha;
-        }
-        // P as the B operand (K = positions 4 kg .. +3, column = head m), hi/lo
-        bf16x2 h01, l01, h23, l23;
-        split2(p[0], p[1], h01, l01);
-        split2(p[2], p[3], h23, l23);
-        const s16x4 ph = __builtin_bit_cast(s16x4, uint2{__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23)});
-        const s16x4 pq = __builtin_bit_cast(s16x4, uint2{__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23)});
-        // chat^T[channel 16 j + 4 kg + e][head m] += latent^T . P over channel tiles
-        // AT_CTW hf .. +AT_CTW-1; this lane's transposed-read source: position
-        // 4 kg + ((lane >> 2) & 3), channels 16 j + 4 (lane & 3) .. +3
-        const int to = (4 * kg + ((lane >> 2) & 3)) * AT_PR + 4 * (lane & 3) + 16 * AT_CTW * hf;
-#pragma unroll
-        for (int j = 0; j < AT_CTW; j++) {
-            const s16x4 ah = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(hi + to + 16 * j));
-            const s16x4 al = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(lo + to + 16 * j));
-            acc[j] = mma3_16(acc[j], ah, al, ph, pq);
-        }
-    };
-
     load_tile(0);
     stage(0);
     load_tile(1);
+    stage(1);
+    load_tile(2);
     __syncthreads();
-    // iteration it: scores of tile it (buffer it & 1); the partial scores meet in LDS; tile
-    // it + 1 (loaded one iteration earlier) is staged into the other buffer and the registers
-    // refilled with tile it + 2; the softmax and weighted sum of tile it
-    for (int it = 0; it < ntile; it++) {
-        const int buf = it & 1;
-        f32x4 s = 0.0f;
-        if (act) {
-            s = scores(buf);
-            sS[(hf * 4 + ht) * 64 + lane] = s;
-        }
-        if (it + 1 < ntile) stage(buf ^ 1);
-        __syncthreads();
-        if (it + 2 < ntile) load_tile(it + 2);
-        if (act) update(buf, it, sS[ht * 64 + lane] + sS[(4 + ht) * 64 + lane]);
-        __syncthreads();
-    }
-
-    // unnormalised sums of this wave's channels and (M, l) of this range for head h
-    lsum += __shfl_xor(lsum, 16, 64);
-    lsum += __shfl_xor(lsum, 32, 64);
-    if (act && h < H) {
-        float *outp = pctx + (((size_t)b * nsplit + sp) * H + h) * KL + 16 * AT_CTW * hf + 4 * kg;
+    // iteration it: S scores tile it, U sums tile it - 1, every thread stages tile it + 2
+    // (loaded one iteration earlier) and loads tile it + 3; both roles pass one barrier per
+    // iteration
+    if (isS) {
+        // S: q B-fragments of all K-steps (channels 32 ks + 8 kg .. +7, column = head h), hi/lo
+        bf16x8 qh[AT_MAXKS], ql[AT_MAXKS];
+        {
 #pragma unroll
-        for (int j = 0; j < AT_CTW; j++)
-            if (16 * (AT_CTW * hf + j) < KL) *reinterpret_cast<f4 *>(outp + 16 * j) = f4{acc[j][0], acc[j][1], acc[j][2], acc[j][3]};
-        if (kg == 0 && hf == 0) {
+            for (int i = 0; i < AT_MAXKS; i++) {
+                float x[8];
+                const int c = 32 * i + 8 * kg;
+                const bool ok = h < H;
+                const size_t bh = (size_t)b * H + (ok ? h : 0);
+                const float *a2 = qs.A2 + bh * CW, *a2lo = a2 + (size_t)qs.B * H * CW;
+                const float *qr = qs.q + bh * qs.QH + qs.QN - KL;
+#pragma unroll
+                for (int e = 0; e < 8; e += 4) {
+                    const int cc = c + e;
+                    f4 v = f4{0.0f, 0.0f, 0.0f, 0.0f};
+                    if (ok && cc < CW) {
+                        if (cc < KL) v = *reinterpret_cast<const f4 *>(a2 + cc) + *reinterpret_cast<const f4 *>(a2lo + cc);
+                        else v = *reinterpret_cast<const f4 *>(qr + cc);
+                    }
+                    x[e] = v.x; x[e + 1] = v.y; x[e + 2] = v.z; x[e + 3] = v.w;
+                }
+#pragma unroll
+                for (int e = 0; e < 8; e += 2) {
+                    bf16x2 hh, ll;
+                    split2(x[e], x[e + 1], hh, ll);
+                    qh[i][e] = hh[0]; qh[i][e + 1] = hh[1];
+                    ql[i][e] = ll[0]; ql[i][e + 1] = ll[1];
+                }
+            }
+        }
+        float M = -INFINITY, lsum = 0.0f;   // head h over this lane's positions
+        auto s_tile = [&](int it) {
+            const int buf = it % AT_NB;
+            const uint16_t *hi = at_smem + (size_t)(2 * buf) * AT_PLANE + m * AT_PR + 8 * kg;
+            const uint16_t *lo = hi + AT_PLANE;
+            f32x4 half[2];
+#pragma unroll
+            for (int hf = 0; hf < 2; hf++) {
+                f32x4 s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+                for (int i = 0; i < AT_KSW; i++) {
+                    const int ks = AT_KSW * hf + i;
+                    const bf16x8 ah = *reinterpret_cast<const bf16x8 *>(hi + 32 * ks);
+                    const bf16x8 al = *reinterpret_cast<const bf16x8 *>(lo + 32 * ks);
+                    if (i & 1) s1 = mma3_32(s1, ah, al, qh[ks], ql[ks]);
+                    else s0 = mma3_32(s0, ah, al, qh[ks], ql[ks]);
+                }
+                half[hf] = s0 + s1;
+            }
+            const f32x4 s = half[0] + half[1];
+            const int t0 = p0 + AT_T * it + 4 * kg;
+            float x[4], mt = -INFINITY;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                x[e] = t0 + e < p1 ? s[e] * scale2 : -INFINITY;
+                mt = fmaxf(mt, x[e]);
+            }
+            mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+            mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+            const float mn = fmaxf(M, mt);
+            const float alpha = __builtin_amdgcn_exp2f(M - mn);
+            float p[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) p[e] = __builtin_amdgcn_exp2f(x[e] - mn);
+            lsum = lsum * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+            M = mn;
+            bf16x2 h01, l01, h23, l23;
+            split2(p[0], p[1], h01, l01);
+            split2(p[2], p[3], h23, l23);
+            char *pb = sbase + AT_P + ((size_t)((it & 1) * 4 + ht) * 64 + lane) * 16;
+            *reinterpret_cast<uint4 *>(pb) = uint4{__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23),
+                                                   __builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23)};
+            reinterpret_cast<float *>(sbase + AT_A)[((it & 1) * 4 + ht) * 64 + lane] = alpha;
+        };
+        for (int it = 0; it <= ntile; it++) {
+            if (act && it < ntile) s_tile(it);
+            stage((it + 2) % AT_NB);   // past the last tile: a copy nothing reads
+            load_tile(it + 3);
+            __syncthreads();
+        }
+        lsum += __shfl_xor(lsum, 16, 64);
+        lsum += __shfl_xor(lsum, 32, 64);
+        if (act && h < H && kg == 0) {
             pm[((size_t)b * nsplit + sp) * H + h] = M;
             pl[((size_t)b * nsplit + sp) * H + h] = lsum;
+        }
+    } else {
+        // chat^T[channel 16 j + 4 kg + e][head m] for all 32 channel tiles
+        f32x4 acc[AT_MAXCT];
+#pragma unroll
+        for (int j = 0; j < AT_MAXCT; j++) acc[j] = 0.0f;
+        auto u_tile = [&](int it) {
+            const int buf = it % AT_NB;
+            const uint16_t *hi = at_smem + (size_t)(2 * buf) * AT_PLANE, *lo = hi + AT_PLANE;
+            const uint4 pv = *reinterpret_cast<const uint4 *>(sbase + AT_P + ((size_t)((it & 1) * 4 + ht) * 64 + lane) * 16);
+            const float alpha = reinterpret_cast<const float *>(sbase + AT_A)[((it & 1) * 4 + ht) * 64 + lane];
+            if (__ballot(alpha != 1.0f)) {
+#pragma unroll
+                for (int j = 0; j < AT_MAXCT; j++) acc[j] *= alpha;
+            }
+            const s16x4 ph = __builtin_bit_cast(s16x4, uint2{pv.x, pv.y});
+            const s16x4 pq = __builtin_bit_cast(s16x4, uint2{pv.z, pv.w});
+            const int to = (4 * kg + ((lane >> 2) & 3)) * AT_PR + 4 * (lane & 3);
+#pragma unroll
+            for (int j = 0; j < AT_MAXCT; j++) {
+                const s16x4 ah = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(hi + to + 16 * j));
+                const s16x4 al = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(lo + to + 16 * j));
+                acc[j] = mma3_16(acc[j], ah, al, ph, pq);
+            }
+        };
+        for (int it = 0; it <= ntile; it++) {
+            if (act && it > 0) u_tile(it - 1);
+            stage((it + 2) % AT_NB);
+            load_tile(it + 3);
+            __syncthreads();
+        }
+        if (act && h < H) {
+            float *outp = pctx + (((size_t)b * nsplit + sp) * H + h) * KL + 4 * kg;
+#pragma unroll
+            for (int j = 0; j < AT_MAXCT; j++)
+                if (16 * j < KL) *reinterpret_cast<f4 *>(outp + 16 * j) = f4{acc[j][0], acc[j][1], acc[j][2], acc[j][3]};
         }
     }
 }
