@@ -61,12 +61,17 @@ constexpr int AT_NB = 4;             // staged tile buffers
 constexpr int AT_MAXSPLIT = 64;      // position ranges per sequence
 constexpr float AT_LOG2E = 1.4426950408889634f;
 
-// LDS: AT_NB buffers x {hi, lo} x [AT_T][AT_PR] bf16 (150 KB), then P and the rescale
-// factors of two tiles (10 KB). Rows hold the 576 channels of the largest
-// shape (smaller shapes are zero past their kv_lora + rope, so every shape runs the same
-// products). The row pitch in dwords is 4 (4 AT_MAXKS + 1): the 16 rows of one 16-byte
-// fragment read start in 16 different 4-bank groups.
-constexpr int AT_PR = 32 * AT_MAXKS + 8;
+// LDS: AT_NB buffers x {hi, lo} x [AT_T][AT_PR] bf16 (152 KB), then P and the rescale
+// factors of two tiles (10 KB). Rows hold the 576 channels of the largest shape (smaller
+// shapes are zero past their kv_lora + rope, so every shape runs the same products). The
+// row pitch is 74 16-byte units and rows 8-15 hold their units in pairs swapped (column c
+// at c ^ 8, at_col): the score product's 16-byte reads (16 rows, one unit) and the
+// transposed 8-byte reads (per 32-lane pass 8 rows, two adjacent units) then both fall on
+// 64 distinct banks. (With an unswizzled 73-unit pitch the transposed reads met 2-way and
+// lost ~15% of CU cycles to bank conflicts; no plain pitch serves both patterns.)
+constexpr int AT_PR = 32 * AT_MAXKS + 16;
+
+__device__ __forceinline__ int at_col(int row, int col) { return col ^ ((row >> 3) << 3); }
 constexpr size_t AT_PLANE = (size_t)AT_T * AT_PR;   // bf16
 constexpr size_t AT_P = (size_t)AT_NB * 2 * AT_PLANE * 2;  // bytes: tiles; then P [2][4][64] x 16 B
 constexpr size_t AT_A = AT_P + 2 * 4 * 64 * 16;              // rescale factors [2][4][64] fp32
@@ -136,7 +141,7 @@ __global__ __launch_bounds__(AT_NT) __attribute__((amdgpu_waves_per_eu(2, 2))) v
         const int padw = 32 * AT_MAXKS - CW;
         for (int i = tid; i < 2 * AT_NB * AT_T * padw; i += AT_NT) {
             const int pl4 = i / (AT_T * padw), r = (i / padw) % AT_T, c = CW + i % padw;
-            at_smem[pl4 * AT_PLANE + (size_t)r * AT_PR + c] = 0;
+            at_smem[pl4 * AT_PLANE + (size_t)r * AT_PR + at_col(r, c)] = 0;
         }
     }
 
@@ -153,7 +158,7 @@ __global__ __launch_bounds__(AT_NT) __attribute__((amdgpu_waves_per_eu(2, 2))) v
             if ((FULL && k < AT_MAXU - 1) || sq + 128 * k < CW) R[k] = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(row + 128 * k));
     };
     auto stage = [&](int buf) {
-        uint16_t *hi = at_smem + (size_t)(2 * buf) * AT_PLANE + sr * AT_PR + sq, *lo = hi + AT_PLANE;
+        uint16_t *hi = at_smem + (size_t)(2 * buf) * AT_PLANE + sr * AT_PR + at_col(sr, sq), *lo = hi + AT_PLANE;
 #pragma unroll
         for (int k = 0; k < AT_MAXU; k++)
             if ((FULL && k < AT_MAXU - 1) || sq + 128 * k < CW) {
@@ -208,7 +213,7 @@ __global__ __launch_bounds__(AT_NT) __attribute__((amdgpu_waves_per_eu(2, 2))) v
         float M = -INFINITY, lsum = 0.0f;   // head h over this lane's positions
         auto s_tile = [&](int it) {
             const int buf = it % AT_NB;
-            const uint16_t *hi = at_smem + (size_t)(2 * buf) * AT_PLANE + m * AT_PR + 8 * kg;
+            const uint16_t *hi = at_smem + (size_t)(2 * buf) * AT_PLANE + m * AT_PR + at_col(m, 8 * kg);
             const uint16_t *lo = hi + AT_PLANE;
             f32x4 half[2];
 #pragma unroll
@@ -277,7 +282,8 @@ __global__ __launch_bounds__(AT_NT) __attribute__((amdgpu_waves_per_eu(2, 2))) v
             }
             const s16x4 ph = __builtin_bit_cast(s16x4, uint2{pv.x, pv.y});
             const s16x4 pq = __builtin_bit_cast(s16x4, uint2{pv.z, pv.w});
-            const int to = (4 * kg + ((lane >> 2) & 3)) * AT_PR + 4 * (lane & 3);
+            const int tr = 4 * kg + ((lane >> 2) & 3);
+            const int to = tr * AT_PR + at_col(tr, 4 * (lane & 3));
 #pragma unroll
             for (int j = 0; j < AT_MAXCT; j++) {
                 const s16x4 ah = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(hi + to + 16 * j));
