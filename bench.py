@@ -382,6 +382,19 @@ def bench_layer(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
     wall = time.perf_counter() - t0
     step_s = e0.elapsed_time(e1) * 1e-3 / steps
     flops = layer_flops_per_token(E, H, D, 64) * T
+    # the same step with every projection on the hand-written MFMA GEMM (reported beside it)
+    k3.set_projection_gemm(k3.GEMM_HANDWRITTEN)
+    try:
+        for _ in range(warmup + 1):
+            step()
+        e0.record()
+        for _ in range(steps):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+        hw_s = e0.elapsed_time(e1) * 1e-3 / steps
+    finally:
+        k3.set_projection_gemm(k3.GEMM_HIPBLASLT)
     dw.close()
     out_d = {
         "value": T / step_s, "unit": "tokens/s", "ms_per_step": step_s * 1e3,
@@ -393,6 +406,9 @@ def bench_layer(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
                      "bound": "mfma", "achieved": flops / step_s / 1e12, "peak": BF16_PEAK / 1e12,
                      "unit": "TFLOP/s", "frac": flops / step_s / BF16_PEAK, "traffic": None,
                      "flops_per_step": flops},
+        "hand_written_gemms": {"ms_per_step": hw_s * 1e3, "tokens_per_s": T / hw_s,
+                               "frac_bf16_peak": flops / hw_s / BF16_PEAK,
+                               "note": "the same step with every projection on k3hip_proj_gemm's kernel"},
     }
     if cpu:   # timed after every GPU workload
         out_d["_cpu"] = lambda: cpu_layer(host, x_host)
@@ -680,6 +696,8 @@ def main() -> int:
         "cpu_baseline": head.get("cpu_baseline"),
         "device": torch.cuda.get_device_name(0),
     }
+    if head is res.get("layer"):
+        line["hand_written_gemms"] = head["hand_written_gemms"]
     if "prefill" in res and "decode" in res:
         line["decode"] = res["decode"]
     if "layer" in res and head is not res["layer"]:

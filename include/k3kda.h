@@ -261,6 +261,15 @@ int k3hip_kda_layer_dev(const k3hip_kda_weights *w, int T, float *out, const flo
 int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *out, int out_dtype,
                             const void *x, int x_dtype, float *state, void *stream);
 
+/* Which projection GEMMs k3hip_kda_layer_prefill runs, process-wide: K3HIP_GEMM_HIPBLASLT
+ * (the default; hipBLASLt's heuristic first choice for each shape) or K3HIP_GEMM_HANDWRITTEN
+ * (k3hip_proj_gemm's kernel for every projection, the gate logits in fp16, f_a/b split over
+ * K). Both hold the same 2e-3 bar but give different bits; change it only while no layer
+ * prefill is in flight. K3HIP_EINVAL for another value. No counterpart in the reference,
+ * whose projections are one CPU routine (k3_matmul_bf16, src/core/k3_ops.c:1122-1227). */
+enum { K3HIP_GEMM_HIPBLASLT = 0, K3HIP_GEMM_HANDWRITTEN = 1 };
+int k3hip_set_projection_gemm(int impl);
+
 /* One decode token for each of B sequences through the whole layer on bf16 weights: the
  * per-token path of k3_kda_layer (src/core/k3_ops.c:864-951, T = 1) batched over
  * sequences. The projections read each weight once for all B (bf16 MFMA, each fp32 input

@@ -10,6 +10,7 @@
 //   7-8 K4: head RMSNorm then sigmoid gate              (:940-947)
 //   9 o_proj                                            (:948)
 #include <algorithm>
+#include <atomic>
 #include <math.h>
 #include <mutex>
 #include <stdarg.h>
@@ -429,6 +430,18 @@ int pair_add(const float *C2, float *y, int B, int N, hipStream_t st)
 }
 }  // namespace k3kda
 
+// Which projection GEMMs the bf16 layer prefill runs (process-wide).
+static std::atomic<int> g_proj_gemm{K3HIP_GEMM_HIPBLASLT};
+
+extern "C" int k3hip_set_projection_gemm(int impl)
+{
+    clear_error();
+    if (impl != K3HIP_GEMM_HIPBLASLT && impl != K3HIP_GEMM_HANDWRITTEN)
+        K3_FAIL(K3HIP_EINVAL, "k3hip_set_projection_gemm: impl=%d (0 hipBLASLt, 1 hand-written)", impl);
+    g_proj_gemm.store(impl, std::memory_order_relaxed);
+    return K3HIP_OK;
+}
+
 extern "C" int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *out, int out_dtype,
                                        const void *x, int x_dtype, float *state, void *stream)
 {
@@ -451,12 +464,11 @@ extern "C" int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *
     hipStream_t st = as_stream(stream);
     const size_t P = (size_t)H * D, TP = (size_t)T * P;
     const size_t wsb = k3hip_kda_chunk_workspace(T, H, D, 64);
-    // The projections are plain GEMMs and run on hipBLASLt: the hand-written MFMA GEMM
-    // (kda_mm.hip, k3hip_proj_gemm) measures 0.88-0.9x of its speed on these shapes (8192 x
-    // 4096 x 4096: 230 against 207 us; the whole layer 1.96 against 1.75 ms), the gap being
-    // the output write of each tile, which hipBLASLt's persistent stream-K kernels overlap
-    // with the next tile. `own` selects the hand-written kernels for every projection.
-    constexpr bool own = false;
+    // The projections are plain GEMMs and run on hipBLASLt by default: the hand-written MFMA
+    // GEMM (kda_mm.hip, k3hip_proj_gemm) measures 0.90-0.93x of its speed on these shapes.
+    // k3hip_set_projection_gemm(K3HIP_GEMM_HANDWRITTEN) selects the hand-written kernels for
+    // every projection (`own`).
+    const bool own = g_proj_gemm.load(std::memory_order_relaxed) == K3HIP_GEMM_HANDWRITTEN;
     int ncu = 256, rc;
     if ((rc = cu_count(ncu))) return rc;
     const int fab_s = own ? mm_splits(T, D + H, E, ncu) : 1;

@@ -33,6 +33,7 @@ EXPORTS = (
     "k3hip_mla_upload", "k3hip_mla_release", "k3hip_mla_cache_floats", "k3hip_mla_decode",
     "k3hip_kda_layer_decode", "k3hip_kda_upload_ex", "k3hip_kda_weights_bytes",
     "k3hip_kda_dropin_bytes", "k3hip_proj_gemm", "k3hip_kda_layer_decode_noalloc",
+    "k3hip_set_projection_gemm",
 )
 
 
@@ -135,6 +136,7 @@ def lib() -> C.CDLL:
         "k3hip_kda_dropin_bytes": (sz, []),
         "k3hip_proj_gemm": (i, [i, i, i, i, _P, C.c_long, _P, C.c_long, _P, i, C.c_long, _P]),
         "k3hip_kda_layer_decode_noalloc": (i, [_P, i, _P, _P, _P, C.c_long, _P]),
+        "k3hip_set_projection_gemm": (i, [i]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -195,6 +197,15 @@ def proj_gemm(a, b, c, stream=None) -> None:
     _check(lib().k3hip_proj_gemm(M, N, K, _dt(a), C.c_void_p(a.data_ptr()), a.stride(0),
                                  C.c_void_p(b.data_ptr()), b.stride(0), C.c_void_p(c.data_ptr()),
                                  _dt(c), c.stride(0), _stream(stream)))
+
+
+GEMM_HIPBLASLT, GEMM_HANDWRITTEN = 0, 1
+
+
+def set_projection_gemm(impl: int) -> None:
+    """Select the projection GEMMs of layer_prefill (process-wide): GEMM_HIPBLASLT (default)
+    or GEMM_HANDWRITTEN (the hand-written MFMA kernel of proj_gemm for every projection)."""
+    _check(lib().k3hip_set_projection_gemm(impl))
 
 
 def kda_decode(S, o, q, k, v, alpha, beta, q_scale: float, stream=None) -> None:

@@ -83,3 +83,12 @@ def test_invalid_arguments_are_refused_before_any_launch():
     assert rc in (k3kda.EINVAL, k3kda.EUNSUPPORTED)
     rc = L.k3hip_kda_epilogue(1, 1, 128, 1e-5, None, None, 0, None, None, 0, None)
     assert rc == k3kda.EINVAL
+
+
+def test_projection_gemm_selector_without_gpu():
+    """The layer prefill's GEMM selector is a host-side setting: unknown values are refused
+    and the default (hipBLASLt) is restored."""
+    L = k3kda.lib()
+    assert L.k3hip_set_projection_gemm(2) == k3kda.EINVAL and b"impl=2" in L.k3hip_last_error()
+    assert L.k3hip_set_projection_gemm(k3kda.GEMM_HANDWRITTEN) == k3kda.OK
+    assert L.k3hip_set_projection_gemm(k3kda.GEMM_HIPBLASLT) == k3kda.OK

@@ -7,9 +7,11 @@ grid-size, indexing and overflow mistakes.
    conv inputs -- the exact launch shape of the benchmark (4096 phase-1 items over the
    persistent grid, 256 phase-2 workgroups with the XCD mapping) -- against the oracle's
    orc_kda_core on the same bf16-rounded inputs, at the chunked bar 2e-3.
-2. The bf16 full layer (k3hip_kda_layer_prefill: hand-written MFMA projections, fused core,
-   epilogue, o_proj) at hidden 4096, H=32, D=128, two prefills with the state carried,
-   against the oracle's k3_kda_layer on the same bf16 weights, at the chunked bar.
+2. The bf16 full layer (k3hip_kda_layer_prefill: projections on hipBLASLt or on the
+   hand-written MFMA GEMM, fused core, epilogue, o_proj) at hidden 4096, H=32, D=128, two
+   prefills with the state carried, against the oracle's k3_kda_layer on the same bf16
+   weights, at the chunked bar (the hand-written run's first prefill, 288 tokens, has a
+   partial last row tile).
 3. The batched decode layer (k3hip_kda_layer_decode) at hidden 7168, H=32, D=128 for B=16
    sequences (the hybrid slice's KDA layer), against the oracle's k3_kda_layer per
    sequence, at the decode bar 1e-4, two steps.
@@ -71,7 +73,16 @@ def test_core_at_benchmark_shape(gpu):
     print(f"core H={H} D={D} T={T}: worst {ry:.4f}x (y) / {rs:.4f}x (S) of the 2e-3 bar, {t4:.3f}x of 1e-4")
 
 
-def test_layer_prefill_at_benchmark_width(gpu):
+@pytest.mark.parametrize("gemm", ["hipblaslt", "hand_written"])
+def test_layer_prefill_at_benchmark_width(gpu, gemm):
+    gpu.set_projection_gemm(gpu.GEMM_HANDWRITTEN if gemm == "hand_written" else gpu.GEMM_HIPBLASLT)
+    try:
+        _layer_prefill_at_benchmark_width(gpu, (288, 64) if gemm == "hand_written" else (160, 64))
+    finally:
+        gpu.set_projection_gemm(gpu.GEMM_HIPBLASLT)
+
+
+def _layer_prefill_at_benchmark_width(gpu, Ts):
     import torch
     hidden, H, D, K = 4096, 32, 128, 4
     rng = np.random.default_rng(0x4B334441 + 22)
@@ -82,7 +93,7 @@ def test_layer_prefill_at_benchmark_width(gpu):
     st_ref = np.zeros(nst, np.float32)
     dw = gpu.DeviceWeights(W.w, cfg, gpu.UPLOAD_DEV | gpu.UPLOAD_PREFILL)
     dst = torch.zeros(nst, device="cuda")
-    for i, T in enumerate((160, 64)):
+    for i, T in enumerate(Ts):
         x = bf16_to_f32(bf16(rng.standard_normal((T, hidden))))
         want = ko.kda_layer(ko.orc(), x, W, cfg, T, st_ref)
         out = torch.full((T, hidden), float("nan"), device="cuda")

@@ -46,9 +46,19 @@ def layer_weights(rng, hidden, H, D, K):
     return ko.Weights(arrays, 1)
 
 
+@pytest.mark.parametrize("gemm", ["hipblaslt", "hand_written"])
 @pytest.mark.parametrize("hidden,H,D,K,Ts", [(512, 4, 128, 4, (200, 77)), (256, 4, 64, 4, (1, 130)),
                                              (384, 3, 128, 2, (64, 1000))])
-def test_layer_prefill_vs_oracle(gpu, hidden, H, D, K, Ts):
+def test_layer_prefill_vs_oracle(gpu, hidden, H, D, K, Ts, gemm):
+    """Both projection GEMM implementations (k3hip_set_projection_gemm) hold the bar."""
+    gpu.set_projection_gemm(gpu.GEMM_HANDWRITTEN if gemm == "hand_written" else gpu.GEMM_HIPBLASLT)
+    try:
+        _layer_prefill_vs_oracle(gpu, hidden, H, D, K, Ts)
+    finally:
+        gpu.set_projection_gemm(gpu.GEMM_HIPBLASLT)
+
+
+def _layer_prefill_vs_oracle(gpu, hidden, H, D, K, Ts):
     import torch
     rng = np.random.default_rng(0x4B334441 + 2 + hidden + sum(Ts))
     W = layer_weights(rng, hidden, H, D, K)
