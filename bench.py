@@ -450,7 +450,7 @@ def cpu_layer(host: dict, x) -> dict:
                       f"D={c['D']}, bf16 weights, zero state, OpenMP {nt} threads, {el:.2f} s"}
 
 
-def bench_hybrid(torch, k3, steps: int, warmup: int) -> dict:
+def bench_hybrid(torch, k3, steps: int, warmup: int, cpu: bool = False) -> dict:
     """Hybrid slice: one decode step of batch 16 through 3 KDA layers (k3hip_kda_layer_decode) and one
     gated MLA layer with absorbed weights over an 8192-position latent cache
     (k3hip_mla_decode), hidden 7168, bf16 weights N(0, 0.02). Each part is timed with HIP
@@ -544,7 +544,7 @@ def bench_hybrid(torch, k3, steps: int, warmup: int) -> dict:
     for dw in kdas:
         dw.close()
     mla.close()
-    return {
+    res = {
         "config": {"workload": "hybrid_decode_slice", "hidden": E, "batch": B, "context": ctx,
                    "kda_layers": len(kdas), "kda_heads": H, "kda_head_dim": D,
                    "mla_heads": Hm, "kv_lora": KL, "qk_rope": QR, "qk_nope": QN, "v_head": VH, "q_lora": QL,
@@ -555,6 +555,64 @@ def bench_hybrid(torch, k3, steps: int, warmup: int) -> dict:
         "kda_hbm_frac": kda_bytes / kda_s / HBM_PEAK, "mla_hbm_frac": mla_bytes / mla_s / HBM_PEAK,
         "kda_bytes_per_step": kda_bytes, "mla_bytes_per_step": mla_bytes,
     }
+    if cpu:   # timed after every GPU workload
+        res["_cpu"] = lambda: cpu_hybrid(keep[0], keep[-1])
+    return res
+
+
+def cpu_hybrid(kda_host: dict, mla_host: dict) -> dict:
+    """The reference's own k3_kda_layer and k3_mla_cached (src/core/k3_ops.c:864-951,
+    :321-424, from oracle/_ref; the C restatement where that is absent) on the hybrid
+    slice's bf16 weights, one sequence at a time as the reference decodes: KDA decode tokens
+    (T = 1, state carried) until ~3 s, then MLA decode tokens over a cache of the slice's
+    context in the reference's expanded layout (H (nope + v) floats per position, random
+    contents), until ~3 s. Slice tokens/s = 1 / (3 t_kda + t_mla)."""
+    import numpy as np
+    sys.path.insert(0, str(REPO / "oracle"))
+    import k3_oracle as ko
+    c = HYB
+    ci = cpu_info()
+    nt = ci["threads"]
+    set_omp_threads(nt)
+    lib = "ref" if ko.ref() is not None else "orc"
+    L = ko.ref() if lib == "ref" else ko.orc()
+    arrays = {n: (a.view(np.uint16) if a.dtype == np.int16 else a) for n, a in kda_host.items()}
+    W = ko.Weights(arrays, 1)
+    E, H, D, K = c["hidden"], c["H"], c["D"], c["K"]
+    cfg = ko.make_cfg(E, H, D, K, c["gate_lb"], 1e-5)
+    P = H * D
+    st = np.zeros(P * D + 3 * P * (K - 1), np.float32)
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((1, E)).astype(np.float32)
+    n_kda, t0 = 0, time.perf_counter()
+    while True:
+        ko.kda_layer(L, x, W, cfg, 1, st)
+        n_kda += 1
+        if time.perf_counter() - t0 > 3.0:
+            break
+    t_kda = (time.perf_counter() - t0) / n_kda
+    MW = ko.MlaWeights({n: (a.view(np.uint16) if a.dtype == np.int16 else a) for n, a in mla_host.items()}, 1)
+    ctx = c["ctx"]
+    Hm, QN, QR, VH = c["mla_heads"], c["qk_nope"], c["qk_rope"], c["v_head"]
+    mcfg = ko.mla_cfg(E, Hm, c["q_lora"], c["kv_lora"], QN, QR, VH, 1e-5, 1)
+    kvc = rng.standard_normal((ctx, Hm * (QN + VH)), dtype=np.float32)
+    ropec = rng.standard_normal((ctx, QR), dtype=np.float32)
+    n_mla, t0 = 0, time.perf_counter()
+    while True:
+        ko.mla(x, MW, mcfg, 1, kvc, ropec, ctx - 1, ctx, lib=lib)
+        n_mla += 1
+        if time.perf_counter() - t0 > 3.0:
+            break
+    t_mla = (time.perf_counter() - t0) / n_mla
+    kind = "reference" if lib == "ref" else "port"
+    return {"value": 1.0 / (c["kda_layers"] * t_kda + t_mla), "unit": "tokens/s", "cores": nt, "kind": kind,
+            "cpu": ci["model"], "physical_cores": ci["physical_cores"],
+            "physical_cores_in_share": ci["physical_cores_in_share"],
+            "kda_ms_per_layer_token": t_kda * 1e3, "mla_ms_per_token": t_mla * 1e3,
+            "sample": f"{'reference C from its own sources' if kind == 'reference' else 'C oracle'}: "
+                      f"{n_kda} k3_kda_layer decode tokens (hidden {E}, H={H}, D={D}) and {n_mla} "
+                      f"k3_mla_cached decode tokens over {ctx} cached positions (64 heads, expanded "
+                      f"cache), one sequence at a time, OpenMP {nt} threads"}
 
 
 def cpu_prefill(torch, q_in, k_in, v_in, z, b_logit, gate, conv, A_log, dt_bias, o_norm) -> dict:
@@ -674,7 +732,7 @@ def main() -> int:
     # the streaming (HBM-bound) workloads before the layer: its seconds of dense MFMA leave the
     # GPU power-limited for a while, which measured the hybrid slice ~5% slower after it
     if a.workload in ("all", "hybrid"):
-        res["hybrid"] = bench_hybrid(torch, k3, a.steps, a.warmup)
+        res["hybrid"] = bench_hybrid(torch, k3, a.steps, a.warmup, not a.no_cpu)
     if a.workload in ("all", "layer"):
         res["layer"] = bench_layer(torch, k3, max(3, a.steps // 2), a.warmup, not a.no_cpu)
     for r in res.values():   # CPU baselines last, after all GPU timing
