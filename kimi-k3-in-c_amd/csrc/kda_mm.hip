@@ -83,9 +83,10 @@ __device__ __forceinline__ void tile_of(int b, int nb, int tiles_m, int tiles_n,
 }
 
 // EDGE: M or N below one tile (or leading dimensions beyond 32-bit buffer offsets), rows
-// past M / N clamped to the last one in every load (the general form). Otherwise a last partial tile is moved back to end at M (or N): the rows it
-// shares with the tile before are computed again, with the same bits, and every load of a
-// thread is a wave-uniform base plus one fixed per-lane offset.
+// past M / N clamped to the last one in every load (the general form). Otherwise a last
+// partial tile is moved back to end at M (or N): the rows it shares with the tile before
+// are computed again, with the same bits, and every load of a thread is a wave-uniform
+// base plus one fixed per-lane offset.
 template <int AB, int OUT, bool EDGE>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void mm_kernel(
     int M, int N, int K, const uint16_t *__restrict__ A, long lda, const uint16_t *__restrict__ B, long ldb,
