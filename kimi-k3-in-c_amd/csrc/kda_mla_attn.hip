@@ -58,6 +58,8 @@ constexpr int AT_KSW = AT_MAXKS / 2; // K-steps per channel half of the score pr
 constexpr int AT_MAXCT = 32;         // 16-channel tiles of the latent (kv_lora <= 512)
 constexpr int AT_MAXU = 5;           // 16-byte cache loads per thread per tile (kv_lora + rope <= 576)
 constexpr int AT_NB = 4;             // staged tile buffers
+constexpr int AT_UPF = 8;            // channel tiles of transposed reads in flight (U waves)
+constexpr int AT_SPF = 4;            // K-steps of cache fragment reads in flight (S waves)
 constexpr int AT_MAXSPLIT = 64;      // position ranges per sequence
 constexpr float AT_LOG2E = 1.4426950408889634f;
 
@@ -215,19 +217,31 @@ __global__ __launch_bounds__(AT_NT) __attribute__((amdgpu_waves_per_eu(2, 2))) v
             const int buf = it % AT_NB;
             const uint16_t *hi = at_smem + (size_t)(2 * buf) * AT_PLANE + m * AT_PR + at_col(m, 8 * kg);
             const uint16_t *lo = hi + AT_PLANE;
-            f32x4 half[2];
+            // the cache fragments are read AT_SPF K-steps ahead of the MFMAs that use them
+            bf16x8 rah[AT_SPF], ral[AT_SPF];
 #pragma unroll
-            for (int hf = 0; hf < 2; hf++) {
-                f32x4 s0 = 0.0f, s1 = 0.0f;
+            for (int ks = 0; ks < AT_SPF; ks++) {
+                rah[ks] = *reinterpret_cast<const bf16x8 *>(hi + 32 * ks);
+                ral[ks] = *reinterpret_cast<const bf16x8 *>(lo + 32 * ks);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            f32x4 half[2], s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
-                for (int i = 0; i < AT_KSW; i++) {
-                    const int ks = AT_KSW * hf + i;
-                    const bf16x8 ah = *reinterpret_cast<const bf16x8 *>(hi + 32 * ks);
-                    const bf16x8 al = *reinterpret_cast<const bf16x8 *>(lo + 32 * ks);
-                    if (i & 1) s1 = mma3_32(s1, ah, al, qh[ks], ql[ks]);
-                    else s0 = mma3_32(s0, ah, al, qh[ks], ql[ks]);
+            for (int ks = 0; ks < AT_MAXKS; ks++) {
+                const int i = ks % AT_KSW;
+                const bf16x8 ah = rah[ks % AT_SPF], al = ral[ks % AT_SPF];
+                if (ks + AT_SPF < AT_MAXKS) {
+                    rah[ks % AT_SPF] = *reinterpret_cast<const bf16x8 *>(hi + 32 * (ks + AT_SPF));
+                    ral[ks % AT_SPF] = *reinterpret_cast<const bf16x8 *>(lo + 32 * (ks + AT_SPF));
                 }
-                half[hf] = s0 + s1;
+                if (i & 1) s1 = mma3_32(s1, ah, al, qh[ks], ql[ks]);
+                else s0 = mma3_32(s0, ah, al, qh[ks], ql[ks]);
+                if (i == AT_KSW - 1) {   // a channel half done: K-steps 0-8, then 9-17
+                    half[ks / AT_KSW] = s0 + s1;
+                    s0 = 0.0f;
+                    s1 = 0.0f;
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
             const f32x4 s = half[0] + half[1];
             const int t0 = p0 + AT_T * it + 4 * kg;
@@ -284,11 +298,23 @@ __global__ __launch_bounds__(AT_NT) __attribute__((amdgpu_waves_per_eu(2, 2))) v
             const s16x4 pq = __builtin_bit_cast(s16x4, uint2{pv.z, pv.w});
             const int tr = 4 * kg + ((lane >> 2) & 3);
             const int to = tr * AT_PR + at_col(tr, 4 * (lane & 3));
+            // the transposed reads run AT_UPF channel tiles ahead of the MFMAs that use them
+            s16x4 rh[AT_UPF], rl[AT_UPF];
+#pragma unroll
+            for (int j = 0; j < AT_UPF; j++) {
+                rh[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(hi + to + 16 * j));
+                rl[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(lo + to + 16 * j));
+            }
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int j = 0; j < AT_MAXCT; j++) {
-                const s16x4 ah = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(hi + to + 16 * j));
-                const s16x4 al = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(lo + to + 16 * j));
+                const s16x4 ah = rh[j % AT_UPF], al = rl[j % AT_UPF];
+                if (j + AT_UPF < AT_MAXCT) {
+                    rh[j % AT_UPF] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(hi + to + 16 * (j + AT_UPF)));
+                    rl[j % AT_UPF] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(lo + to + 16 * (j + AT_UPF)));
+                }
                 acc[j] = mma3_16(acc[j], ah, al, ph, pq);
+                __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead (the scheduler sinks them)
             }
         };
         for (int it = 0; it <= ntile; it++) {
