@@ -169,8 +169,11 @@ int k3hip_kda_prep(int T, int H, int D, int K, float gate_lb, int in_dtype,
  * (src/core/k3_ops.c:927-938) from state S, with q scaled by q_scale. Inputs are K1's
  * outputs: q,k L2-normalised (unscaled), v, g = log-decay, beta.
  *   q,k,v,g [T][P] fp32   beta [T][H] fp32   S [H][D][D] in/out   o [T][P] fp32
- * D = 128 or 64, chunk = 64. workspace: NULL = library-managed, else at least
- * k3hip_kda_chunk_workspace(T,H,D,chunk) bytes of device memory. */
+ * D = 128 or 64, chunk = 64. workspace: NULL = library-managed (the whole sequence at
+ * once), else device memory of workspace_bytes. Given fewer than
+ * k3hip_kda_chunk_workspace(T,H,D,chunk) bytes, the sequence is processed in passes of
+ * the most whole 64-token chunks that fit (S carried; the same bits as one pass); fewer
+ * than k3hip_kda_chunk_workspace(64,H,D,chunk) bytes is K3HIP_EINVAL. */
 size_t k3hip_kda_chunk_workspace(int T, int H, int D, int chunk);
 int k3hip_kda_chunk(int T, int H, int D, int chunk,
                     const float *q, const float *k, const float *v,
@@ -184,7 +187,9 @@ int k3hip_kda_chunk(int T, int H, int D, int chunk,
  * src/core/k3_ops.c:888-938 for a T-token prefill.
  *   in_dtype = K3HIP_BF16 or K3HIP_F32; D = 128 or 64; conv_k 1..4; -80/15 <= gate_lb < 0 (the
  *   bounded gate of k3_kda_decay); q_in, k_in, v_in, z 16-byte aligned; workspace as for
- *   k3hip_kda_chunk (chunk 64). Other shapes return K3HIP_EUNSUPPORTED: use prep + chunk. */
+ *   k3hip_kda_chunk (chunk 64; in passes, conv_state carries the history between them,
+ *   and with conv_state NULL and conv_k > 1 the workspace also holds 3*P*(conv_k-1) floats
+ *   of it, rounded up to 256 bytes). Other shapes return K3HIP_EUNSUPPORTED: use prep + chunk. */
 int k3hip_kda_prefill(int T, int H, int D, int K, float gate_lb, int in_dtype,
                       const void *q_in, const void *k_in, const void *v_in,
                       const float *z, const float *b_logit,

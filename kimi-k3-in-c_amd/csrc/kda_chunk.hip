@@ -42,6 +42,7 @@
 #include "kda_internal.h"
 #include "kda_prep_math.h"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace k3kda {
@@ -1255,6 +1256,18 @@ static int prefill_k(int K, const PrefillArgs &a, hipStream_t st)
     }
 }
 
+// Tokens per pass: all of T when the workspace holds every chunk of the sequence, otherwise
+// the largest multiple of CH whose blocks fit in `avail` bytes (0: not even one chunk). The
+// passes then run one after the other on the stream, S carried between them; chunk
+// boundaries do not move, so the results are the same bits as one pass.
+static long pass_tokens(long T, int H, int D, size_t avail)
+{
+    const size_t per_chunk = (size_t)H * (D == 128 ? Ws<128>::SIZE : Ws<64>::SIZE);
+    const size_t chunks = avail / per_chunk;
+    if ((long)chunks * CH >= T) return T;
+    return (long)chunks * CH;
+}
+
 }  // namespace k3kda
 
 using namespace k3kda;
@@ -1288,17 +1301,29 @@ extern "C" int k3hip_kda_chunk(int T, int H, int D, int chunk, const float *q, c
     hipStream_t st = as_stream(stream);
     StreamBuf own;
     char *ws = (char *)workspace;
+    long pass = T;
     if (ws) {
-        if (workspace_bytes < need)
-            K3_FAIL(K3HIP_EINVAL, "k3hip_kda_chunk: workspace %zu bytes < %zu needed", workspace_bytes, need);
         if ((uintptr_t)ws & 15) K3_FAIL(K3HIP_EINVAL, "k3hip_kda_chunk: workspace must be 16-byte aligned");
+        pass = pass_tokens(T, H, D, workspace_bytes);
+        if (pass == 0)
+            K3_FAIL(K3HIP_EINVAL, "k3hip_kda_chunk: workspace %zu bytes < %zu for one chunk", workspace_bytes,
+                    k3hip_kda_chunk_workspace(CH, H, D, chunk));
     } else {
         int rc = stream_alloc(own, need, st);
         if (rc) return rc;
         ws = (char *)own.p;
     }
-    if (D == 128) return launch_chunk<128>(T, H, q, k, v, g, beta, q_scale, S, o, ws, st);
-    return launch_chunk<64>(T, H, q, k, v, g, beta, q_scale, S, o, ws, st);
+    const size_t P = (size_t)H * D;
+    for (long t0 = 0; t0 < T; t0 += pass) {
+        const int Ts = (int)std::min(pass, (long)T - t0);
+        const size_t r = (size_t)t0 * P;
+        const int rc = D == 128 ? launch_chunk<128>(Ts, H, q + r, k + r, v + r, g + r, beta + (size_t)t0 * H, q_scale,
+                                                    S, o + r, ws, st)
+                                : launch_chunk<64>(Ts, H, q + r, k + r, v + r, g + r, beta + (size_t)t0 * H, q_scale,
+                                                   S, o + r, ws, st);
+        if (rc) return rc;
+    }
+    return K3HIP_OK;
 }
 
 extern "C" int k3hip_kda_prefill(int T, int H, int D, int K, float gate_lb, int in_dtype,
@@ -1326,20 +1351,48 @@ extern "C" int k3hip_kda_prefill(int T, int H, int D, int K, float gate_lb, int 
     if (nch * H > 0x7fffffffL || H > 65535 || (long)T * H * D > 0x7fffffffL * 4L)
         K3_FAIL(K3HIP_EINVAL, "k3hip_kda_prefill: T=%d H=%d too large", T, H);
     const size_t need = k3hip_kda_chunk_workspace(T, H, D, CH);
+    const size_t P = (size_t)H * D;
     hipStream_t st = as_stream(stream);
     StreamBuf own;
     char *ws = (char *)workspace;
+    long pass = T;
+    float *cs = conv_state;
     if (ws) {
-        if (workspace_bytes < need)
-            K3_FAIL(K3HIP_EINVAL, "k3hip_kda_prefill: workspace %zu bytes < %zu needed", workspace_bytes, need);
         if ((uintptr_t)ws & 15) K3_FAIL(K3HIP_EINVAL, "k3hip_kda_prefill: workspace must be 16-byte aligned");
+        pass = pass_tokens(T, H, D, workspace_bytes);
+        if (pass < T && !cs && K > 1) {
+            // several passes without a caller's history: the history between passes lives
+            // at the start of the workspace, zeroed (a fresh sequence)
+            const size_t hist = (3 * P * (K - 1) * sizeof(float) + 255) & ~(size_t)255;
+            pass = workspace_bytes > hist ? pass_tokens(T, H, D, workspace_bytes - hist) : 0;
+            if (pass) {
+                cs = (float *)ws;
+                ws += hist;
+                int rc = zero_fill(cs, 3 * P * (K - 1), st);
+                if (rc) return rc;
+            }
+        }
+        if (pass == 0)
+            K3_FAIL(K3HIP_EINVAL, "k3hip_kda_prefill: workspace %zu bytes < %zu for one chunk%s", workspace_bytes,
+                    k3hip_kda_chunk_workspace(CH, H, D, CH), cs || K == 1 ? "" : " and the conv history");
     } else {
         int rc = stream_alloc(own, need, st);
         if (rc) return rc;
         ws = (char *)own.p;
     }
-    const PrefillArgs a{T, H, gate_lb, q_scale, in_dtype, q_in, k_in, v_in, z, b_logit, q_conv,
-                        k_conv, v_conv, A_log, dt_bias, conv_state, S, o, ws};
-    if (in_dtype == K3HIP_BF16) return D == 128 ? prefill_k<128, K3HIP_BF16>(K, a, st) : prefill_k<64, K3HIP_BF16>(K, a, st);
-    return D == 128 ? prefill_k<128, K3HIP_F32>(K, a, st) : prefill_k<64, K3HIP_F32>(K, a, st);
+    const size_t esz = in_dtype == K3HIP_BF16 ? 2 : 4;
+    for (long t0 = 0; t0 < T; t0 += pass) {
+        // a pass reads the conv history the pass before it wrote (phase 2 writes the history
+        // after the pass's last token into cs)
+        const int Ts = (int)std::min(pass, (long)T - t0);
+        const size_t r = (size_t)t0 * P;
+        const PrefillArgs a{Ts, H, gate_lb, q_scale, in_dtype, (const char *)q_in + r * esz,
+                            (const char *)k_in + r * esz, (const char *)v_in + r * esz, z + r,
+                            b_logit + (size_t)t0 * H, q_conv, k_conv, v_conv, A_log, dt_bias, cs, S, o + r, ws};
+        int rc;
+        if (in_dtype == K3HIP_BF16) rc = D == 128 ? prefill_k<128, K3HIP_BF16>(K, a, st) : prefill_k<64, K3HIP_BF16>(K, a, st);
+        else rc = D == 128 ? prefill_k<128, K3HIP_F32>(K, a, st) : prefill_k<64, K3HIP_F32>(K, a, st);
+        if (rc) return rc;
+    }
+    return K3HIP_OK;
 }

@@ -142,6 +142,26 @@ def test_chunk_frozen_state_invariant(gpu):
     assert_close(got_S, S0, 1e-7, 1e-6, "frozen S")
 
 
+def test_chunk_in_passes_bitwise(gpu):
+    """A workspace for 4 chunks runs a 1000-token sequence in passes of 256 tokens with S
+    carried between them: the same bits as one pass."""
+    import torch
+    rng = np.random.default_rng(31)
+    T, H, D = 1000, 2, 128
+    q, k, v, g, beta, S0 = inputs(rng, T, H, D)
+    qs = float(np.float32(1) / np.sqrt(np.float32(D)))
+    a_o, a_S = run_chunk(gpu, q, k, v, g, beta, S0, qs)
+    dq, dk, dv, dg = (torch.from_numpy(np.ascontiguousarray(x.reshape(T, -1))).cuda() for x in (q, k, v, g))
+    db = torch.from_numpy(np.ascontiguousarray(beta)).cuda()
+    dS = torch.from_numpy(S0.copy()).cuda()
+    do = torch.full((T, H * D), float("nan"), device="cuda")
+    ws = torch.empty(gpu.kda_chunk_workspace(4 * 64, H, D), dtype=torch.uint8, device="cuda")
+    gpu.kda_chunk(dq, dk, dv, dg, db, dS, do, H, D, qs, 64, ws)
+    torch.cuda.synchronize()
+    assert np.array_equal(do.cpu().numpy().reshape(T, H, D).view(np.uint32), a_o.view(np.uint32))
+    assert np.array_equal(dS.cpu().numpy().view(np.uint32), a_S.view(np.uint32))
+
+
 def test_chunk_deterministic(gpu):
     rng = np.random.default_rng(29)
     q, k, v, g, beta, S0 = inputs(rng, 200, 2, 128)

@@ -8,6 +8,8 @@
 2. Against the CPU oracle (prep, then the sequential recurrence, on the inputs the GPU
    sees) at the chunked bar: |got - want| <= 2e-3 * rms(want) + 2e-3 |want|.
 3. Shapes outside the fused kernel are refused with K3HIP_EUNSUPPORTED / K3HIP_EINVAL.
+4. A workspace for fewer chunks than the sequence runs it in passes with the same bits (the
+   conv history carried in conv_state, or in the workspace when conv_state is NULL).
 """
 from __future__ import annotations
 
@@ -94,6 +96,40 @@ def test_prefill_bitwise_vs_prep_then_chunk(gpu, T, H, D, K, hist, fp32):
     assert torch.equal(Sa, Sb), "fused final state differs from prep + chunk"
     if csa is not None:
         assert torch.equal(csa, csb), "fused outgoing conv history differs"
+
+
+@pytest.mark.parametrize("T,H,D,K,hist,fp32,chunks", [
+    (1000, 3, 128, 4, True, False, 3),    # 16 chunks in passes of 3, a last pass of 40 tokens
+    (193, 2, 128, 4, True, False, 3),     # a last pass of 1 token: older history slots shift
+    (300, 2, 64, 3, False, True, 2),      # no caller history: it lives in the workspace
+    (130, 2, 128, 1, False, False, 1)])   # conv_k 1: no history at all
+def test_prefill_in_passes_bitwise(gpu, T, H, D, K, hist, fp32, chunks):
+    """A workspace for fewer chunks than the sequence: passes of whole chunks, the same bits."""
+    import torch
+    rng = np.random.default_rng(0x4B334441 + 11 + T + D + K)
+    qs = float(np.float32(1) / np.sqrt(np.float32(D)))
+    P = H * D
+    _, _, _, _, d, cs, S0 = setup(rng, T, H, D, K, hist, fp32)
+    oa, Sa, csa = run_fused(gpu, d, cs, S0, T, H, D, K, qs)
+    nbytes = gpu.kda_chunk_workspace(64 * chunks, H, D)
+    hist_bytes = (3 * P * (K - 1) * 4 + 255) // 256 * 256 if (cs is None and K > 1) else 0
+    ws = torch.empty(nbytes + hist_bytes, dtype=torch.uint8, device="cuda")
+    dcs = dev(cs) if cs is not None else None
+    S = dev(S0)
+    ob = torch.full((T, P), float("nan"), device="cuda")
+    args = lambda w: (*d["ins"], d["z"], d["bl"], *d["conv"], d["A_log"], d["dt"], dcs, S, ob, H, D, K,
+                      LB, qs, w)
+    gpu.kda_prefill(*args(ws))
+    torch.cuda.synchronize()
+    assert torch.equal(oa, ob), "output in passes differs from one pass"
+    assert torch.equal(Sa, S), "final state in passes differs from one pass"
+    if csa is not None:
+        assert torch.equal(csa, dcs), "outgoing conv history in passes differs from one pass"
+    # less than one chunk (and the history it needs) is refused
+    small = torch.empty(gpu.kda_chunk_workspace(64, H, D) + hist_bytes - 16, dtype=torch.uint8, device="cuda")
+    with pytest.raises(gpu.K3HipError) as e:
+        gpu.kda_prefill(*args(small))
+    assert e.value.code == 1
 
 
 @pytest.mark.parametrize("T,H,D,K,fp32", [(1, 2, 128, 4, False), (70, 2, 64, 2, False),
