@@ -136,7 +136,8 @@ def test_long_context_drift_full_heads(gpu):
     (1,024 chunks, the state carried through all of them) on fp32 conv inputs, against the
     oracle's orc_kda_core (conv, L2, decay, sequential recurrence) on the same inputs. The
     worst error of every 4,096-position window is the drift curve; with K3KDA_RECORD_DIR set
-    it is also written there as long_context_drift_h32.json."""
+    it is also written there as long_context_drift_h32.json. The same prefill in a 512 MiB
+    workspace (passes of whole chunks) must give the same bits."""
     import json
     import os
     import torch
@@ -156,6 +157,15 @@ def test_long_context_drift_full_heads(gpu):
     gpu.kda_prefill(q_in, k_in, v_in, z, bl, *conv, A_log, dt_bias, None, S, o, H, D, K, LB, qs, ws)
     torch.cuda.synchronize()
     del ws
+    # the same prefill in a 512 MiB workspace: passes of whole chunks (the conv history
+    # between them kept in the workspace), the same bits
+    ws = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+    S2 = torch.zeros((H, D, D), device="cuda")
+    o2 = torch.full((T, P), float("nan"), device="cuda")
+    gpu.kda_prefill(q_in, k_in, v_in, z, bl, *conv, A_log, dt_bias, None, S2, o2, H, D, K, LB, qs, ws)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o2) and torch.equal(S, S2), "prefill in passes differs from one pass"
+    del ws, S2, o2
     h = lambda t: t.cpu().numpy()
     arrays = {"q_conv": h(conv[0]), "k_conv": h(conv[1]), "v_conv": h(conv[2]), "A_log": h(A_log),
               "dt_bias": h(dt_bias), "o_norm": np.ones(D, np.float32)}
