@@ -9,6 +9,8 @@ Workloads (synthetic inputs resident in HBM before the timed region):
   decode   H=32, D=128, B=64 sequences, one token each: one step = K3 over all 2048
            (sequence, head) states. The state sets rotate over 4 independent buffers
            (512 MiB) so that the 256 MB last-level cache cannot hold the working set.
+  long     the prefill step above at T=65,536, then 256 single-token decode steps of the
+           same sequence (K1 at T=1 -> K3 at B=1 -> K4).
 
 Prints ONE JSON line. `value` is prefill tokens/s; the decode result (state-update GB/s)
 is the `decode` object of the same line. `roofline` is for the dominant prefill kernel;
@@ -37,6 +39,8 @@ FP32_PEAK = 157.3e12       # flop/s, dense fp32 MFMA
 # prefill core / layer at T=8192, hidden 4096; batch-64 decode
 PRE = dict(hidden=4096, H=32, D=128, T=8192, chunk=64, K=4, gate_lb=-5.0, rms_eps=1e-5)
 DEC = dict(B=64, H=32, D=128)
+# long context: the core alone over 65,536 tokens, then 256 single-token decode steps
+LONG = dict(T=65536, decode=256)
 # hybrid decode slice: 3 KDA layers + 1 gated MLA layer, decode at batch 16 over an 8192 context
 HYB = dict(hidden=7168, B=16, ctx=8192, kda_layers=3, H=32, D=128, K=4, gate_lb=-5.0,
            mla_heads=64, q_lora=1536, kv_lora=512, qk_nope=128, qk_rope=64, v_head=128)
@@ -651,6 +655,119 @@ def cpu_prefill(torch, q_in, k_in, v_in, z, b_logit, gate, conv, A_log, dt_bias,
                       f"OpenMP over heads, {el:.2f} s"}
 
 
+def bench_long(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
+    """Long context, the core alone: one prefill of T=65,536 tokens (fused K1+K2 -> K4, bf16
+    activations, zero state), then 256 single-token decode steps of the same sequence
+    (K1 at T=1 with the conv history carried -> K3 at B=1 -> K4), H=32, D=128."""
+    c = PRE
+    H, D, K, T, ND = c["H"], c["D"], c["K"], LONG["T"], LONG["decode"]
+    P, Ta = H * D, LONG["T"] + LONG["decode"]
+    g = torch.Generator(device="cuda").manual_seed(0x4B334441 + 3)
+    bf = torch.bfloat16
+    q_in, k_in, v_in = (torch.randn((Ta, P), device="cuda", generator=g).to(bf) for _ in range(3))
+    z = torch.randn((Ta, P), device="cuda", generator=g) * 0.02
+    b_logit = torch.randn((Ta, H), device="cuda", generator=g)
+    gate = torch.randn((Ta, P), device="cuda", generator=g).to(bf)
+    conv = [torch.randn((P, K), device="cuda", generator=g) * 0.5 for _ in range(3)]
+    A_log = torch.rand((H,), device="cuda", generator=g) * 1.5
+    dt_bias = torch.randn((P,), device="cuda", generator=g)
+    o_norm = 1 + 0.1 * torch.randn((D,), device="cuda", generator=g)
+    f32 = dict(device="cuda", dtype=torch.float32)
+    S = torch.zeros((H, D, D), **f32)
+    cs = torch.zeros(3 * P * (K - 1), **f32)
+    o = torch.empty((T, P), **f32)
+    y = torch.empty((T, P), device="cuda", dtype=bf)
+    ws = torch.empty(k3.kda_chunk_workspace(T, H, D, 64), dtype=torch.uint8, device="cuda")
+    qs = 1.0 / math.sqrt(D)
+    # decode tail buffers: K1 outputs for one token, the state as one B=1 slot
+    q1, k1, v1, g1, a1 = (torch.empty((1, P), **f32) for _ in range(5))
+    b1 = torch.empty((1, H), **f32)
+    o1 = torch.empty((1, P), **f32)
+    y1 = torch.empty((1, P), device="cuda", dtype=bf)
+    S1 = S.view(1, H, D, D)
+
+    def prefill():
+        S.zero_()
+        cs.zero_()
+        k3.kda_prefill(q_in[:T], k_in[:T], v_in[:T], z[:T], b_logit[:T], conv[0], conv[1], conv[2], A_log,
+                       dt_bias, cs, S, o, H, D, K, c["gate_lb"], qs, ws)
+        k3.kda_epilogue(o, gate[:T], o_norm, y, H, D, c["rms_eps"])
+
+    def tail():
+        for t in range(T, Ta):
+            k3.kda_prep(q_in[t:t + 1], k_in[t:t + 1], v_in[t:t + 1], z[t:t + 1], b_logit[t:t + 1], conv[0],
+                        conv[1], conv[2], A_log, dt_bias, cs, q1, k1, v1, g1, a1, b1, H, D, K, c["gate_lb"])
+            k3.kda_decode(S1, o1.view(1, H, D), q1.view(1, H, D), k1.view(1, H, D), v1.view(1, H, D),
+                          a1.view(1, H, D), b1, qs)
+            k3.kda_epilogue(o1, gate[t:t + 1], o_norm, y1, H, D, c["rms_eps"])
+
+    prefill()
+    tail()
+    torch.cuda.synchronize()
+    ramp(torch, prefill)
+    for _ in range(warmup):
+        prefill()
+    torch.cuda.synchronize()
+    e0, e1 = ev_pair(torch)
+    pre_ms, dec_ms = [], []
+    for _ in range(steps):
+        e0.record()
+        prefill()
+        e1.record()
+        torch.cuda.synchronize()
+        pre_ms.append(e0.elapsed_time(e1))
+        e0.record()
+        tail()
+        e1.record()
+        torch.cuda.synchronize()
+        dec_ms.append(e0.elapsed_time(e1) / ND)
+    pre, dec = sum(pre_ms) / steps, sum(dec_ms) / steps
+    out = {
+        "prefill_tokens_per_s": T / (pre * 1e-3), "prefill_ms": pre,
+        "decode_tail_ms_per_token": dec,
+        "decode_tail_note": "three launches per token from Python at B=1: bound by launch overhead, not the kernels",
+        "config": {"workload": "kda_long_context", "heads": H, "head_dim": D, "T": T, "decode_steps": ND,
+                   "chunk": 64, "conv_k": K, "activations": "bf16", "state": "fp32",
+                   "workspace_bytes": k3.kda_chunk_workspace(T, H, D, 64),
+                   "step": "prefill = k3hip_kda_prefill + k3hip_kda_epilogue; decode token = "
+                           "k3hip_kda_prep (T=1) + k3hip_kda_decode (B=1) + k3hip_kda_epilogue (T=1)"},
+    }
+    del ws
+    if cpu:
+        host = [t.cpu() for t in (q_in, k_in, v_in, z, b_logit, gate)] + [
+            t.cpu() for t in (*conv, A_log, dt_bias, o_norm)]
+        out["_cpu"] = lambda: cpu_long(host)
+    return out
+
+
+def cpu_long(host) -> dict:
+    """orc_kda_core over all 65,792 tokens (the prefill's and the decode tail's steps, one
+    sequential recurrence from zero state)."""
+    import numpy as np
+    sys.path.insert(0, str(REPO / "oracle"))
+    import k3_oracle as ko
+    c = PRE
+    H, D, K = c["H"], c["D"], c["K"]
+    Ta = LONG["T"] + LONG["decode"]
+    ci = cpu_info()
+    nt = ci["threads"]
+    cfg = ko.make_cfg(c["hidden"], H, D, K, c["gate_lb"], c["rms_eps"])
+    q_in, k_in, v_in, z, bl, gate, qc, kc, vc, A_log, dt_bias, o_norm = host
+    arrays = {"q_conv": qc.numpy(), "k_conv": kc.numpy(), "v_conv": vc.numpy(), "A_log": A_log.numpy(),
+              "dt_bias": dt_bias.numpy(), "o_norm": o_norm.numpy()}
+    for n in ("q", "k", "v", "g", "f_a", "f_b", "b", "o"):
+        arrays[n] = np.zeros((1, 1), np.float32)
+    W = ko.Weights(arrays, 0)
+    ins = [t.float().numpy() for t in (q_in, k_in, v_in, z, bl, gate)]
+    t0 = time.perf_counter()
+    ko.core(*ins, W, cfg, Ta, None, nt)
+    el = time.perf_counter() - t0
+    return {"value": Ta / el, "unit": "tokens/s", "cores": nt, "kind": "port", "cpu": ci["model"],
+            "physical_cores": ci["physical_cores"], "physical_cores_in_share": ci["physical_cores_in_share"],
+            "sample": f"C oracle orc_kda_core over all {Ta} tokens (the prefill's and the decode tail's), "
+                      f"H={H}, D={D}, OpenMP over heads, {el:.2f} s"}
+
+
 def bench_gemm(torch, k3, steps: int) -> dict:
     """The layer's projection shapes at T=8192, hidden 4096 on the hand-written MFMA GEMM
     (k3hip_proj_gemm) and on hipBLASLt (torch.mm, fp32 output), bf16 operands N(0,1), each
@@ -704,7 +821,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["all", "prefill", "decode", "layer", "hybrid", "copy", "gemm"],
+    ap.add_argument("--workload", choices=["all", "prefill", "decode", "layer", "hybrid", "long", "copy", "gemm"],
                     default="all", help="copy: the 1 GiB device copy used to calibrate HBM traffic counters; "
                     "gemm: the layer's projection shapes on the hand-written GEMM and on hipBLASLt")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -733,6 +850,9 @@ def main() -> int:
     # GPU power-limited for a while, which measured the hybrid slice ~5% slower after it
     if a.workload in ("all", "hybrid"):
         res["hybrid"] = bench_hybrid(torch, k3, a.steps, a.warmup, not a.no_cpu)
+    if a.workload in ("all", "long"):
+        res["long_context"] = bench_long(torch, k3, 3, 1, not a.no_cpu)
+        torch.cuda.empty_cache()
     if a.workload in ("all", "layer"):
         res["layer"] = bench_layer(torch, k3, max(3, a.steps // 2), a.warmup, not a.no_cpu)
     for r in res.values():   # CPU baselines last, after all GPU timing
@@ -740,8 +860,9 @@ def main() -> int:
         if f is not None:
             r["cpu_baseline"] = f()
     head = res.get("prefill") or res.get("layer") or res.get("decode")
-    if head is None:   # hybrid alone
-        print(json.dumps({"workload": "hybrid", **res["hybrid"]}))
+    if head is None:   # hybrid or long context alone
+        name = "hybrid" if "hybrid" in res else "long_context"
+        print(json.dumps({"workload": name, **res[name]}))
         return 0
     line = {
         "metric": "KDA prefill tokens/s (H=32,d=128,T=8k) + decode state-update GB/s, 1 GPU",
@@ -762,6 +883,8 @@ def main() -> int:
         line["layer"] = res["layer"]
     if "hybrid" in res:
         line["hybrid"] = res["hybrid"]
+    if "long_context" in res:
+        line["long_context"] = res["long_context"]
     print(json.dumps(line))
     return 0
 
