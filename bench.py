@@ -11,6 +11,8 @@ Workloads (synthetic inputs resident in HBM before the timed region):
            (512 MiB) so that the 256 MB last-level cache cannot hold the working set.
   long     the prefill step above at T=65,536, then 256 single-token decode steps of the
            same sequence (K1 at T=1 -> K3 at B=1 -> K4).
+  small    one KDA layer on fp32 weights, hidden 256, H=4, D=64: a 32-token prefill then 8
+           single-token decode steps.
 
 Prints ONE JSON line. `value` is prefill tokens/s; the decode result (state-update GB/s)
 is the `decode` object of the same line. `roofline` is for the dominant prefill kernel;
@@ -41,6 +43,8 @@ PRE = dict(hidden=4096, H=32, D=128, T=8192, chunk=64, K=4, gate_lb=-5.0, rms_ep
 DEC = dict(B=64, H=32, D=128)
 # long context: the core alone over 65,536 tokens, then 256 single-token decode steps
 LONG = dict(T=65536, decode=256)
+# the small CPU-runnable layer: hidden 256, H=4, D=64, fp32, 32-token prefill + 8 decode steps
+SMALL = dict(hidden=256, H=4, D=64, K=4, T=32, decode=8, gate_lb=-5.0, rms_eps=1e-5)
 # hybrid decode slice: 3 KDA layers + 1 gated MLA layer, decode at batch 16 over an 8192 context
 HYB = dict(hidden=7168, B=16, ctx=8192, kda_layers=3, H=32, D=128, K=4, gate_lb=-5.0,
            mla_heads=64, q_lora=1536, kv_lora=512, qk_nope=128, qk_rope=64, v_head=128)
@@ -454,6 +458,98 @@ def cpu_layer(host: dict, x) -> dict:
                       f"D={c['D']}, bf16 weights, zero state, OpenMP {nt} threads, {el:.2f} s"}
 
 
+def bench_small(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
+    """The small CPU-runnable layer: one KDA layer on fp32 weights N(0, 0.02) (hidden 256, H=4,
+    D=64, conv 4), a 32-token prefill then 8 single-token decode steps carrying the state,
+    x N(0, 1), A_log U(0, 1.5), dt_bias N(0, 1) -- nine k3hip_kda_layer_dev calls per step."""
+    import ctypes as C
+    import numpy as np
+    c = SMALL
+    E, H, D, K, T, ND = c["hidden"], c["H"], c["D"], c["K"], c["T"], c["decode"]
+    P = H * D
+    rng = np.random.default_rng(0x4B334441 + 0)
+    nrm = lambda *s: (rng.standard_normal(s) * 0.02).astype(np.float32)
+    host = {"q": nrm(P, E), "k": nrm(P, E), "v": nrm(P, E), "g": nrm(P, E), "o": nrm(E, P), "f_a": nrm(D, E),
+            "f_b": nrm(P, D), "b": nrm(H, E), "q_conv": nrm(P, K), "k_conv": nrm(P, K), "v_conv": nrm(P, K),
+            "A_log": rng.uniform(0, 1.5, H).astype(np.float32),
+            "dt_bias": rng.standard_normal(P).astype(np.float32),
+            "o_norm": (1 + 0.02 * rng.standard_normal(D)).astype(np.float32)}
+    w = k3.K3KdaW()
+    C.memset(C.byref(w), 0, C.sizeof(w))
+    for n, a in host.items():
+        setattr(w, n, a.ctypes.data)
+    w.wdt = 0
+    cfg = k3.make_cfg(E, H, D, K, c["gate_lb"], c["rms_eps"])
+    dw = k3.DeviceWeights(w, cfg, k3.UPLOAD_DEV)
+    xs = rng.standard_normal((T + ND, E)).astype(np.float32)
+    x = torch.from_numpy(xs).cuda()
+    out = torch.empty((T + ND, E), device="cuda")
+    state = torch.zeros(P * D + 3 * P * (K - 1), device="cuda")
+
+    def step():
+        state.zero_()
+        dw.layer(out[:T], x[:T], state, T)
+        for t in range(T, T + ND):
+            dw.layer(out[t:t + 1], x[t:t + 1], state, 1)
+
+    step()
+    torch.cuda.synchronize()
+    ramp(torch, step)
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = ev_pair(torch)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    step_s = e0.elapsed_time(e1) * 1e-3 / steps
+    dw.close()
+    out_d = {"value": (T + ND) / step_s, "unit": "tokens/s", "ms_per_step": step_s * 1e3,
+             "config": {"workload": "kda_small_layer", "hidden": E, "heads": H, "head_dim": D, "conv_k": K,
+                        "prefill_T": T, "decode_steps": ND, "weights": "fp32", "activations": "fp32",
+                        "entry_point": "k3hip_kda_layer_dev (exact-order fp32 projections), nine calls per step",
+                        "note": "launch-bound at this size"}}
+    if cpu:
+        out_d["_cpu"] = lambda: cpu_small(host, xs)
+    return out_d
+
+
+def cpu_small(host: dict, xs) -> dict:
+    """The reference's own k3_kda_layer (compiled from its sources into oracle/_ref; the C
+    restatement where that is absent) on the same sequence: the 32-token prefill then 8
+    single-token steps, repeated for a few seconds."""
+    import numpy as np
+    sys.path.insert(0, str(REPO / "oracle"))
+    import k3_oracle as ko
+    c = SMALL
+    ci = cpu_info()
+    nt = ci["threads"]
+    set_omp_threads(nt)
+    L, kind = ko.ref(), "reference"
+    if L is None:
+        L, kind = ko.orc(), "port"
+    W = ko.Weights(dict(host), 0)
+    cfg = ko.make_cfg(c["hidden"], c["H"], c["D"], c["K"], c["gate_lb"], c["rms_eps"])
+    P, T, ND = c["H"] * c["D"], c["T"], c["decode"]
+    n, t0 = 0, time.perf_counter()
+    while True:
+        st = np.zeros(P * c["D"] + 3 * P * (c["K"] - 1), np.float32)
+        ko.kda_layer(L, np.ascontiguousarray(xs[:T]), W, cfg, T, st)
+        for t in range(T, T + ND):
+            ko.kda_layer(L, np.ascontiguousarray(xs[t:t + 1]), W, cfg, 1, st)
+        n += 1
+        el = time.perf_counter() - t0
+        if el > 3.0:
+            break
+    return {"value": n * (T + ND) / el, "unit": "tokens/s", "cores": nt, "kind": kind, "cpu": ci["model"],
+            "physical_cores": ci["physical_cores"], "physical_cores_in_share": ci["physical_cores_in_share"],
+            "sample": f"k3_kda_layer ({'reference C from its own sources' if kind == 'reference' else 'C oracle'}), "
+                      f"{n} sequences of a {T}-token prefill + {ND} decode steps, hidden {c['hidden']}, "
+                      f"H={c['H']}, D={c['D']}, fp32 weights, OpenMP {nt} threads, {el:.2f} s"}
+
+
 def bench_hybrid(torch, k3, steps: int, warmup: int, cpu: bool = False) -> dict:
     """Hybrid slice: one decode step of batch 16 through 3 KDA layers (k3hip_kda_layer_decode) and one
     gated MLA layer with absorbed weights over an 8192-position latent cache
@@ -821,7 +917,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["all", "prefill", "decode", "layer", "hybrid", "long", "copy", "gemm"],
+    ap.add_argument("--workload", choices=["all", "prefill", "decode", "layer", "hybrid", "long", "small", "copy",
+                                           "gemm"],
                     default="all", help="copy: the 1 GiB device copy used to calibrate HBM traffic counters; "
                     "gemm: the layer's projection shapes on the hand-written GEMM and on hipBLASLt")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -853,6 +950,8 @@ def main() -> int:
     if a.workload in ("all", "long"):
         res["long_context"] = bench_long(torch, k3, 3, 1, not a.no_cpu)
         torch.cuda.empty_cache()
+    if a.workload in ("all", "small"):
+        res["small_layer"] = bench_small(torch, k3, a.steps, a.warmup, not a.no_cpu)
     if a.workload in ("all", "layer"):
         res["layer"] = bench_layer(torch, k3, max(3, a.steps // 2), a.warmup, not a.no_cpu)
     for r in res.values():   # CPU baselines last, after all GPU timing
@@ -860,8 +959,8 @@ def main() -> int:
         if f is not None:
             r["cpu_baseline"] = f()
     head = res.get("prefill") or res.get("layer") or res.get("decode")
-    if head is None:   # hybrid or long context alone
-        name = "hybrid" if "hybrid" in res else "long_context"
+    if head is None:   # hybrid, long context or the small layer alone
+        name = next(iter(res))
         print(json.dumps({"workload": name, **res[name]}))
         return 0
     line = {
@@ -885,6 +984,8 @@ def main() -> int:
         line["hybrid"] = res["hybrid"]
     if "long_context" in res:
         line["long_context"] = res["long_context"]
+    if "small_layer" in res:
+        line["small_layer"] = res["small_layer"]
     print(json.dumps(line))
     return 0
 
