@@ -551,7 +551,9 @@ extern "C" int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *
         // 9 o_proj on fp16 MFMA against the fp16 copy of W_o
         return mm(T, E, (int)P, K3_DT_F16, y16, (long)P, w->o16, (long)P, out, out_dtype, E, st);
     }
-    float *gl = z;   // the fallback keeps fp32 gate logits; z is consumed by now
+    // hipBLASLt has no bf16-in, fp16-out algorithm: this path keeps fp32 gate logits (z is
+    // consumed by now)
+    float *gl = z;
     if ((rc = gemm_bf16(T, (int)P, E, xb, w->g, gl, K3HIP_F32, st))) return rc;
     if ((rc = epilogue_split(T, H, D, w->rms_eps, o, gl, K3HIP_F32, w->o_norm, y16, st, true))) return rc;
     if (out_dtype == K3HIP_F32) return gemm_f16(T, E, (int)P, y16, w->o16, out, K3HIP_F32, st);
