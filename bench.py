@@ -315,6 +315,7 @@ def bench_prefill(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
     out = {
         "value": T / step_s, "unit": "tokens/s", "ms_per_step": step_s * 1e3,
         "core_ms_avg": kavg * 1e3, "core_ms_median": ks[len(ks) // 2] * 1e3,
+        "core_ms_min": ks[0] * 1e3, "core_ms_max": ks[-1] * 1e3,
         "config": {"workload": "kda_prefill_core", "hidden": c["hidden"], "heads": H, "head_dim": D,
                    "T": T, "chunk": 64, "batch": 1, "conv_k": K, "activations": "bf16",
                    "state": "fp32", "core": kname},
