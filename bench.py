@@ -941,7 +941,9 @@ def main() -> int:
         return 0
     res = {}
     if a.workload in ("all", "decode"):
-        res["decode"] = bench_decode(torch, k3, max(a.steps, 50), a.warmup + 2, not a.no_cpu)
+        # 1,000 launches (~48 ms) per repeat: the host's synchronize after a repeat then adds
+        # well under 0.1 us per launch to the wall figure (50 launches: ~0.6 us)
+        res["decode"] = bench_decode(torch, k3, max(a.steps, 1000), a.warmup + 2, not a.no_cpu)
     if a.workload in ("all", "prefill"):
         res["prefill"] = bench_prefill(torch, k3, a.steps, a.warmup, not a.no_cpu)
     # the streaming (HBM-bound) workloads before the layer: its seconds of dense MFMA leave the
