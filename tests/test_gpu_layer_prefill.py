@@ -4,8 +4,8 @@ hipBLASLt, the fused conv..recurrence, the epilogue and o_proj, against the CPU 
 k3_kda_layer on the same bf16 weights and the same bf16-rounded inputs.
 
 The GPU projections accumulate in fp32 (the oracle in double) and the core runs on
-split-bf16 MFMA; f_a and the epilogue output reach their GEMMs as bf16 hi/lo pairs, so no
-intermediate is rounded to bf16. Held to the chunked bf16-MFMA bar:
+split-bf16 MFMA; f_a reaches its GEMM as a bf16 hi/lo pair and the RMS-normalised epilogue
+output as fp16 (against an exact fp16 copy of W_o), so no intermediate is rounded to bf16. Held to the chunked bf16-MFMA bar:
 |got - want| <= 2e-3 * rms(want) + 2e-3 |want|, for the layer output and the carried state
 (recurrent part and conv history), over two prefills in a row with the state carried.
 """
@@ -58,11 +58,29 @@ def test_layer_prefill_vs_oracle(gpu, hidden, H, D, K, Ts, gemm):
         gpu.set_projection_gemm(gpu.GEMM_HIPBLASLT)
 
 
-def _layer_prefill_vs_oracle(gpu, hidden, H, D, K, Ts):
+@pytest.mark.parametrize("case", range(12))
+def test_layer_prefill_random_shapes_vs_oracle(gpu, case):
+    """Seeded random layers: hidden a multiple of 64 in [128, 768], H 1-5, D 64 or 128,
+    conv_k 1-4, a gate bound the chunked form takes, two calls carrying the state; even cases
+    on hipBLASLt, odd ones on the hand-written GEMM."""
+    rng = np.random.default_rng(0x4B334441 + 0x1A7E + case)
+    hidden, H = 64 * int(rng.integers(2, 13)), int(rng.integers(1, 6))
+    D, K = int(rng.choice([64, 128])), int(rng.integers(1, 5))
+    Ts = (int(rng.integers(1, 401)), int(rng.integers(1, 401)))
+    lb = float(np.float32(-rng.uniform(0.1, 5.3)))
+    gpu.set_projection_gemm(gpu.GEMM_HANDWRITTEN if case % 2 else gpu.GEMM_HIPBLASLT)
+    try:
+        _layer_prefill_vs_oracle(gpu, hidden, H, D, K, Ts, lb, 0x4B334441 + 0x1A7E + case)
+    finally:
+        gpu.set_projection_gemm(gpu.GEMM_HIPBLASLT)
+
+
+def _layer_prefill_vs_oracle(gpu, hidden, H, D, K, Ts, lb=-5.0, seed=None):
     import torch
-    rng = np.random.default_rng(0x4B334441 + 2 + hidden + sum(Ts))
+    rng = np.random.default_rng(0x4B334441 + 2 + hidden + sum(Ts) if seed is None else seed)
+    print(f"hidden={hidden} H={H} D={D} K={K} T={Ts} gate_lb={lb:.3f}", flush=True)
     W = layer_weights(rng, hidden, H, D, K)
-    cfg = ko.make_cfg(hidden, H, D, K, -5.0, 1e-5)
+    cfg = ko.make_cfg(hidden, H, D, K, lb, 1e-5)
     P = H * D
     nst = P * D + 3 * P * (K - 1)
     st_ref = np.zeros(nst, np.float32)
