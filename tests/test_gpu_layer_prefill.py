@@ -98,7 +98,9 @@ def _layer_prefill_vs_oracle(gpu, hidden, H, D, K, Ts, lb=-5.0, seed=None):
         ro = assert_close(got, want, TOL * rms(want), TOL, f"layer T={T} out")
         rs = assert_close(gst[:P * D], st_ref[:P * D], TOL * rms(st_ref[:P * D]), TOL, f"layer T={T} S")
         # the conv history holds the last projected inputs: fp32 vs double accumulation
-        assert_close(gst[P * D:], st_ref[P * D:], 1e-5 * rms(st_ref[P * D:]), 1e-5, f"layer T={T} conv history")
+        if K > 1:
+            assert_close(gst[P * D:], st_ref[P * D:], 1e-5 * rms(st_ref[P * D:]), 1e-5,
+                         f"layer T={T} conv history")
         print(f"hidden={hidden} H={H} D={D} K={K} call {i} T={T}: worst {ro:.3f}x (out) / "
               f"{rs:.3f}x (S) of the 2e-3 bar")
     dw.close()
