@@ -189,10 +189,26 @@ def test_batched_layer_decode_vs_oracle(gpu, D, K, B, lb):
     k3_kda_layer with T = 1 on its own state, at the decode bar (rtol 1e-4, atol 1e-4*rms).
     B = 17 and 70 take two 16-row tiles and two 64-row passes of the projection kernel; D = 16
     gives K = 16 for f_b. The lb = 0 case runs the unbounded softplus gate (parity unpinned)."""
+    _batched_layer_decode(gpu, D, K, B, lb, 3, 192, 0x4B334441 + 25 + D + B)
+
+
+@pytest.mark.parametrize("case", range(10))
+def test_batched_layer_decode_random_vs_oracle(gpu, case):
+    """Seeded random batched decodes at the decode bar: D 16-128, conv_k 1-4, B 1-40, 1-4 heads,
+    hidden a multiple of 64 in [64, 512], a gate bound in [-5.3, -0.1] (every fourth case the
+    unbounded softplus gate)."""
+    rng = np.random.default_rng(0x4B334441 + 0xDEC + case)
+    D, K = int(rng.choice([16, 32, 64, 128])), int(rng.integers(1, 5))
+    B, Hh, hid = int(rng.integers(1, 41)), int(rng.integers(1, 5)), 64 * int(rng.integers(1, 9))
+    lb = 0.0 if case % 4 == 3 else float(np.float32(-rng.uniform(0.1, 5.3)))
+    _batched_layer_decode(gpu, D, K, B, lb, Hh, hid, 0x4B334441 + 0xDEC + case)
+
+
+def _batched_layer_decode(gpu, D, K, B, lb, Hh, hid, seed):
     import torch
     from test_oracle_ref import bf16
-    rng = np.random.default_rng(0x4B334441 + 25 + D + B)
-    Hh, hid = 3, 192
+    rng = np.random.default_rng(seed)
+    print(f"D={D} K={K} B={B} heads={Hh} hidden={hid} gate_lb={lb:.3f}", flush=True)
     P = Hh * D
     cfg = ko.make_cfg(hid, Hh, D, K, lb, 1e-5)
     nrm = lambda *s: rng.standard_normal(s) * 0.05
@@ -223,5 +239,5 @@ def test_batched_layer_decode_vs_oracle(gpu, D, K, B, lb):
     for b in range(B):
         assert_close(st[b, :kper], host[b], 1e-4 * rms(host[b]), 1e-4, f"state of sequence {b}")
         assert np.all(st[b, kper:] == 0.0), "padding between slots untouched"
-    print(f"D={D} K={K} B={B} lb={lb}: worst {worst:.3f}x of the 1e-4 bar")
+    print(f"  worst {worst:.3f}x of the 1e-4 bar")
     dw.close()
