@@ -42,8 +42,27 @@ def mla_case(rng, hidden, H, ql, kvl, qn, qr, vh, gate=1):
     (256, 64, 64, 512, 32, 64, 32, 2, 150, 1),   # the 576-channel latent + rope rows of Kimi K3
 ])
 def test_mla_decode_vs_expanded_oracle(gpu, hidden, H, ql, kvl, qn, qr, vh, B, T, gate):
+    _mla_decode_vs_oracle(gpu, hidden, H, ql, kvl, qn, qr, vh, B, T, gate, 0x4B334441 + 4 + hidden + B + T)
+
+
+@pytest.mark.parametrize("case", range(10))
+def test_mla_decode_random_vs_expanded_oracle(gpu, case):
+    """Seeded random MLA layers inside the one-pass attention kernel's geometry: 1-64 heads,
+    kv_lora a multiple of 16 up to 512, rope 8-64 channels, nope and v heads 16-64, gated or
+    not, B 1-12 sequences over 1-40 steps."""
+    rng = np.random.default_rng(0x4B334441 + 0x31A + case)
+    hidden, H, ql = 64 * int(rng.integers(1, 7)), int(rng.integers(1, 65)), 32 * int(rng.integers(1, 5))
+    kvl, qr = 16 * int(rng.integers(1, 33)), int(rng.choice([8, 16, 32, 64]))
+    qn, vh = int(rng.choice([16, 32, 64])), int(rng.choice([16, 32, 64]))
+    B, T, gate = int(rng.integers(1, 13)), int(rng.integers(1, 41)), int(rng.integers(0, 2))
+    _mla_decode_vs_oracle(gpu, hidden, H, ql, kvl, qn, qr, vh, B, T, gate, 0x4B334441 + 0x31A + case)
+
+
+def _mla_decode_vs_oracle(gpu, hidden, H, ql, kvl, qn, qr, vh, B, T, gate, seed):
     import torch
-    rng = np.random.default_rng(0x4B334441 + 4 + hidden + B + T)
+    rng = np.random.default_rng(seed)
+    print(f"hidden={hidden} H={H} q_lora={ql} kv_lora={kvl} nope={qn} rope={qr} v_head={vh} B={B} T={T} "
+          f"gate={gate}", flush=True)
     cfg, W = mla_case(rng, hidden, H, ql, kvl, qn, qr, vh, gate)
     cap = T + 3
     kvcs = [np.zeros((cap, H * (qn + vh)), np.float32) for _ in range(B)]
@@ -60,7 +79,7 @@ def test_mla_decode_vs_expanded_oracle(gpu, hidden, H, ql, kvl, qn, qr, vh, B, T
         got = out.cpu().numpy()
         assert_close(got, want, 1e-4 * rms(want), 1e-4, f"MLA step {t}")
         worst = max(worst, worst_ratio(got, want, 1e-4 * rms(want), 1e-4))
-    print(f"hidden={hidden} H={H} B={B} T={T} gate={gate}: worst {worst:.3f}x of the 1e-4 bar")
+    print(f"  worst {worst:.3f}x of the 1e-4 bar")
     mw.close()
 
 
