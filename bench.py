@@ -405,6 +405,7 @@ def bench_layer(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
     finally:
         k3.set_projection_gemm(k3.GEMM_HIPBLASLT)
     dw.close()
+    dropin = bench_dropin(torch, k3, w, cfg, x_host)
     out_d = {
         "value": T / step_s, "unit": "tokens/s", "ms_per_step": step_s * 1e3,
         "wall_ms_per_step": wall / steps * 1e3,
@@ -418,10 +419,49 @@ def bench_layer(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
         "hand_written_gemms": {"ms_per_step": hw_s * 1e3, "tokens_per_s": T / hw_s,
                                "frac_bf16_peak": flops / hw_s / BF16_PEAK,
                                "note": "the same step with every projection on k3hip_proj_gemm's kernel"},
+        "dropin": dropin,
     }
     if cpu:   # timed after every GPU workload
         out_d["_cpu"] = lambda: cpu_layer(host, x_host)
     return out_d
+
+
+def bench_dropin(torch, k3, w, cfg, x_host) -> dict:
+    """The drop-in k3_kda_layer itself (host pointers, the reference's signature) on the layer
+    workload's bf16 weights: a T=8192 prefill from a zero state and single-token decode calls
+    from the state it leaves, timed on the host clock around each call (its weight upload, the
+    host-to-device and device-to-host copies and the compute: the call is synchronous)."""
+    import numpy as np
+    T, E = x_host.shape
+    P = cfg.kda_heads * cfg.kda_head_dim
+    nst = P * cfg.kda_head_dim + 3 * P * (cfg.conv_k - 1)
+    out = np.empty((T, E), np.float32)
+    st = np.zeros(nst, np.float32)
+    k3.kda_layer_host(out, x_host, w, cfg, T, st)   # first call: page-in and kernel loads
+    pre = []
+    for _ in range(3):
+        st[:] = 0
+        t0 = time.perf_counter()
+        k3.kda_layer_host(out, x_host, w, cfg, T, st)
+        pre.append(time.perf_counter() - t0)
+    moved = k3.dropin_bytes()
+    dec = []
+    o1 = np.empty((1, E), np.float32)
+    for i in range(10):
+        x1 = np.ascontiguousarray(x_host[i:i + 1])
+        t0 = time.perf_counter()
+        k3.kda_layer_host(o1, x1, w, cfg, 1, st)
+        dec.append(time.perf_counter() - t0)
+    moved1 = k3.dropin_bytes()
+    p_ms, d_ms = 1e3 * sorted(pre)[1], 1e3 * sorted(dec)[len(dec) // 2]
+    return {"prefill_ms": p_ms, "prefill_tokens_per_s": T / (p_ms * 1e-3), "prefill_bytes_moved": moved,
+            "decode_ms_per_call": d_ms, "decode_bytes_moved": moved1,
+            "config": {"entry_point": "k3_kda_layer (host pointers)", "hidden": E, "heads": cfg.kda_heads,
+                       "head_dim": cfg.kda_head_dim, "T": T, "weights": "bf16",
+                       "projections": "T >= 16: bf16 MFMA GEMMs of x split into bf16 hi + lo (fp32 accuracy); "
+                                      "T = 1: double-accumulating GEMV"},
+            "note": "median host time per call; every call uploads the layer's weights (the reference binds "
+                    "them per call) and copies x, out and the state between host and device"}
 
 
 def cpu_layer(host: dict, x) -> dict:
@@ -754,8 +794,11 @@ def cpu_prefill(torch, q_in, k_in, v_in, z, b_logit, gate, conv, A_log, dt_bias,
 
 def bench_long(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
     """Long context, the core alone: one prefill of T=65,536 tokens (fused K1+K2 -> K4, bf16
-    activations, zero state), then 256 single-token decode steps of the same sequence
-    (K1 at T=1 with the conv history carried -> K3 at B=1 -> K4), H=32, D=128."""
+    activations, zero state), then 256 single-token decode steps of the same sequence, H=32,
+    D=128. A decode step is one k3hip_kda_decode_step launch (K1 at T=1 with the conv history
+    carried, K3 at B=1, K4); the 256 launches are captured in one HIP graph and its replay is
+    timed with HIP events (device time per token), beside the same launches issued one by one
+    from Python (host-bound)."""
     c = PRE
     H, D, K, T, ND = c["H"], c["D"], c["K"], LONG["T"], LONG["decode"]
     P, Ta = H * D, LONG["T"] + LONG["decode"]
@@ -776,12 +819,9 @@ def bench_long(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
     y = torch.empty((T, P), device="cuda", dtype=bf)
     ws = torch.empty(k3.kda_chunk_workspace(T, H, D, 64), dtype=torch.uint8, device="cuda")
     qs = 1.0 / math.sqrt(D)
-    # decode tail buffers: K1 outputs for one token, the state as one B=1 slot
-    q1, k1, v1, g1, a1 = (torch.empty((1, P), **f32) for _ in range(5))
-    b1 = torch.empty((1, H), **f32)
-    o1 = torch.empty((1, P), **f32)
-    y1 = torch.empty((1, P), device="cuda", dtype=bf)
-    S1 = S.view(1, H, D, D)
+    # decode tail: the state as one B=1 slot, one output row per token
+    S1, cs1 = S.view(1, H, D, D), cs.view(1, -1)
+    y_dec = torch.empty((ND, P), device="cuda", dtype=bf)
 
     def prefill():
         S.zero_()
@@ -791,22 +831,34 @@ def bench_long(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
         k3.kda_epilogue(o, gate[:T], o_norm, y, H, D, c["rms_eps"])
 
     def tail():
-        for t in range(T, Ta):
-            k3.kda_prep(q_in[t:t + 1], k_in[t:t + 1], v_in[t:t + 1], z[t:t + 1], b_logit[t:t + 1], conv[0],
-                        conv[1], conv[2], A_log, dt_bias, cs, q1, k1, v1, g1, a1, b1, H, D, K, c["gate_lb"])
-            k3.kda_decode(S1, o1.view(1, H, D), q1.view(1, H, D), k1.view(1, H, D), v1.view(1, H, D),
-                          a1.view(1, H, D), b1, qs)
-            k3.kda_epilogue(o1, gate[t:t + 1], o_norm, y1, H, D, c["rms_eps"])
+        for i in range(ND):
+            t = T + i
+            k3.kda_decode_step(q_in[t:t + 1], k_in[t:t + 1], v_in[t:t + 1], z[t:t + 1], b_logit[t:t + 1],
+                               gate[t:t + 1], conv[0], conv[1], conv[2], A_log, dt_bias, o_norm, cs1, S1,
+                               y_dec[i:i + 1], H, D, K, c["gate_lb"], c["rms_eps"], qs)
 
     prefill()
     tail()
     torch.cuda.synchronize()
+    # the 256 decode launches as one graph (no memset nodes: the step kernel only reads and
+    # writes its operands), captured after an eager pass on the capture's side stream
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        tail()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        tail()
+    torch.cuda.synchronize()
     ramp(torch, prefill)
     for _ in range(warmup):
         prefill()
+        graph.replay()
     torch.cuda.synchronize()
     e0, e1 = ev_pair(torch)
-    pre_ms, dec_ms = [], []
+    pre_ms, dec_ms, eager_ms = [], [], []
     for _ in range(steps):
         e0.record()
         prefill()
@@ -814,20 +866,31 @@ def bench_long(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
         torch.cuda.synchronize()
         pre_ms.append(e0.elapsed_time(e1))
         e0.record()
-        tail()
+        graph.replay()
         e1.record()
         torch.cuda.synchronize()
         dec_ms.append(e0.elapsed_time(e1) / ND)
-    pre, dec = sum(pre_ms) / steps, sum(dec_ms) / steps
+        e0.record()
+        tail()
+        e1.record()
+        torch.cuda.synchronize()
+        eager_ms.append(e0.elapsed_time(e1) / ND)
+    pre, dec, eager = sum(pre_ms) / steps, sum(dec_ms) / steps, sum(eager_ms) / steps
+    floor_us = decode_bytes_per_token(H, D) / HBM_PEAK * 1e6
     out = {
         "prefill_tokens_per_s": T / (pre * 1e-3), "prefill_ms": pre,
         "decode_tail_ms_per_token": dec,
-        "decode_tail_note": "three launches per token from Python at B=1: bound by launch overhead, not the kernels",
+        "decode_tail_hbm_floor_ms_per_token": floor_us * 1e-3,
+        "decode_tail_roofline_frac": floor_us * 1e-3 / dec,
+        "decode_tail_eager_ms_per_token": eager,
+        "decode_tail_note": "one k3hip_kda_decode_step launch per token at B=1 (32 workgroups, one per head); "
+                            "the 256 launches replayed as one HIP graph, HIP events around the replay; the eager "
+                            "figure issues the same launches one by one from Python (host-bound)",
         "config": {"workload": "kda_long_context", "heads": H, "head_dim": D, "T": T, "decode_steps": ND,
                    "chunk": 64, "conv_k": K, "activations": "bf16", "state": "fp32",
                    "workspace_bytes": k3.kda_chunk_workspace(T, H, D, 64),
                    "step": "prefill = k3hip_kda_prefill + k3hip_kda_epilogue; decode token = "
-                           "k3hip_kda_prep (T=1) + k3hip_kda_decode (B=1) + k3hip_kda_epilogue (T=1)"},
+                           "k3hip_kda_decode_step (K1 at T=1 + K3 at B=1 + K4, one launch)"},
     }
     del ws
     if cpu:
@@ -979,6 +1042,7 @@ def main() -> int:
     }
     if head is res.get("layer"):
         line["hand_written_gemms"] = head["hand_written_gemms"]
+        line["dropin"] = head["dropin"]
     if "prefill" in res and "decode" in res:
         line["decode"] = res["decode"]
     if "layer" in res and head is not res["layer"]:

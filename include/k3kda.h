@@ -207,6 +207,24 @@ int k3hip_kda_recurrent(int T, int H, int D,
                         const float *alpha, const float *beta, float q_scale,
                         float *S, float *o, void *stream);
 
+/* K1 (T = 1) + K3 + K4 in one launch: one decode token for each of B sequences, the work of
+ * k3hip_kda_prep on one token, k3hip_kda_decode and k3hip_kda_epilogue (src/core/k3_ops.c:888-947
+ * at T = 1) without q, k, v, alpha, beta or o leaving the chip. One workgroup per (head,
+ * sequence); the state is read once and written once.
+ *   q_in,k_in,v_in [B][P] (in_dtype)  z [B][P] fp32 = f_b(f_a(x)) before dt_bias
+ *   b_logit [B][H] fp32               gate [B][P] output-gate logits (gate_dtype)
+ *   conv_state [B][3][P][K-1] in/out (may be NULL only for conv_k = 1)
+ *   S [B][H][D][D] in/out             y [B][P] = RMSNorm(o) * sigmoid(gate) (y_dtype)
+ * D in {16, 32, 64, 128}, conv_k 1..4, gate_lb <= 0 (0 selects the softplus gate); S and
+ * o_norm 16-byte aligned, gate and y 16-byte (fp32) or 8-byte (bf16) aligned. */
+int k3hip_kda_decode_step(int B, int H, int D, int K, float gate_lb, float rms_eps, int in_dtype,
+                          const void *q_in, const void *k_in, const void *v_in, const float *z,
+                          const float *b_logit, const void *gate, int gate_dtype,
+                          const float *q_conv, const float *k_conv, const float *v_conv,
+                          const float *A_log, const float *dt_bias, const float *o_norm,
+                          float *conv_state, float q_scale, float *S, void *y, int y_dtype,
+                          void *stream);
+
 /* K4: per (token, head) RMSNorm over D with the shared weight o_norm[D] (eps inside the
  * root, double-width mean in the reference, src/core/k3_ops.c:94-102), THEN multiply by
  * sigmoid(gate). Replaces src/core/k3_ops.c:940-947 up to the o_proj matmul.
@@ -227,8 +245,13 @@ enum { K3HIP_F16 = 3 };
 int k3hip_proj_gemm(int M, int N, int K, int ab_dtype, const void *A, long lda, const void *B, long ldb,
                     void *C, int c_dtype, long ldc, void *stream);
 
-/* Device-resident weights for the full layer. Matrices keep their wdt (fp32 or bf16);
- * the small fp32 vectors are copied as is. */
+/* Device-resident weights for the full layer. Matrices keep their wdt: fp32, bf16, or the
+ * per-row int8 draft format K3_WI8 (include/k3/k3.h:266-283, each row [f32 scale][int8 * in],
+ * which the reference engine binds for its --draft-trunk hybrid decode, src/model/k3_bind.c:441);
+ * the small fp32 vectors are copied as is. Int8 weights serve k3hip_kda_layer_dev and the
+ * drop-in k3_kda_layer (the reference's k3_matmul_q8 arithmetic, src/core/k3_ops.c:1228-1301,
+ * summed in double: within float rounding of the reference, which states no exactness
+ * contract for the format); the bf16 prefill and batched decode paths refuse them. */
 typedef struct k3hip_kda_weights k3hip_kda_weights;
 int k3hip_kda_upload(const K3KdaW *w, const K3Cfg *c, k3hip_kda_weights **out);
 int k3hip_kda_release(k3hip_kda_weights *w);
@@ -270,7 +293,9 @@ int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *out, int ou
  * (the default; hipBLASLt's heuristic first choice for each shape) or K3HIP_GEMM_HANDWRITTEN
  * (k3hip_proj_gemm's kernel for every projection, the gate logits in fp16, f_a/b split over
  * K). Both hold the same 2e-3 bar but give different bits; change it only while no layer
- * prefill is in flight. K3HIP_EINVAL for another value. No counterpart in the reference,
+ * prefill is in flight. K3HIP_EINVAL for another value. The hand-written kernel needs
+ * hidden % 64 == 0 and, for bf16 x, a 16-byte aligned x: a layer outside that runs its
+ * projections on hipBLASLt whatever the setting. No counterpart in the reference,
  * whose projections are one CPU routine (k3_matmul_bf16, src/core/k3_ops.c:1122-1227). */
 enum { K3HIP_GEMM_HIPBLASLT = 0, K3HIP_GEMM_HANDWRITTEN = 1 };
 int k3hip_set_projection_gemm(int impl);
@@ -281,18 +306,22 @@ int k3hip_set_projection_gemm(int impl);
  * element split into bf16 hi + lo in registers); needs hidden % 8 == 0 and x 16-byte
  * aligned. Sequence b's state (S then conv history, the reference layout)
  * starts at states + b * state_stride floats (>= H*D*D + 3*P*(conv_k-1), a multiple of 4).
- * x, out [B][hidden] fp32. */
+ * x, out [B][hidden] fp32. When o_proj runs as two K-ranges and `out` is ordinary
+ * (coarse-grained) device memory, both ranges are added into `out` by float atomics; on
+ * pinned-host, managed or fine-grained memory the ranges are summed by a reduction launch
+ * instead (the same bits unless a partial is denormal). */
 int k3hip_kda_layer_decode(const k3hip_kda_weights *w, int B, float *out, const float *x,
                            float *states, long state_stride, void *stream);
 
 /* k3hip_kda_layer_decode that allocates nothing: for callers that cannot call hipMalloc
  * (code under HIP graph capture, tight serving loops, harnesses that forbid allocation). No
  * counterpart in the reference. Same arguments, results bit-identical to
- * k3hip_kda_layer_decode. Its scratch (projections, split-K partial planes, z, y) is a
- * fixed 64 MiB device array inside this library, one per GPU, held until the process ends;
+ * k3hip_kda_layer_decode. Its scratch (projections, split-K partial planes, y) is a
+ * fixed 16 MiB device array inside this library, one per GPU, held until the process ends;
  * a call whose B and layer width need more returns K3HIP_EINVAL (at hidden 7168 with 32 x 128
- * heads that is beyond about 300 sequences). Every call on one GPU uses that GPU's array:
- * calls that overlap on one GPU (other streams, other threads) race; serialise them. */
+ * heads: more than 99 sequences), as does any step that would need scratch beyond it (the
+ * call allocates nothing, ever). Every call on one GPU uses that GPU's array: calls that
+ * overlap on one GPU (other streams, other threads) race; serialise them. */
 int k3hip_kda_layer_decode_noalloc(const k3hip_kda_weights *w, int B, float *out, const float *x,
                                    float *states, long state_stride, void *stream);
 

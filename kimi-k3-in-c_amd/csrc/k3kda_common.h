@@ -66,4 +66,18 @@ __device__ __forceinline__ float softplus_ref(float x) { return x > 20.0f ? x : 
 
 inline bool is_pow2_head(int D) { return D == 16 || D == 32 || D == 64 || D == 128; }
 
+// True when p is ordinary (coarse-grained) device memory, where the hardware float atomics
+// are exact: hipMalloc, hipMallocAsync and torch's allocator. Host-pinned, managed and
+// fine-grained allocations (hipHostMalloc, hipMallocManaged, hipExtMallocWithFlags with a
+// fine-grained or uncached flag), and pointers HIP does not know, give false.
+inline bool coarse_device_mem(const void *p)
+{
+    hipPointerAttribute_t a{};
+    if (hipPointerGetAttributes(&a, p) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return a.type == hipMemoryTypeDevice && !a.isManaged && (a.allocationFlags & hipDeviceMallocFinegrained) == 0;
+}
+
 }  // namespace k3kda

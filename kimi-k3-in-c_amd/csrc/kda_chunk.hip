@@ -1079,8 +1079,9 @@ __global__ __launch_bounds__(512) void kda_chunk_state(int T, int H, const char 
             for (int i = 0; i < TPL; i++) asm volatile("" ::"v"(t[i]));
         };
         int tA[TPL], tB[TPL];
-        // this thread's channel of the outgoing conv history (one per state-wave thread
-        // suffices: 3 H D <= 256 H D / 16)
+        // this thread's channel of the outgoing conv history: the grid's H NG workgroups have
+        // 256 state-wave threads each, one per channel of the 3 H D
+        static_assert(256 * NG >= 3 * D, "the state waves must cover the 3 H D conv channels");
         const int NHc = co.K - 1;
         const long chbc = (long)blockIdx.x * 256 + (threadIdx.x - 256);
         const bool chdo = co.cs && NHc > 0 && chbc < 3L * (long)P;

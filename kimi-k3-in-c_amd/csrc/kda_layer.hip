@@ -53,9 +53,16 @@ int zero_fill(float *p, size_t n, hipStream_t st)
     return K3HIP_OK;
 }
 
+// Set while a no-allocation entry point runs on this thread: any stream allocation its
+// call path would make is refused instead (the call then returns an error, allocating nothing).
+static thread_local bool g_no_alloc;
+
 int stream_alloc(StreamBuf &b, size_t bytes, hipStream_t st)
 {
     b.st = st;
+    if (g_no_alloc)
+        K3_FAIL(K3HIP_EINVAL, "no-allocation entry point: a step needs %zu bytes of scratch beyond the fixed "
+                "array", bytes);
     if (bytes == 0) bytes = 256;
     hipError_t e = hipMallocAsync(&b.p, bytes, st);
     if (e != hipSuccess) {
@@ -74,8 +81,12 @@ struct k3hip_kda_weights {
     int hidden, H, D, K, wdt, parts;   // parts: the K3HIP_UPLOAD_* copies that were made
     size_t bytes;                      // device bytes held
     float gate_lb, rms_eps;
-    // q, k, v, f_a, b are row blocks of one allocation xin ([3P + D + H][hidden], in that
-    // order), so a decode step projects into all five with one pass over the weights
+    // The DEV part (every matrix in its own storage and the fp32 vectors) is one device block,
+    // dev_block, freed on release when owned (the drop-in binds a stream-ordered block of its
+    // own). q, k, v, f_a, b are row blocks of xin ([3P + D + H][hidden], in that order) inside
+    // it, so a decode step projects into all five with one pass over the weights.
+    void *dev_block;
+    bool own_dev_block;
     void *xin;
     void *q, *k, *v, *f_a, *f_b, *b, *g, *o;        // matrices, wdt storage
     float *q_conv, *k_conv, *v_conv, *A_log, *dt_bias, *o_norm;
@@ -119,14 +130,64 @@ __global__ void bf16_to_f16_kernel(const uint16_t *__restrict__ w, uint16_t *__r
 static thread_local size_t g_dropin_h2d, g_dropin_d2h;
 static thread_local bool g_in_dropin;   // counting: inside k3_kda_layer
 
-static int upload(void **dst, const void *src, size_t bytes, size_t *held)
+// The DEV part's layout in one block: xin (q, k, v, f_a, b rows), f_b, g, o, then the fp32
+// vectors, each region 256-byte aligned. Row bytes of a matrix with `cols` inputs: int8 rows
+// carry their fp32 scale in front (include/k3/k3.h:266-283), the other tags are per element.
+struct DevPart {
+    size_t rowbytes_E, off[10], total;
+};
+static DevPart dev_part_layout(const K3KdaW *w, const K3Cfg *c)
 {
-    *dst = nullptr;
-    if (!src) K3_FAIL(K3HIP_EINVAL, "k3hip_kda_upload: NULL weight");
-    K3_HIP(hipMalloc(dst, bytes ? bytes : 4));
-    K3_HIP(hipMemcpy(*dst, src, bytes, hipMemcpyHostToDevice));
-    *held += bytes;
-    if (g_in_dropin) g_dropin_h2d += bytes;
+    const size_t E = (size_t)c->hidden, H = (size_t)c->kda_heads, D = (size_t)c->kda_head_dim, K = (size_t)c->conv_k;
+    const size_t P = H * D, es = w->wdt == K3_WBF16 ? 2 : 4;
+    auto rb = [&](size_t cols) { return w->wdt == K3_WI8 ? 4 + cols : cols * es; };
+    const size_t sizes[10] = {(3 * P + D + H) * rb(E), P * rb(D), P * rb(E), E * rb(P), P * K * 4, P * K * 4,
+                              P * K * 4, H * 4, P * 4, D * 4};
+    DevPart L{};
+    L.rowbytes_E = rb(E);
+    for (int i = 0; i < 10; i++) {
+        L.off[i] = L.total;
+        L.total += (sizes[i] + 255) & ~(size_t)255;
+    }
+    return L;
+}
+static size_t dev_part_bytes(const K3KdaW *w, const K3Cfg *c) { return dev_part_layout(w, c).total; }
+
+// Copy the DEV part of w into `base` (dev_part_bytes of device memory) on stream st and point
+// d's fields at it; d's sizes and tag are set by the caller.
+static int bind_dev_part(k3hip_kda_weights *d, const K3KdaW *w, const K3Cfg *c, char *base, hipStream_t st)
+{
+    const size_t E = (size_t)c->hidden, H = (size_t)c->kda_heads, D = (size_t)c->kda_head_dim, K = (size_t)c->conv_k;
+    const size_t P = H * D, es = w->wdt == K3_WBF16 ? 2 : 4;
+    auto rb = [&](size_t cols) { return w->wdt == K3_WI8 ? 4 + cols : cols * es; };
+    const DevPart L = dev_part_layout(w, c);
+    const void *src[14] = {w->q, w->k, w->v, w->f_a, w->b, w->f_b, w->g, w->o,
+                           w->q_conv, w->k_conv, w->v_conv, w->A_log, w->dt_bias, w->o_norm};
+    for (const void *p : src)
+        if (!p) K3_FAIL(K3HIP_EINVAL, "k3hip_kda_upload: NULL weight");
+    void **dst[14] = {&d->q, &d->k, &d->v, &d->f_a, &d->b, &d->f_b, &d->g, &d->o,
+                      (void **)&d->q_conv, (void **)&d->k_conv, (void **)&d->v_conv, (void **)&d->A_log,
+                      (void **)&d->dt_bias, (void **)&d->o_norm};
+    size_t off[14], bytes[14];
+    const size_t xrows[5] = {P, P, P, D, H};
+    size_t at = 0;
+    for (int i = 0; i < 5; i++) {   // q k v f_a b: consecutive row blocks of xin
+        off[i] = L.off[0] + at * L.rowbytes_E;
+        bytes[i] = xrows[i] * L.rowbytes_E;
+        at += xrows[i];
+    }
+    const size_t rest[9] = {P * rb(D), P * rb(E), E * rb(P), P * K * 4, P * K * 4, P * K * 4, H * 4, P * 4, D * 4};
+    for (int i = 5; i < 14; i++) {
+        off[i] = L.off[i - 4];
+        bytes[i] = rest[i - 5];
+    }
+    for (int i = 0; i < 14; i++) {
+        *dst[i] = base + off[i];
+        K3_HIP(hipMemcpyAsync(*dst[i], src[i], bytes[i], hipMemcpyHostToDevice, st));
+        d->bytes += bytes[i];
+        if (g_in_dropin) g_dropin_h2d += bytes[i];
+    }
+    d->xin = d->q;
     return K3HIP_OK;
 }
 
@@ -134,9 +195,8 @@ extern "C" int k3hip_kda_release(k3hip_kda_weights *w)
 {
     clear_error();
     if (!w) return K3HIP_OK;
-    void *ptrs[] = {w->xin, w->f_b, w->g, w->o, w->q_conv, w->k_conv, w->v_conv, w->A_log,
-                    w->dt_bias, w->o_norm, w->f_b2, w->o16, w->xin_f, w->g_f, w->f_b_f,
-                    w->o_f};   // q k v f_a b live inside xin
+    void *ptrs[] = {w->own_dev_block ? w->dev_block : nullptr, w->f_b2, w->o16, w->xin_f, w->g_f, w->f_b_f,
+                    w->o_f};   // the DEV part's matrices and vectors live inside dev_block
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
     free(w);
@@ -161,53 +221,31 @@ extern "C" int k3hip_kda_upload_ex(const K3KdaW *w, const K3Cfg *c, int parts, k
     const int E = c->hidden, H = c->kda_heads, D = c->kda_head_dim, K = c->conv_k;
     if (E <= 0 || H <= 0 || D <= 0 || K <= 0)
         K3_FAIL(K3HIP_EINVAL, "k3hip_kda_upload: hidden=%d H=%d D=%d conv_k=%d", E, H, D, K);
-    if (w->wdt != K3_WF32 && w->wdt != K3_WBF16)
-        K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_upload: weight tag %d (fp32=0, bf16=1 only)", w->wdt);
+    if (w->wdt != K3_WF32 && w->wdt != K3_WBF16 && w->wdt != K3_WI8)
+        K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_kda_upload: weight tag %d (fp32=0, bf16=1, int8 rows=2)", w->wdt);
     k3hip_kda_weights *d = (k3hip_kda_weights *)calloc(1, sizeof *d);
     if (!d) K3_FAIL(K3HIP_ENOMEM, "k3hip_kda_upload: host allocation");
     d->hidden = E; d->H = H; d->D = D; d->K = K; d->wdt = w->wdt; d->parts = parts | K3HIP_UPLOAD_DEV;
     d->gate_lb = c->gate_lb; d->rms_eps = c->rms_eps;
-    const size_t P = (size_t)H * D, es = w->wdt == K3_WBF16 ? 2 : 4;
+    const size_t P = (size_t)H * D;
     int rc = K3HIP_OK;
     {
-        const size_t rowb = (size_t)E * es, nin = 3 * P + D + H;
-        const void *src[5] = {w->q, w->k, w->v, w->f_a, w->b};
-        const size_t rows[5] = {P, P, P, (size_t)D, (size_t)H};
-        void **dst[5] = {&d->q, &d->k, &d->v, &d->f_a, &d->b};
-        for (int i = 0; i < 5 && rc == K3HIP_OK; i++)
-            if (!src[i]) {
-                set_error("k3hip_kda_upload: NULL weight");
-                rc = K3HIP_EINVAL;
-            }
-        if (rc == K3HIP_OK && hipMalloc(&d->xin, nin * rowb) != hipSuccess) {
+        void *blk = nullptr;
+        const size_t need = dev_part_bytes(w, c);
+        if (hipMalloc(&blk, need) != hipSuccess) {
             (void)hipGetLastError();
-            d->xin = nullptr;
-            set_error("k3hip_kda_upload: hipMalloc(%zu bytes)", nin * rowb);
+            set_error("k3hip_kda_upload: hipMalloc(%zu bytes)", need);
             rc = K3HIP_ENOMEM;
-        }
-        size_t at = 0;
-        for (int i = 0; i < 5 && rc == K3HIP_OK; i++) {
-            *dst[i] = (char *)d->xin + at * rowb;
-            if (hipMemcpy(*dst[i], src[i], rows[i] * rowb, hipMemcpyHostToDevice) != hipSuccess) {
+        } else {
+            d->dev_block = blk;
+            d->own_dev_block = true;
+            rc = bind_dev_part(d, w, c, (char *)blk, nullptr);
+            if (rc == K3HIP_OK && hipStreamSynchronize(nullptr) != hipSuccess) {
                 set_error("k3hip_kda_upload: weight copy failed");
                 rc = K3HIP_EHIP;
             }
-            d->bytes += rows[i] * rowb;
-            if (g_in_dropin) g_dropin_h2d += rows[i] * rowb;
-            at += rows[i];
         }
     }
-#define UP(field, src, nbytes) if (rc == K3HIP_OK) rc = upload((void **)&d->field, src, nbytes, &d->bytes)
-    UP(f_b, w->f_b, P * D * es);
-    UP(g, w->g, P * E * es);
-    UP(o, w->o, (size_t)E * P * es);
-    UP(q_conv, w->q_conv, P * K * 4);
-    UP(k_conv, w->k_conv, P * K * 4);
-    UP(v_conv, w->v_conv, P * K * 4);
-    UP(A_log, w->A_log, (size_t)H * 4);
-    UP(dt_bias, w->dt_bias, P * 4);
-    UP(o_norm, w->o_norm, (size_t)D * 4);
-#undef UP
     // [W | W] copies of f_b (P x 2D) and o (E x 2P) for the bf16 prefill path
     auto twice = [&](void **dst, const void *src, size_t rows, size_t cols) -> int {
         const size_t rb = cols * 2;
@@ -308,13 +346,38 @@ extern "C" int k3hip_kda_layer_dev(const k3hip_kda_weights *w, int T, float *out
     }
     float *cs = state ? state + (size_t)H * D * D : nullptr;
 
-    if ((rc = proj(T, E, (int)P, x, w->q, w->wdt, qp, st))) return rc;
-    if ((rc = proj(T, E, (int)P, x, w->k, w->wdt, kp, st))) return rc;
-    if ((rc = proj(T, E, (int)P, x, w->v, w->wdt, vp, st))) return rc;
-    if ((rc = proj(T, E, H, x, w->b, w->wdt, bl, st))) return rc;
-    if ((rc = proj(T, E, D, x, w->f_a, w->wdt, fa, st))) return rc;
-    if ((rc = proj(T, D, (int)P, fa, w->f_b, w->wdt, z, st))) return rc;
-    if ((rc = proj(T, E, (int)P, x, w->g, w->wdt, gl, st))) return rc;
+    // Projections. bf16 weights on a T >= 16 prefill: MFMA GEMMs (kda_mm.hip) of the input
+    // split into bf16 hi + lo rows, the two halves' fp32 products added, so the products keep
+    // fp32 accuracy (x = hi + lo to 2^-17, bf16 x bf16 exact in fp32, fp32 sums over K) and
+    // the layer stays within the reference's 1e-4 bar. Otherwise (fp32 or int8 weights,
+    // short T, widths that are not multiples of 64) the double-accumulating GEMV.
+    const bool mfma = w->wdt == K3_WBF16 && T >= 16 && E % 64 == 0 && D % 64 == 0 && P % 64 == 0 &&
+                      ((uintptr_t)x & 15) == 0;
+    StreamBuf sbuf;
+    uint16_t *xs = nullptr;
+    float *C2 = nullptr;
+    if (mfma) {
+        const size_t maxin = std::max<size_t>(E, P), maxout = std::max<size_t>(E, P);
+        const size_t xsb = ((2 * (size_t)T * maxin * 2) + 255) & ~(size_t)255;
+        if ((rc = stream_alloc(sbuf, xsb + 2 * (size_t)T * maxout * 4, st))) return rc;
+        xs = (uint16_t *)sbuf.p;
+        C2 = (float *)((char *)sbuf.p + xsb);
+    }
+    // y[T][out] = in[T][nin] . W[out][nin]^T, from the split input xs when mfma
+    auto project = [&](int nin, int nout, const float *in, const void *W, float *y) -> int {
+        if (!mfma) return proj(T, nin, nout, in, W, w->wdt, y, st);
+        int r = mm(2 * T, nout, nin, K3HIP_BF16, xs, nin, W, nin, C2, K3HIP_F32, nout, st);
+        return r ? r : pair_add(C2, y, T, nout, st);
+    };
+    if (mfma && (rc = split_rows2(x, xs, T, E, st))) return rc;
+    if ((rc = project(E, (int)P, x, w->q, qp))) return rc;
+    if ((rc = project(E, (int)P, x, w->k, kp))) return rc;
+    if ((rc = project(E, (int)P, x, w->v, vp))) return rc;
+    if ((rc = project(E, H, x, w->b, bl))) return rc;
+    if ((rc = project(E, D, x, w->f_a, fa))) return rc;
+    if ((rc = project(E, (int)P, x, w->g, gl))) return rc;
+    if (mfma && (rc = split_rows2(fa, xs, T, D, st))) return rc;
+    if ((rc = project(D, (int)P, fa, w->f_b, z))) return rc;
 
     if ((rc = k3hip_kda_prep(T, H, D, K, w->gate_lb, K3HIP_F32, qp, kp, vp, z, bl, w->q_conv,
                              w->k_conv, w->v_conv, w->A_log, w->dt_bias, cs, q, k, v, g, al, bt,
@@ -331,7 +394,8 @@ extern "C" int k3hip_kda_layer_dev(const k3hip_kda_weights *w, int T, float *out
     if ((rc = k3hip_kda_epilogue(T, H, D, w->rms_eps, o, gl, K3HIP_F32, w->o_norm, y, K3HIP_F32,
                                  stream)))
         return rc;
-    return proj(T, (int)P, E, y, w->o, w->wdt, out, st);
+    if (mfma && (rc = split_rows2(y, xs, T, (int)P, st))) return rc;
+    return project((int)P, E, y, w->o, out);
 }
 
 // fp32 -> bf16 (round to nearest even), for fp32 layer inputs of the bf16 prefill path.
@@ -468,7 +532,11 @@ extern "C" int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *
     // GEMM (kda_mm.hip, k3hip_proj_gemm) measures 0.90-0.93x of its speed on these shapes.
     // k3hip_set_projection_gemm(K3HIP_GEMM_HANDWRITTEN) selects the hand-written kernels for
     // every projection (`own`).
-    const bool own = g_proj_gemm.load(std::memory_order_relaxed) == K3HIP_GEMM_HANDWRITTEN;
+    // The hand-written kernel needs hidden % 64 == 0 and a 16-byte aligned bf16 x (an fp32 x is
+    // converted into aligned scratch first); other layers take hipBLASLt, which has no such
+    // limits, whatever the setting.
+    const bool own = g_proj_gemm.load(std::memory_order_relaxed) == K3HIP_GEMM_HANDWRITTEN &&
+                     mm_supported(E, E, E) && (x_dtype == K3HIP_F32 || ((uintptr_t)x & 15) == 0);
     int ncu = 256, rc;
     if ((rc = cu_count(ncu))) return rc;
     const int fab_s = own ? mm_splits(T, D + H, E, ncu) : 1;
@@ -633,9 +701,10 @@ static int layer_decode_impl(const k3hip_kda_weights *w, int B, float *out, cons
     //   planes that the step kernel adds
     if ((rc = gemm_rows_with_part(B, E, x, E, NI, Win, Cin, ldi, (int)P, Wg, glp, st, ws, wsf))) return rc;
     // 2-8 the f_b product, K1, K3 and K4 on one token per sequence (kda_step.hip), conv
-    //   history and state in each slot, then 9 o_proj: when it runs as two K-ranges, the
-    //   step kernel zeroes `out` and both ranges add into it (no reduction launch)
-    const bool oz = gemm_rows_splits(E, (int)P) == 2;
+    //   history and state in each slot, then 9 o_proj: when it runs as two K-ranges into
+    //   ordinary device memory, the step kernel zeroes `out` and both ranges add into it by
+    //   float atomics (no reduction launch); other memory takes the ordered reduction
+    const bool oz = gemm_rows_splits(E, (int)P) == 2 && coarse_device_mem(out);
     if ((rc = layer_step(B, H, D, K, w->gate_lb, w->rms_eps, 1.0f / sqrtf((float)D), Cin, ldi,
                          3 * (int)P + D, 3 * (int)P, Wfb, glp, gs, (long)BP, w->q_conv, w->k_conv, w->v_conv,
                          w->A_log, w->dt_bias, w->o_norm, states, state_stride, y, oz ? out : nullptr,
@@ -656,7 +725,7 @@ extern "C" int k3hip_kda_layer_decode(const k3hip_kda_weights *w, int B, float *
 // held until the process ends. Host code never passes `noalloc_scratch` itself (on the host
 // it only names the symbol); it takes the array's device address on each device from
 // hipGetSymbolAddress, once, with that device current, and passes that address on.
-constexpr size_t NOALLOC_SCRATCH_BYTES = 64ull << 20;
+constexpr size_t NOALLOC_SCRATCH_BYTES = 16ull << 20;
 static __device__ __align__(256) char noalloc_scratch[NOALLOC_SCRATCH_BYTES];
 
 static constexpr int NOALLOC_MAX_DEV = 64;
@@ -689,6 +758,10 @@ extern "C" int k3hip_kda_layer_decode_noalloc(const k3hip_kda_weights *w, int B,
     char *scr = nullptr;
     int rc;
     if ((rc = noalloc_scratch_ptr(&scr))) return rc;
+    struct NoAlloc {
+        NoAlloc() { g_no_alloc = true; }
+        ~NoAlloc() { g_no_alloc = false; }
+    } guard;
     return layer_decode_impl(w, B, out, x, states, state_stride, stream, scr, NOALLOC_SCRATCH_BYTES,
                              "k3hip_kda_layer_decode_noalloc");
 }
@@ -714,37 +787,52 @@ extern "C" void k3_kda_layer(float *out, const float *x, const K3KdaW *w, const 
 {
     (void)scratch;
     if (T <= 0) return;
+    if (!w || !c || !out || !x) {
+        set_error("NULL argument");
+        fatal("k3_kda_layer");
+    }
     const int E = c->hidden, H = c->kda_heads, D = c->kda_head_dim, K = c->conv_k;
+    if (E <= 0 || H <= 0 || D <= 0 || K <= 0) {
+        set_error("hidden=%d H=%d D=%d conv_k=%d", E, H, D, K);
+        fatal("k3_kda_layer");
+    }
+    if (w->wdt != K3_WF32 && w->wdt != K3_WBF16 && w->wdt != K3_WI8) {
+        set_error("weight tag %d (fp32=0, bf16=1, int8 rows=2)", w->wdt);
+        fatal("k3_kda_layer");
+    }
     const size_t P = (size_t)H * D;
     const size_t nstate = P * D + 3 * P * (size_t)(K - 1);
     g_dropin_h2d = g_dropin_d2h = 0;
     g_in_dropin = true;
-    // only what k3hip_kda_layer_dev reads: the matrices in their own storage and the vectors
-    k3hip_kda_weights *dw = nullptr;
-    if (k3hip_kda_upload_ex(w, c, K3HIP_UPLOAD_DEV, &dw)) fatal("k3_kda_layer (weight upload)");
-    float *dx = nullptr, *dout = nullptr, *dst = nullptr;
-    const size_t xb = (size_t)T * E * sizeof(float);
-    if (hipMalloc((void **)&dx, xb) != hipSuccess || hipMalloc((void **)&dout, xb) != hipSuccess ||
-        (state && hipMalloc((void **)&dst, nstate * sizeof(float)) != hipSuccess)) {
-        set_error("hipMalloc of %zu activation bytes failed", 2 * xb + nstate * 4);
-        fatal("k3_kda_layer");
-    }
-    if (hipMemcpy(dx, x, xb, hipMemcpyHostToDevice) != hipSuccess ||
-        (state && hipMemcpy(dst, state, nstate * 4, hipMemcpyHostToDevice) != hipSuccess)) {
+    // One stream-ordered block per call for what k3hip_kda_layer_dev reads (the matrices in
+    // their own storage, the vectors) and for x, out and the state: no hipMalloc / hipFree.
+    const hipStream_t st = nullptr;
+    const size_t wbytes = dev_part_bytes(w, c), xb = (size_t)T * E * sizeof(float);
+    const size_t sb = state ? nstate * sizeof(float) : 0;
+    const size_t xoff = (wbytes + 255) & ~(size_t)255, ooff = xoff + ((xb + 255) & ~(size_t)255),
+                 soff = ooff + ((xb + 255) & ~(size_t)255);
+    StreamBuf blk;
+    if (stream_alloc(blk, soff + sb, st)) fatal("k3_kda_layer");
+    char *base = (char *)blk.p;
+    k3hip_kda_weights dw{};
+    dw.hidden = E; dw.H = H; dw.D = D; dw.K = K; dw.wdt = w->wdt; dw.parts = K3HIP_UPLOAD_DEV;
+    dw.gate_lb = c->gate_lb; dw.rms_eps = c->rms_eps;
+    dw.dev_block = base;
+    if (bind_dev_part(&dw, w, c, base, st)) fatal("k3_kda_layer (weight upload)");
+    float *dx = (float *)(base + xoff), *dout = (float *)(base + ooff), *dst = state ? (float *)(base + soff) : nullptr;
+    if (hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, st) != hipSuccess ||
+        (state && hipMemcpyAsync(dst, state, sb, hipMemcpyHostToDevice, st) != hipSuccess)) {
         set_error("host-to-device copy failed");
         fatal("k3_kda_layer");
     }
-    g_dropin_h2d += xb + (state ? nstate * 4 : 0);
-    if (k3hip_kda_layer_dev(dw, T, dout, dx, dst, nullptr)) fatal("k3_kda_layer");
-    if (hipMemcpy(out, dout, xb, hipMemcpyDeviceToHost) != hipSuccess ||
-        (state && hipMemcpy(state, dst, nstate * 4, hipMemcpyDeviceToHost) != hipSuccess)) {
+    g_dropin_h2d += xb + sb;
+    if (k3hip_kda_layer_dev(&dw, T, dout, dx, dst, st)) fatal("k3_kda_layer");
+    if (hipMemcpyAsync(out, dout, xb, hipMemcpyDeviceToHost, st) != hipSuccess ||
+        (state && hipMemcpyAsync(state, dst, sb, hipMemcpyDeviceToHost, st) != hipSuccess) ||
+        hipStreamSynchronize(st) != hipSuccess) {
         set_error("device-to-host copy failed: %s", hipGetErrorString(hipGetLastError()));
         fatal("k3_kda_layer");
     }
-    g_dropin_d2h += xb + (state ? nstate * 4 : 0);
+    g_dropin_d2h += xb + sb;
     g_in_dropin = false;
-    (void)hipFree(dx);
-    (void)hipFree(dout);
-    if (dst) (void)hipFree(dst);
-    k3hip_kda_release(dw);
 }

@@ -392,7 +392,7 @@ extern "C" int k3hip_mla_decode(const k3hip_mla_weights *w, int B, int pos, int 
     gu.sa = KL; gu.sb = (long)(QN + VH) * KL; gu.sc = VH;
     if ((rc = gemm(gu, ch2, kvb + (size_t)QN * KL, O2, st))) return rc;
     // o_proj as two K-ranges adds into `out`, which the gate kernel zeroes (no reduction launch)
-    const bool oz = gemm_rows_splits(E, HV) == 2;
+    const bool oz = gemm_rows_splits(E, HV) == 2 && coarse_device_mem(out);   // atomics: ordinary device memory only
     hipLaunchKernelGGL(mla_gate_kernel, dim3(mla_grid((size_t)B * HV)), dim3(256), 0, st, O2,
                        w->gate ? C1 + QL + CW : nullptr, ld1, B, (size_t)HV, o, oz ? out : nullptr,
                        oz ? (size_t)B * E : (size_t)0);

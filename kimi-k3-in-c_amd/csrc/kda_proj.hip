@@ -9,6 +9,13 @@
 // PROJ_TB tokens and fused into PROJ_TB double accumulators; a wave reduction finishes.
 // This is the parity path of k3_kda_layer (small T, fp32 or bf16 weights), not the
 // throughput GEMM.
+//
+// The int8 draft format (K3_WI8, include/k3/k3.h:266-283; k3_matmul_q8,
+// src/core/k3_ops.c:1228-1301) stores row o as [f32 scale][int8 * in] (4 + in bytes, so rows
+// are byte-aligned only): the int8 weights are dotted with x in double and the row's scale
+// applied once at the end, y = (float)dot * scale. The reference sums in float in its SIMD
+// order and states no exactness contract for the format; the double sum is within float
+// rounding of it.
 #include "k3kda_common.h"
 #include "kda_internal.h"
 
@@ -32,9 +39,11 @@ __global__ __launch_bounds__(64 * PROJ_WAVES) void kda_proj_kernel(int T, int in
 #pragma unroll
     for (int b = 0; b < PROJ_TB; b++) acc[b] = 0.0;
     const size_t wrow = (size_t)row * in;
+    const unsigned char *q8row = reinterpret_cast<const unsigned char *>(W) + (size_t)row * (4 + (size_t)in);
     for (int i = lane; i < in; i += 64) {
         double wv;
         if constexpr (WDT == K3_WBF16) wv = (double)bf2f(reinterpret_cast<const uint16_t *>(W)[wrow + i]);
+        else if constexpr (WDT == K3_WI8) wv = (double)(signed char)q8row[4 + i];
         else wv = (double)reinterpret_cast<const float *>(W)[wrow + i];
 #pragma unroll
         for (int b = 0; b < PROJ_TB; b++)
@@ -45,7 +54,14 @@ __global__ __launch_bounds__(64 * PROJ_WAVES) void kda_proj_kernel(int T, int in
         double s = acc[b];
 #pragma unroll
         for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m, 64);
-        if (lane == 0 && b < nt) y[(size_t)(t0 + b) * out + row] = (float)s;
+        if constexpr (WDT == K3_WI8) {
+            // the row's scale, an unaligned little-endian fp32 at the row's start
+            const uint32_t u = (uint32_t)q8row[0] | ((uint32_t)q8row[1] << 8) | ((uint32_t)q8row[2] << 16) |
+                               ((uint32_t)q8row[3] << 24);
+            if (lane == 0 && b < nt) y[(size_t)(t0 + b) * out + row] = (float)s * __uint_as_float(u);
+        } else if (lane == 0 && b < nt) {
+            y[(size_t)(t0 + b) * out + row] = (float)s;
+        }
     }
 }
 
@@ -59,8 +75,10 @@ int proj(int T, int in, int out, const float *x, const void *W, int wdt, float *
         hipLaunchKernelGGL((kda_proj_kernel<K3_WBF16>), grid, dim3(64 * PROJ_WAVES), 0, st, T, in, out, x, W, y);
     else if (wdt == K3_WF32)
         hipLaunchKernelGGL((kda_proj_kernel<K3_WF32>), grid, dim3(64 * PROJ_WAVES), 0, st, T, in, out, x, W, y);
+    else if (wdt == K3_WI8)
+        hipLaunchKernelGGL((kda_proj_kernel<K3_WI8>), grid, dim3(64 * PROJ_WAVES), 0, st, T, in, out, x, W, y);
     else
-        K3_FAIL(K3HIP_EUNSUPPORTED, "projection: weight tag %d (only fp32=0 and bf16=1)", wdt);
+        K3_FAIL(K3HIP_EUNSUPPORTED, "projection: weight tag %d (fp32=0, bf16=1, int8 rows=2)", wdt);
     K3_LAUNCHED();
     return K3HIP_OK;
 }

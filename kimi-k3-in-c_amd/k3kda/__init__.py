@@ -33,7 +33,7 @@ EXPORTS = (
     "k3hip_mla_upload", "k3hip_mla_release", "k3hip_mla_cache_floats", "k3hip_mla_decode",
     "k3hip_kda_layer_decode", "k3hip_kda_upload_ex", "k3hip_kda_weights_bytes",
     "k3hip_kda_dropin_bytes", "k3hip_proj_gemm", "k3hip_kda_layer_decode_noalloc",
-    "k3hip_set_projection_gemm",
+    "k3hip_set_projection_gemm", "k3hip_kda_decode_step",
 )
 
 
@@ -137,6 +137,8 @@ def lib() -> C.CDLL:
         "k3hip_proj_gemm": (i, [i, i, i, i, _P, C.c_long, _P, C.c_long, _P, i, C.c_long, _P]),
         "k3hip_kda_layer_decode_noalloc": (i, [_P, i, _P, _P, _P, C.c_long, _P]),
         "k3hip_set_projection_gemm": (i, [i]),
+        "k3hip_kda_decode_step": (i, [i, i, i, i, f, f, i, _P, _P, _P, _P, _P, _P, i, _P, _P, _P, _P, _P, _P,
+                                      _P, f, _P, _P, i, _P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -260,6 +262,19 @@ def kda_recurrent(q, k, v, alpha, beta, S, o, H: int, D: int, q_scale: float,
     T = q.shape[0]
     _check(lib().k3hip_kda_recurrent(T, H, D, _ptr(q), _ptr(k), _ptr(v), _ptr(alpha),
                                      _ptr(beta), q_scale, _ptr(S), _ptr(o), _stream(stream)))
+
+
+def kda_decode_step(q_in, k_in, v_in, z, b_logit, gate, q_conv, k_conv, v_conv, A_log, dt_bias, o_norm,
+                    conv_state, S, y, H: int, D: int, K: int, gate_lb: float, rms_eps: float,
+                    q_scale: float, stream=None) -> None:
+    """K1 (T=1) + K3 + K4 in one launch for B = q_in.shape[0] sequences: q_in/k_in/v_in [B,P]
+    (fp32 or bf16), z [B,P], b_logit [B,H], gate [B,P] (fp32 or bf16), conv_state
+    [B,3,P,K-1] and S [B,H,D,D] in/out, y [B,P] (fp32 or bf16)."""
+    B = q_in.shape[0]
+    _check(lib().k3hip_kda_decode_step(B, H, D, K, gate_lb, rms_eps, _dt(q_in), _ptr(q_in), _ptr(k_in),
+                                       _ptr(v_in), _ptr(z), _ptr(b_logit), _ptr(gate), _dt(gate), _ptr(q_conv),
+                                       _ptr(k_conv), _ptr(v_conv), _ptr(A_log), _ptr(dt_bias), _ptr(o_norm),
+                                       _ptr(conv_state), q_scale, _ptr(S), _ptr(y), _dt(y), _stream(stream)))
 
 
 def kda_epilogue(o, gate, o_norm, y, H: int, D: int, rms_eps: float, stream=None) -> None:

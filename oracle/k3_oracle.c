@@ -18,6 +18,8 @@
  *                      beta=0 frozen state; exact-write property)
  *   orc_matmul[_bf16]  bitwise vs the reference C; bf16 path == fp32 path on widened
  *                      weights (the reference's own t_matmul_bf16 property)
+ *   orc_matmul_q8      bitwise vs the reference C (its AVX2 order); within float rounding
+ *                      of the double-precision dot of the dequantised row
  *   orc_l2norm         closed form (unit norm); kda_layer1/8.json
  *   orc_kda_layer      kda_layer1/8.json (out + recurrent state); bitwise vs reference
  *   orc_kda_core       equals orc_kda_layer minus the projections (tested by composing)
@@ -252,11 +254,48 @@ void orc_matmul_bf16(float *y, const float *x, const uint16_t *W, int in, int ou
     for (int o = 0; o < out; o++) y[o] = (float)orc_dot16(x, W + (size_t)o * in, in, 1);
 }
 
-/* include/k3/k3.h:290-296 dispatch; the int8 draft format carries no exactness
- * contract in the reference and is not part of this path. */
+/* src/core/k3_ops.c:1228-1301, the per-row int8 draft format (include/k3/k3.h:266-283): row
+ * o is [f32 scale][int8 * in], 4 + in bytes. The reference carries no exactness contract for
+ * it and sums in float in the order of its AVX2 branch, which is the build here (-mavx2
+ * -mfma); that order is restated so the two agree bit for bit on x86: two 8-lane float
+ * accumulators over 16-element blocks (elements i..i+7 into the first, i+8..i+15 into the
+ * second, each a fused multiply-add), their lane sum, the 8 lanes folded as
+ * (l + l4) for l = 0..3, then (m0 + m2, m1 + m3), then their sum; the in%16 tail added
+ * sequentially (product then add); the scale applied once at the end. */
+void orc_matmul_q8(float *y, const float *x, const void *W, int in, int out)
+{
+    const unsigned char *base = (const unsigned char *)W;
+    const size_t rowb = (size_t)4 + (size_t)in;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) if (out > 64)
+#endif
+    for (int o = 0; o < out; o++) {
+        const unsigned char *row = base + (size_t)o * rowb;
+        float scale;
+        memcpy(&scale, row, 4);
+        const signed char *w = (const signed char *)(row + 4);
+        float v0[8] = {0}, v1[8] = {0};
+        int i = 0;
+        for (; i + 15 < in; i += 16)
+            for (int l = 0; l < 8; l++) {
+                v0[l] = fmaf((float)w[i + l], x[i + l], v0[l]);
+                v1[l] = fmaf((float)w[i + 8 + l], x[i + 8 + l], v1[l]);
+            }
+        float vs[8], lo[4];
+        for (int l = 0; l < 8; l++) vs[l] = v0[l] + v1[l];
+        for (int l = 0; l < 4; l++) lo[l] = vs[l] + vs[l + 4];
+        const float m0 = lo[0] + lo[2], m1 = lo[1] + lo[3];
+        float acc = m0 + m1;
+        for (; i < in; i++) acc += (float)w[i] * x[i];
+        y[o] = acc * scale;
+    }
+}
+
+/* include/k3/k3.h:290-296 dispatch */
 void orc_mmw(float *y, const float *x, const void *W, int wdt, int in, int out)
 {
     if (wdt == K3_WBF16) orc_matmul_bf16(y, x, (const uint16_t *)W, in, out);
+    else if (wdt == K3_WI8) orc_matmul_q8(y, x, W, in, out);
     else if (wdt == K3_WF32) orc_matmul(y, x, (const float *)W, in, out);
     else { fprintf(stderr, "k3_oracle: weight tag %d not supported\n", wdt); abort(); }
 }

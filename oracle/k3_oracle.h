@@ -35,6 +35,7 @@ void   orc_kda_step(float *S, float *o, const float *q, const float *k, const fl
                     const float *alpha, float beta, int dk, int dv);
 void   orc_matmul(float *y, const float *x, const float *W, int in, int out);
 void   orc_matmul_bf16(float *y, const float *x, const uint16_t *W, int in, int out);
+void   orc_matmul_q8(float *y, const float *x, const void *W, int in, int out);
 void   orc_mmw(float *y, const float *x, const void *W, int wdt, int in, int out);
 size_t orc_kda_scratch(const K3Cfg *c, int T);
 void   orc_kda_layer(float *out, const float *x, const K3KdaW *w, const K3Cfg *c,

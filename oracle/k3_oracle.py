@@ -43,6 +43,7 @@ def _bind(L: C.CDLL, prefix: str) -> C.CDLL:
         "kda_step": (None, [_P, _P, _P, _P, _P, _P, f, i, i]),
         "matmul": (None, [_P, _P, _P, i, i]),
         "matmul_bf16": (None, [_P, _P, _P, i, i]),
+        "matmul_q8": (None, [_P, _P, _P, i, i]),
         "kda_scratch": (C.c_size_t, [C.POINTER(K3Cfg), i]),
         "kda_layer": (None, [_P, _P, C.POINTER(K3KdaW), C.POINTER(K3Cfg), i, _P, _P]),
     }
@@ -122,7 +123,7 @@ class Weights:
         self.arrays = {}
         for n in self.NAMES:
             a = arrays[n]
-            if a.dtype == np.uint16:
+            if a.dtype in (np.uint16, np.uint8):   # bf16 bit patterns / int8 rows (q8_rows)
                 self.arrays[n] = np.ascontiguousarray(a)
             else:
                 self.arrays[n] = f32(a)
@@ -132,6 +133,27 @@ class Weights:
             setattr(self.w, n, self.arrays[n].ctypes.data)
         self.w.wdt = wdt
         self.w._arrays = self.arrays   # the struct holds raw addresses: keep their owners alive
+
+
+def q8_rows(W) -> np.ndarray:
+    """A float matrix [out][in] in the reference's per-row int8 draft format (K3_WI8,
+    include/k3/k3.h:266-283): each row [f32 scale][int8 * in] with scale = max|row| / 127 and
+    the weights rounded to nearest; returned as raw bytes [out][4 + in]."""
+    W = np.asarray(W, np.float32)
+    out, n = W.shape
+    amax = np.abs(W).max(axis=1)
+    scale = np.where(amax > 0, amax / np.float32(127), np.float32(1)).astype(np.float32)
+    q = np.clip(np.rint(W / scale[:, None]), -127, 127).astype(np.int8)
+    rows = np.empty((out, 4 + n), np.uint8)
+    rows[:, :4] = scale.view(np.uint8).reshape(out, 4)
+    rows[:, 4:] = q.view(np.uint8)
+    return rows
+
+
+def q8_dequant(rows: np.ndarray, n: int) -> np.ndarray:
+    """The float matrix a K3_WI8 row block stands for: scale * int8, exact in fp32."""
+    scale = np.ascontiguousarray(rows[:, :4]).view(np.float32)[:, 0]
+    return rows[:, 4:4 + n].view(np.int8).astype(np.float32) * scale[:, None]
 
 
 def kda_layer(L, x: np.ndarray, W: Weights, cfg: K3Cfg, T: int, state: np.ndarray | None):

@@ -132,29 +132,38 @@ def test_long_context_drift(gpu):
 
 
 def test_long_context_drift_full_heads(gpu):
-    """The long-context drift at the benchmark's full width: one prefill of T = 65,536 tokens at H = 32, D = 128
-    (1,024 chunks, the state carried through all of them) on fp32 conv inputs, against the
-    oracle's orc_kda_core (conv, L2, decay, sequential recurrence) on the same inputs. The
-    worst error of every 4,096-position window is the drift curve; with K3KDA_RECORD_DIR set
-    it is also written there as long_context_drift_h32.json. The same prefill in a 512 MiB
-    workspace (passes of whole chunks) must give the same bits."""
+    """The long-context configuration at the benchmark's full width: one prefill of T = 65,536
+    tokens at H = 32, D = 128 (1,024 chunks, the state carried through all of them) on fp32
+    conv inputs, then 256 decode steps at batch 1 through k3hip_kda_decode_step (one launch
+    per token: K1 + K3 + K4), against the oracle's orc_kda_core (conv, L2, decay, sequential
+    recurrence, RMSNorm and gate) over the same 65,792 tokens. The worst error of every
+    4,096-position window of the prefill is the drift curve; with K3KDA_RECORD_DIR set it is
+    also written there as long_context_drift_h32.json. The same prefill in a 512 MiB workspace
+    (passes of whole chunks) must give the same bits. The first decode token is also held
+    to the decode bar (1e-4) against the oracle continuing from the GPU's own state."""
     import json
     import os
     import torch
-    H, D, K, T, LB = 32, 128, 4, 65536, -5.0
+    H, D, K, T, NDEC, LB, EPS = 32, 128, 4, 65536, 256, -5.0, 1e-5
+    Tall = T + NDEC
     P = H * D
     g = torch.Generator(device="cuda").manual_seed(0x4B334441 + 3)
-    q_in, k_in, v_in = (torch.randn((T, P), device="cuda", generator=g) for _ in range(3))
-    z = torch.randn((T, P), device="cuda", generator=g) * 0.5
-    bl = torch.randn((T, H), device="cuda", generator=g)
+    q_in, k_in, v_in = (torch.randn((Tall, P), device="cuda", generator=g) for _ in range(3))
+    z = torch.randn((Tall, P), device="cuda", generator=g) * 0.5
+    bl = torch.randn((Tall, H), device="cuda", generator=g)
+    gate = torch.randn((Tall, P), device="cuda", generator=g)
     conv = [torch.randn((P, K), device="cuda", generator=g) * 0.5 for _ in range(3)]
     A_log = torch.rand((H,), device="cuda", generator=g) * 1.5
     dt_bias = torch.randn((P,), device="cuda", generator=g)
+    o_norm = 1 + 0.1 * torch.randn((D,), device="cuda", generator=g)
     S = torch.zeros((H, D, D), device="cuda")
+    cs = torch.zeros(3 * P * (K - 1), device="cuda")
     o = torch.full((T, P), float("nan"), device="cuda")
     ws = torch.empty(gpu.kda_chunk_workspace(T, H, D), dtype=torch.uint8, device="cuda")
     qs = float(np.float32(1) / np.sqrt(np.float32(D)))
-    gpu.kda_prefill(q_in, k_in, v_in, z, bl, *conv, A_log, dt_bias, None, S, o, H, D, K, LB, qs, ws)
+    pre = lambda t: t[:T]
+    gpu.kda_prefill(pre(q_in), pre(k_in), pre(v_in), pre(z), pre(bl), *conv, A_log, dt_bias, cs, S, o, H, D, K, LB,
+                    qs, ws)
     torch.cuda.synchronize()
     del ws
     # the same prefill in a 512 MiB workspace: passes of whole chunks (the conv history
@@ -162,35 +171,57 @@ def test_long_context_drift_full_heads(gpu):
     ws = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
     S2 = torch.zeros((H, D, D), device="cuda")
     o2 = torch.full((T, P), float("nan"), device="cuda")
-    gpu.kda_prefill(q_in, k_in, v_in, z, bl, *conv, A_log, dt_bias, None, S2, o2, H, D, K, LB, qs, ws)
+    gpu.kda_prefill(pre(q_in), pre(k_in), pre(v_in), pre(z), pre(bl), *conv, A_log, dt_bias, None, S2, o2, H, D, K,
+                    LB, qs, ws)
     torch.cuda.synchronize()
     assert torch.equal(o, o2) and torch.equal(S, S2), "prefill in passes differs from one pass"
     del ws, S2, o2
     h = lambda t: t.cpu().numpy()
+    S_pre, cs_pre = h(S), h(cs)
+    # decode tail: one launch per token, batch 1, from the prefill's state and conv history
+    S1, cs1 = S.view(1, H, D, D), cs.view(1, -1)
+    y_dec = torch.full((NDEC, P), float("nan"), device="cuda")
+    for i in range(NDEC):
+        t = T + i
+        r = lambda a: a[t:t + 1]
+        gpu.kda_decode_step(r(q_in), r(k_in), r(v_in), r(z), r(bl), r(gate), *conv, A_log, dt_bias, o_norm, cs1, S1,
+                            y_dec[i:i + 1], H, D, K, LB, EPS, qs)
+    torch.cuda.synchronize()
     arrays = {"q_conv": h(conv[0]), "k_conv": h(conv[1]), "v_conv": h(conv[2]), "A_log": h(A_log),
-              "dt_bias": h(dt_bias), "o_norm": np.ones(D, np.float32)}
+              "dt_bias": h(dt_bias), "o_norm": h(o_norm)}
     for n in ("q", "k", "v", "g", "f_a", "f_b", "b", "o"):
         arrays[n] = np.zeros((1, 1), np.float32)
     W = ko.Weights(arrays, 0)
-    cfg = ko.make_cfg(8, H, D, K, LB, 1e-5)
+    cfg = ko.make_cfg(8, H, D, K, LB, EPS)
+    # the first decode token at the decode bar, from the GPU's own state after the prefill
+    st_gpu = np.concatenate([S_pre.ravel(), cs_pre])
+    y1 = ko.core(h(q_in[T:T + 1]), h(k_in[T:T + 1]), h(v_in[T:T + 1]), h(z[T:T + 1]), h(bl[T:T + 1]),
+                 h(gate[T:T + 1]), W, cfg, 1, st_gpu)
+    got_dec = h(y_dec)
+    assert_close(got_dec[:1], y1, 1e-4 * rms(y1), 1e-4, "first decode token after the H=32 prefill, same state")
     st = np.zeros(P * D + 3 * P * (K - 1), np.float32)
-    _, o_ref = ko.core(h(q_in), h(k_in), h(v_in), h(z), h(bl), np.zeros((T, P), np.float32), W, cfg, T, st,
-                       nthreads=16, want_rec=True)
+    y_ref, o_ref = ko.core(h(q_in), h(k_in), h(v_in), h(z), h(bl), h(gate), W, cfg, Tall, st, nthreads=16,
+                           want_rec=True)
     got = h(o)
     curve = []
     for t in range(4095, T, 4096):
         seg = slice(t - 4095, t + 1)
         curve.append((t + 1, worst_ratio(got[seg], o_ref[seg], 2e-3 * rms(o_ref[seg]), 2e-3),
                       worst_ratio(got[seg], o_ref[seg], 1e-4 * rms(o_ref[seg]), 1e-4)))
+    r_dec = worst_ratio(got_dec, y_ref[T:], 2e-3 * rms(y_ref[T:]), 2e-3)
     r_state = worst_ratio(h(S).ravel(), st[:P * D], 2e-3 * rms(st[:P * D]), 2e-3)
+    conv_same = np.array_equal(h(cs), st[P * D:])   # the history holds the inputs themselves: bitwise
     print("long-context H=32 drift (position, worst fraction of the 2e-3 bar):",
-          " ".join(f"{p}:{r:.4f}" for p, r, _ in curve), f"; final state {r_state:.4f}x")
+          " ".join(f"{p}:{r:.4f}" for p, r, _ in curve),
+          f"; decode tail (256 tokens) {r_dec:.4f}x; final state {r_state:.4f}x", flush=True)
     rec = os.environ.get("K3KDA_RECORD_DIR")
     if rec:
         os.makedirs(rec, exist_ok=True)
         with open(os.path.join(rec, "long_context_drift_h32.json"), "w") as f:
-            json.dump({"T": T, "H": H, "D": D, "chunk": 64, "inputs": "fp32 conv inputs N(0,1), z N(0,0.25), "
-                       "b logits N(0,1), gate_lb -5, zero state", "window": 4096,
+            json.dump({"T": T, "H": H, "D": D, "chunk": 64, "decode_steps": NDEC,
+                       "inputs": "fp32 conv inputs N(0,1), z N(0,0.25), b logits N(0,1), gate logits N(0,1), "
+                       "gate_lb -5, zero state", "window": 4096,
                        "worst_2e-3_bar": [[p, r] for p, r, _ in curve],
-                       "worst_1e-4_bar": [[p, r4] for p, _, r4 in curve], "final_state_2e-3_bar": r_state}, f, indent=1)
-    assert max(r for _, r, _ in curve) <= 1.0 and r_state <= 1.0
+                       "worst_1e-4_bar": [[p, r4] for p, _, r4 in curve],
+                       "decode_tail_2e-3_bar": r_dec, "final_state_2e-3_bar": r_state}, f, indent=1)
+    assert max(r for _, r, _ in curve) <= 1.0 and r_dec <= 1.0 and r_state <= 1.0 and conv_same

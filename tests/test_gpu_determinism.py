@@ -1,8 +1,11 @@
 # SPDX-License-Identifier: Apache-2.0
 """Bit identity as the race detector (the reference's own gate, tests/unit/test_ops.c:457-472):
-the bf16 layer prefill (hand-written GEMMs, split-K f_a / b with an ordered reduction, the
-fused core, epilogue, o_proj) and the batched decode layer give the same bits twice in one
-process and in two fresh processes (no algorithm choice by timing, no atomics in any sum)."""
+the work of tests/layer_bits.py gives the same bits twice in one process and in two fresh
+processes. It covers the bf16 layer prefill on both projection GEMMs (hipBLASLt's heuristic
+first choice, never a timing; the hand-written GEMM with split-K f_a / b planes summed in
+order), the batched decode layer with its decode GEMVs in one K-range, in 16 K-ranges (an
+ordered reduction) and in two K-ranges added into the output by float atomics (a two-term
+sum, the same in either order), and the gated MLA decode at the hybrid width."""
 from __future__ import annotations
 
 import subprocess

@@ -12,6 +12,8 @@ grid-size, indexing and overflow mistakes.
    prefills with the state carried, against the oracle's k3_kda_layer on the same bf16
    weights, at the chunked bar (the hand-written run's first prefill, 288 tokens, has a
    partial last row tile).
+   And the same layer at exactly the timed shape, T=8192 from a zero state, on both GEMM
+   paths against one oracle run.
 3. The batched decode layer (k3hip_kda_layer_decode) at hidden 7168, H=32, D=128 for B=16
    sequences (the hybrid slice's KDA layer), against the oracle's k3_kda_layer per
    sequence, at the decode bar 1e-4, two steps.
@@ -105,6 +107,82 @@ def _layer_prefill_at_benchmark_width(gpu, Ts):
         assert_close(gst[P * D:], st_ref[P * D:], 1e-5 * rms(st_ref[P * D:]), 1e-5, f"layer T={T} conv history")
         print(f"hidden={hidden} H={H} D={D} call {i} T={T}: worst {ro:.3f}x (out) / {rs:.3f}x (S) of the 2e-3 bar")
     dw.close()
+
+
+_FULL_LAYER = {}
+
+
+def _full_layer_case():
+    """The bench's layer workload (hidden 4096, H=32, D=128, T=8192, bf16 weights, bf16 x,
+    zero state) and the oracle's k3_kda_layer on it, computed once for both GEMM paths."""
+    if not _FULL_LAYER:
+        hidden, H, D, K, T = 4096, 32, 128, 4, 8192
+        rng = np.random.default_rng(0x4B334441 + 2)
+        W = layer_weights(rng, hidden, H, D, K)
+        cfg = ko.make_cfg(hidden, H, D, K, -5.0, 1e-5)
+        x = bf16_to_f32(bf16(rng.standard_normal((T, hidden))))
+        st = np.zeros(H * D * D + 3 * H * D * (K - 1), np.float32)
+        want = ko.kda_layer(ko.orc(), x, W, cfg, T, st)
+        _FULL_LAYER.update(W=W, cfg=cfg, x=x, want=want, st=st, T=T)
+    return _FULL_LAYER
+
+
+def test_dropin_at_benchmark_shape(gpu):
+    """The drop-in k3_kda_layer (host pointers) on the same workload: its projections are the
+    split-x MFMA GEMMs (fp32 accuracy), the core the chunked prefill, so it holds the chunked
+    bar against the oracle; its 1e-4 ratio is reported."""
+    c = _full_layer_case()
+    W, cfg, T = c["W"], c["cfg"], c["T"]
+    P = cfg.kda_heads * cfg.kda_head_dim
+    st = np.zeros(P * cfg.kda_head_dim + 3 * P * (cfg.conv_k - 1), np.float32)
+    out = np.zeros((T, cfg.hidden), np.float32)
+    gpu.kda_layer_host(out, c["x"], W.w, cfg, T, st)
+    want = c["want"]
+    r = assert_close(out, want, 2e-3 * rms(want), 2e-3, "drop-in k3_kda_layer at T=8192")
+    rs = assert_close(st, c["st"], 2e-3 * rms(c["st"]), 2e-3, "drop-in state at T=8192")
+    r4 = worst_ratio(out, want, 1e-4 * rms(want), 1e-4)
+    print(f"drop-in hidden=4096 T={T}: worst {r:.4f}x (out) / {rs:.4f}x (state) of the 2e-3 bar; "
+          f"{r4:.3f}x of 1e-4", flush=True)
+
+
+@pytest.mark.parametrize("gemm", ["hipblaslt", "hand_written"])
+def test_layer_prefill_at_benchmark_shape(gpu, gemm):
+    """The bf16 layer prefill at exactly the shape bench.py times (hidden 4096, H=32, D=128,
+    T=8192 from a zero state) on both projection GEMMs, against the oracle's k3_kda_layer on
+    the same bf16 weights and bf16-rounded x, at the chunked bar (rtol 2e-3, atol 2e-3 * rms).
+    The o_proj input y enters in fp16; the worst output element is reported as a fraction of
+    the bar (with K3KDA_RECORD_DIR set, also written to layer_prefill_t8192_<gemm>.json)."""
+    import json
+    import os
+    import torch
+    c = _full_layer_case()
+    W, cfg, T = c["W"], c["cfg"], c["T"]
+    H, D = cfg.kda_heads, cfg.kda_head_dim
+    P = H * D
+    gpu.set_projection_gemm(gpu.GEMM_HANDWRITTEN if gemm == "hand_written" else gpu.GEMM_HIPBLASLT)
+    try:
+        dw = gpu.DeviceWeights(W.w, cfg, gpu.UPLOAD_DEV | gpu.UPLOAD_PREFILL)
+        dst = torch.zeros(P * D + 3 * P * (cfg.conv_k - 1), device="cuda")
+        out = torch.full((T, cfg.hidden), float("nan"), device="cuda")
+        dw.layer_prefill(out, torch.from_numpy(c["x"]).cuda().to(torch.bfloat16), dst, T)
+        torch.cuda.synchronize()
+    finally:
+        gpu.set_projection_gemm(gpu.GEMM_HIPBLASLT)
+    got, gst = out.cpu().numpy(), dst.cpu().numpy()
+    dw.close()
+    want, st = c["want"], c["st"]
+    ro = assert_close(got, want, 2e-3 * rms(want), 2e-3, f"layer T={T} out ({gemm})")
+    rs = assert_close(gst[:P * D], st[:P * D], 2e-3 * rms(st[:P * D]), 2e-3, f"layer T={T} S ({gemm})")
+    assert_close(gst[P * D:], st[P * D:], 1e-5 * rms(st[P * D:]), 1e-5, f"layer T={T} conv history ({gemm})")
+    r4 = worst_ratio(got, want, 1e-4 * rms(want), 1e-4)
+    print(f"layer prefill hidden=4096 H=32 D=128 T={T} ({gemm}): worst {ro:.3f}x (out) / {rs:.4f}x (S) of the "
+          f"2e-3 bar; {r4:.1f}x of 1e-4", flush=True)
+    rec = os.environ.get("K3KDA_RECORD_DIR")
+    if rec:
+        os.makedirs(rec, exist_ok=True)
+        with open(os.path.join(rec, f"layer_prefill_t8192_{gemm}.json"), "w") as f:
+            json.dump({"gemm": gemm, "T": T, "hidden": 4096, "H": H, "D": D, "worst_out_2e-3_bar": ro,
+                       "worst_state_2e-3_bar": rs, "worst_out_1e-4_bar": r4}, f, indent=1)
 
 
 def test_layer_decode_at_hybrid_width(gpu):

@@ -168,3 +168,19 @@ def test_mla_at_hybrid_width(gpu):
     gcache, kvcs, ropecs = seeded_caches(rng, W, H, kvl, qn, qr, vh, B, 597, cap)
     w = run_steps(gpu, rng, W, cfg, hidden, B, gcache, kvcs, ropecs, (597, 598), cap)
     print(f"hybrid-width MLA B={B}: worst {w:.3f}x of the 1e-4 bar")
+
+
+def test_mla_at_hybrid_width_timed_context(gpu):
+    """The hybrid slice's MLA layer at the context the benchmark times: hidden 7168, 64 heads,
+    q_lora 1536, kv_lora 512, rope 64, B = 16 sequences attending over 8,192 then 8,193 cached
+    positions (the fused attention's position ranges at their timed lengths). The nope and v
+    heads are 16 wide so that the oracle's expanded per-head cache stays small (two seeded
+    caches shared by the 16 sequences); the attention kernel reads only the latent rows,
+    whose width does not depend on them."""
+    rng = np.random.default_rng(0x4B334441 + 78)
+    hidden, H, ql, kvl, qn, qr, vh, B = 7168, 64, 1536, 512, 16, 64, 16, 16
+    cfg, W = mla_case(rng, hidden, H, ql, kvl, qn, qr, vh, 1)
+    cap = 8200
+    gcache, kvcs, ropecs = seeded_caches(rng, W, H, kvl, qn, qr, vh, B, 8192, cap, ncache=2)
+    w = run_steps(gpu, rng, W, cfg, hidden, B, gcache, kvcs, ropecs, (8192, 8193), cap)
+    print(f"hybrid-width MLA B={B} over 8,192 positions: worst {w:.3f}x of the 1e-4 bar")

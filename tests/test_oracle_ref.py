@@ -27,7 +27,7 @@ def rand_layer(rng, hidden, H, D, K, wdt):
 
     def mat(o, i, s=0.02):
         m = (rng.standard_normal((o, i)) * s).astype(np.float32)
-        return bf16(m) if wdt == 1 else m
+        return bf16(m) if wdt == 1 else (ko.q8_rows(m) if wdt == 2 else m)
 
     arrays = {
         "q": mat(P, hidden), "k": mat(P, hidden), "v": mat(P, hidden), "g": mat(P, hidden),
@@ -53,6 +53,8 @@ def bf16(m: np.ndarray) -> np.ndarray:
     (256, 2, 128, 4, 17, 1),
     (96, 3, 32, 1, 5, 0),      # conv_k = 1: no history at all
     (64, 2, 16, 2, 3, 1),
+    (256, 4, 64, 4, 9, 2),     # the int8 draft format (K3_WI8), hidden a multiple of 16
+    (200, 3, 32, 3, 5, 2),     # and with ragged int8 row tails
 ])
 def test_layer_bitwise_vs_reference(hidden, H, D, K, T, wdt):
     rng = np.random.default_rng(1000 + hidden + D + T)
@@ -111,6 +113,25 @@ def test_matmul_bitwise(i_n, o_n):
     ko.orc().orc_matmul_bf16(ptr(y1), ptr(x), ptr(Wb), i_n, o_n)
     R.k3_matmul_bf16(ptr(y2), ptr(x), ptr(Wb), i_n, o_n)
     assert bits_equal(y1, y2)
+
+
+@pytest.mark.parametrize("i_n,o_n", [(257, 129), (16, 3), (15, 5), (7168 // 8, 40)])
+def test_matmul_q8_bitwise(i_n, o_n):
+    """The per-row int8 draft matmul (K3_WI8, src/core/k3_ops.c:1228-1301): the oracle's
+    restatement of the reference's AVX2 summation order equals the reference bit for bit,
+    and both lie within float rounding of the double-precision dot of the dequantised row."""
+    rng = np.random.default_rng(5000 + i_n)
+    Wf = f32(rng.standard_normal((o_n, i_n)))
+    Wq = ko.q8_rows(Wf)
+    x = f32(rng.standard_normal(i_n))
+    y1, y2 = np.zeros(o_n, np.float32), np.zeros(o_n, np.float32)
+    ko.orc().orc_matmul_q8(ptr(y1), ptr(x), ptr(Wq), i_n, o_n)
+    R.k3_matmul_q8(ptr(y2), ptr(x), ptr(Wq), i_n, o_n)
+    assert bits_equal(y1, y2)
+    deq = ko.q8_dequant(Wq, i_n).astype(np.float64)
+    exact = deq @ x.astype(np.float64)
+    mag = np.abs(deq) @ np.abs(x.astype(np.float64))
+    assert np.all(np.abs(y1 - exact) <= 2.0 ** -20 * mag + 1e-30)
 
 
 def test_shortconv_short_sequence_carries_history():
