@@ -86,6 +86,8 @@ __global__ __launch_bounds__(4 * D) void kda_layer_step_kernel(const StepArgs a)
     static_assert(CPR * RPP == NT && NPASS * RPP == D, "tile shape");
     constexpr int CPL = D >= 32 ? D / 32 : 1;   // K1 channels per lane of a half-wave
     constexpr int NH = K - 1;
+    constexpr int HWS = NT / 32;                // half-waves
+    constexpr int TPT = (4 + HWS - 1) / HWS;    // K1 tasks per half-wave
 
     __shared__ float s_q[D], s_k[D], s_v[D], s_a[D], s_z[D];
     __shared__ f4 s_red[RPP][CPR];
@@ -97,18 +99,68 @@ __global__ __launch_bounds__(4 * D) void kda_layer_step_kernel(const StepArgs a)
     const int cg = tid % CPR, rs = tid / CPR;
     const size_t P = (size_t)H * D;
 
+    // Every global operand is requested up front, so the step waits for memory once: this
+    // thread's K1 inputs (task hw + i HWS: 0..2 = q, k, v conv, 3 = the decay gate), the
+    // state, the beta logit and, for the K4 lanes, the gate logits and o_norm.
+    const int hw = tid >> 5, l32 = tid & 31;
+    const bool active = l32 * CPL < D;
+    const int cl = active ? l32 * CPL : 0;   // channel within the head
+    const size_t c0 = (size_t)h * D + cl;
+    float *hist = a.hist + (size_t)b * a.h_stride;   // [3][P][K-1]
+    float pcur[TPT][CPL], pw[TPT][CPL][K], ph[TPT][CPL][NH > 0 ? NH : 1], pz[CPL], pdt[CPL];
+    float pA = 0.0f;
+#pragma unroll
+    for (int i = 0; i < TPT; i++) {
+        const int task = hw + i * HWS;
+        if (task < 3) {
+            const float *cw = task == 0 ? a.q_conv : (task == 1 ? a.k_conv : a.v_conv);
+            const void *src = task == 0 ? a.qi : (task == 1 ? a.ki : a.vi);
+#pragma unroll
+            for (int e = 0; e < CPL; e++) {
+                const size_t ch = c0 + e;
+                const size_t at = (size_t)b * a.ldi + ch;
+                pcur[i][e] = a.in_dt == K3HIP_BF16 ? load_act<K3HIP_BF16>(src, at) : load_act<K3HIP_F32>(src, at);
+#pragma unroll
+                for (int j = 0; j < K; j++) pw[i][e][j] = cw[ch * K + j];
+                const float *hs = hist + ((size_t)task * P + ch) * NH;
+#pragma unroll
+                for (int j = 0; j < NH; j++) ph[i][e][j] = hs[j];
+            }
+        } else if (task == 3) {
+            pA = a.A_log[h];
+#pragma unroll
+            for (int e = 0; e < CPL; e++) {
+                pdt[e] = a.dt_bias[c0 + e];
+                if constexpr (ZIN) pz[e] = a.z[(size_t)b * a.ldz + c0 + e];
+            }
+        }
+    }
+    float pbl = 0.0f;
+    if (tid == 0) pbl = a.bl[(size_t)b * a.ldb + h];
+    const size_t at4 = (size_t)b * P + (size_t)h * D + 4 * (tid % CPR);
+    f4 gt = 0.0f, wn = 0.0f;
+    if (tid < CPR) {
+        if (a.g_dt == K3HIP_BF16) {
+            const uint2 v = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(a.gl) + at4);
+            gt = f4{__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u), __uint_as_float(v.y << 16),
+                    __uint_as_float(v.y & 0xffff0000u)};
+        } else {
+            const float *g32 = reinterpret_cast<const float *>(a.gl);
+            gt = *reinterpret_cast<const f4 *>(g32 + at4);
+            for (int sp = 1; sp < a.gsplit; sp++)
+                gt = gt + *reinterpret_cast<const f4 *>(g32 + (size_t)sp * a.gplane + at4);
+        }
+        wn = reinterpret_cast<const f4 *>(a.o_norm)[tid];
+    }
+
     // layer form, z: wave wv takes the head's 16-channel group wv of W_fb (D / 16 groups =
-    // NT / 64 waves); A-operand row 0 is this sequence's f_a, rows 1..15 zero. The weight and
-    // f_a loads go out before the state's, so the MFMAs below wait for them only.
+    // NT / 64 waves); A-operand row 0 is this sequence's f_a, rows 1..15 zero.
     typedef float f32x4 __attribute__((ext_vector_type(4)));
     constexpr int KT = (D + 31) / 32;   // K-steps over the D-wide f_a
     const int ln = tid & 63, r16 = ln & 15, kq = ln >> 4, wv = tid >> 6;
     bsplit::bf16x8 wfr[KT];
     f4 fxa[KT], fxb[KT];
-    float zin = 0.0f;
-    if constexpr (ZIN) {
-        if (tid < D) zin = a.z[(size_t)b * a.ldz + (size_t)h * D + tid];
-    } else {
+    if constexpr (!ZIN) {
         const bsplit::bf16x8 *wf = reinterpret_cast<const bsplit::bf16x8 *>(a.Wfb) +
                                    ((size_t)h * (D / 16) + wv) * KT * 64 + ln;
         const float *fa = a.fa + (size_t)b * a.ldfa;
@@ -124,6 +176,13 @@ __global__ __launch_bounds__(4 * D) void kda_layer_step_kernel(const StepArgs a)
         }
     }
 
+    // the state
+    f4 *Sp = reinterpret_cast<f4 *>(a.S + (size_t)b * a.s_stride + (size_t)h * D * D);
+    f4 s[NPASS];
+#pragma unroll
+    for (int m = 0; m < NPASS; m++)
+        s[m] = a.stream_state ? __builtin_nontemporal_load(&Sp[(rs + m * RPP) * CPR + cg]) : Sp[(rs + m * RPP) * CPR + cg];
+
     // zout[0 .. zn) = 0 for the o_proj product that adds its two K-range partials there
     // (stream-ordered after every reader of the layer input), spread over the grid
     if (a.zout) {
@@ -132,16 +191,7 @@ __global__ __launch_bounds__(4 * D) void kda_layer_step_kernel(const StepArgs a)
         for (long i = z0 + tid; i < z1; i += NT) a.zout[i] = 0.0f;
     }
 
-    // then the state: its latency overlaps the z product and the K1 arithmetic below
-    f4 *Sp = reinterpret_cast<f4 *>(a.S + (size_t)b * a.s_stride + (size_t)h * D * D);
-    f4 s[NPASS];
-#pragma unroll
-    for (int m = 0; m < NPASS; m++)
-        s[m] = a.stream_state ? __builtin_nontemporal_load(&Sp[(rs + m * RPP) * CPR + cg]) : Sp[(rs + m * RPP) * CPR + cg];
-
-    if constexpr (ZIN) {
-        if (tid < D) s_z[tid] = zin;
-    } else {
+    if constexpr (!ZIN) {
         f32x4 zs = 0.0f;
 #pragma unroll
         for (int t = 0; t < KT; t++) {
@@ -152,36 +202,26 @@ __global__ __launch_bounds__(4 * D) void kda_layer_step_kernel(const StepArgs a)
             zs = t == 0 ? p : zs + p;
         }
         if (ln < 16) s_z[16 * wv + ln] = zs[0];   // C layout: lane n < 16 holds row 0, column n
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < CPL; e++) pz[e] = s_z[cl + e];
     }
-    __syncthreads();
 
-    // K1: task 0..3 = q, k, v, decay gate; half-wave hw takes tasks hw, hw + NT/32, ...
-    const int hw = tid >> 5, l32 = tid & 31;
-    const bool active = l32 * CPL < D;
-    const int cl = active ? l32 * CPL : 0;   // channel within the head
-    const size_t c0 = (size_t)h * D + cl;
-    float *hist = a.hist + (size_t)b * a.h_stride;   // [3][P][K-1]
-    for (int task = hw; task < 4; task += NT / 32) {
-        float yv[CPL];
+    // K1 on the preloaded operands
+#pragma unroll
+    for (int i = 0; i < TPT; i++) {
+        const int task = hw + i * HWS;
         if (task < 3) {
-            const float *cw = task == 0 ? a.q_conv : (task == 1 ? a.k_conv : a.v_conv);
-            const void *src = task == 0 ? a.qi : (task == 1 ? a.ki : a.vi);
+            float yv[CPL];
 #pragma unroll
             for (int e = 0; e < CPL; e++) {
                 const size_t ch = c0 + e;
-                const size_t at = (size_t)b * a.ldi + ch;
-                const float cur = a.in_dt == K3HIP_BF16 ? load_act<K3HIP_BF16>(src, at) : load_act<K3HIP_F32>(src, at);
-                float w[K], win[NH > 0 ? NH : 1];
-#pragma unroll
-                for (int j = 0; j < K; j++) w[j] = cw[ch * K + j];
-                float *hs = hist + ((size_t)task * P + ch) * NH;
-#pragma unroll
-                for (int j = 0; j < NH; j++) win[j] = hs[j];
-                yv[e] = active ? conv_silu<K>(w, win, cur) : 0.0f;
+                yv[e] = active ? conv_silu<K>(pw[i][e], ph[i][e], pcur[i][e]) : 0.0f;
                 if (active) {
+                    float *hs = hist + ((size_t)task * P + ch) * NH;
 #pragma unroll
-                    for (int j = 0; j + 1 < NH; j++) hs[j] = win[j + 1];
-                    if constexpr (NH > 0) hs[NH - 1] = cur;
+                    for (int j = 0; j + 1 < NH; j++) hs[j] = ph[i][e][j + 1];
+                    if constexpr (NH > 0) hs[NH - 1] = pcur[i][e];
                 }
             }
             if (task < 2) l2norm_half<CPL>(yv);   // uniform per half-wave: both halves of a wave
@@ -189,19 +229,17 @@ __global__ __launch_bounds__(4 * D) void kda_layer_step_kernel(const StepArgs a)
             if (active)
 #pragma unroll
                 for (int e = 0; e < CPL; e++) dst[cl + e] = task == 0 ? yv[e] * a.q_scale : yv[e];
-        } else if (active) {
-            const float ea = expf(a.A_log[h]);
+        } else if (task == 3 && active) {
+            const float ea = expf(pA);
 #pragma unroll
             for (int e = 0; e < CPL; e++) {
-                const size_t ch = c0 + e;
-                const float z = s_z[cl + e];
-                const float g = a.lb != 0.0f ? gate_bounded(a.lb, gate_a2(ea), z, a.dt_bias[ch])
-                                             : -ea * softplus_ref(z + a.dt_bias[ch]);   // softplus gate
+                const float g = a.lb != 0.0f ? gate_bounded(a.lb, gate_a2(ea), pz[e], pdt[e])
+                                             : -ea * softplus_ref(pz[e] + pdt[e]);   // softplus gate
                 s_a[cl + e] = fast_exp(g);
             }
         }
     }
-    if (tid == 0) s_beta = fast_sigmoid(a.bl[(size_t)b * a.ldb + h]);
+    if (tid == 0) s_beta = fast_sigmoid(pbl);
     __syncthreads();
 
     // K3 (kda_decode_kernel): decay the rows, partial u over this thread's rows
@@ -243,18 +281,6 @@ __global__ __launch_bounds__(4 * D) void kda_layer_step_kernel(const StepArgs a)
     f4 x = s_red[0][tid];
 #pragma unroll
     for (int r = 1; r < RPP; r++) x = x + s_red[r][tid];
-    const size_t at = (size_t)b * P + (size_t)h * D + 4 * tid;
-    f4 gt;
-    if (a.g_dt == K3HIP_BF16) {
-        const uint2 v = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(a.gl) + at);
-        gt = f4{__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u), __uint_as_float(v.y << 16),
-                __uint_as_float(v.y & 0xffff0000u)};
-    } else {
-        const float *g32 = reinterpret_cast<const float *>(a.gl);
-        gt = *reinterpret_cast<const f4 *>(g32 + at);
-        for (int sp = 1; sp < a.gsplit; sp++) gt = gt + *reinterpret_cast<const f4 *>(g32 + (size_t)sp * a.gplane + at);
-    }
-    const f4 w = reinterpret_cast<const f4 *>(a.o_norm)[tid];
     double ss = (double)(((x.x * x.x) + (x.y * x.y)) + ((x.z * x.z) + (x.w * x.w)));
 #pragma unroll
     for (int m = CPR / 2; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
@@ -263,14 +289,14 @@ __global__ __launch_bounds__(4 * D) void kda_layer_step_kernel(const StepArgs a)
 #pragma unroll
     for (int e = 0; e < 4; e++) {
         const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-gt[e] * 1.4426950408889634f));
-        out[e] = ((w[e] * x[e]) * inv) * sg;
+        out[e] = ((wn[e] * x[e]) * inv) * sg;
     }
     if (a.y_dt == K3HIP_BF16) {
         const uint2 v = {(uint32_t)f2bf(out[0]) | ((uint32_t)f2bf(out[1]) << 16),
                          (uint32_t)f2bf(out[2]) | ((uint32_t)f2bf(out[3]) << 16)};
-        *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(a.y) + at) = v;
+        *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(a.y) + at4) = v;
     } else {
-        *reinterpret_cast<f4 *>(reinterpret_cast<float *>(a.y) + at) = out;
+        *reinterpret_cast<f4 *>(reinterpret_cast<float *>(a.y) + at4) = out;
     }
 }
 
