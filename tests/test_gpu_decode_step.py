@@ -7,7 +7,8 @@ configuration (H=32, D=128) down to D=16 with conv_k 1-4, both input and output 
 bounded and the softplus gate.
 
 Tolerance: the decode bar, rtol 1e-4 and atol 1e-4 * rms(ref) on fp32 outputs and on the
-state; bf16 y adds its own rounding (rtol 2^-8). The same step through the three launches
+state; a bf16 y adds one bf16 ulp (rtol 2^-7: a value within the kernel's fp32 error of a
+rounding midpoint may round either way). The same step through the three launches
 (k3hip_kda_prep, k3hip_kda_decode, k3hip_kda_epilogue) is held to the same bar."""
 from __future__ import annotations
 
@@ -83,7 +84,7 @@ def test_decode_step_vs_oracle(gpu, B, H, D, K, in_bf16, g_bf16, y_bf16, lb):
         gpu.kda_epilogue(o3.view(B, P), dg, dev["o_norm"], y3, H, D, 1e-5)
         torch.cuda.synchronize()
         got = y.float().cpu().numpy()
-        yr = 2.0 ** -8 if y_bf16 else 1e-4
+        yr = 2.0 ** -7 + 1e-4 if y_bf16 else 1e-4
         r = assert_close(got, want, 1e-4 * rms(want), yr, f"decode step {step} y")
         r3 = assert_close(y3.cpu().numpy(), want, 1e-4 * rms(want), 1e-4, f"three-launch step {step} y")
         gS = S.cpu().numpy()
@@ -109,3 +110,16 @@ def test_decode_step_refusals(gpu):
                             torch.zeros((1, 1, 48, 48), device="cuda"), torch.zeros((1, 48), device="cuda"),
                             1, 48, 1, -5.0, 1e-5, 0.125)
     assert e.value.code == gpu.EUNSUPPORTED
+
+
+@pytest.mark.parametrize("case", range(8))
+def test_decode_step_random_vs_oracle(gpu, case):
+    """Seeded random decode steps: B 1-70, H 1-6, D in {16, 32, 64, 128}, conv_k 1-4, gate bound
+    -0.1 to -5.3 or the softplus gate, either input, gate and output dtype, two steps."""
+    rng = np.random.default_rng(0x4B334441 + 0x5E9 + case)
+    B, H = int(rng.integers(1, 71)), int(rng.integers(1, 7))
+    D, K = int(rng.choice([16, 32, 64, 128])), int(rng.integers(1, 5))
+    lb = 0.0 if rng.random() < 0.25 else -float(rng.uniform(0.1, 5.3))
+    flags = [bool(b) for b in rng.integers(0, 2, 3)]
+    print(f"B={B} H={H} D={D} K={K} lb={lb:.3f} bf16 in/gate/y={flags}", flush=True)
+    test_decode_step_vs_oracle(gpu, B, H, D, K, *flags, lb)

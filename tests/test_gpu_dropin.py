@@ -164,3 +164,26 @@ def test_dropin_bf16_prefill_mfma_vs_oracle(gpu, hidden, H, D, K, Ts):
         assert_close(dst.cpu().numpy(), st_ref, 1e-4 * rms(st_ref), 1e-4, f"bf16 device layer call {i} state")
         print(f"bf16 drop-in hidden={hidden} H={H} D={D} T={T}: worst {r:.3f}x of the 1e-4 bar", flush=True)
     dw.close()
+
+
+@pytest.mark.parametrize("case", range(5))
+def test_dropin_int8_random_vs_oracle(gpu, case):
+    """Seeded random int8-weight layers through the host drop-in: hidden 64-520 (any width,
+    so row scales sit at every byte alignment), H 1-4, D in {16, 32, 64, 128}, conv_k 1-4, a
+    prefill of 1-90 tokens then one decode step, against the oracle at the 1e-4 bar."""
+    rng = np.random.default_rng(0x4B334441 + 0x18 + case)
+    hidden, H = int(rng.integers(64, 521)), int(rng.integers(1, 5))
+    D, K, T = int(rng.choice([16, 32, 64, 128])), int(rng.integers(1, 5)), int(rng.integers(1, 91))
+    print(f"hidden={hidden} H={H} D={D} K={K} T={T}", flush=True)
+    W = q8_layer(rng, hidden, H, D, K)
+    cfg = ko.make_cfg(hidden, H, D, K, -5.0, 1e-5)
+    P = H * D
+    st_ref = f32(rng.standard_normal(P * D + 3 * P * (K - 1)) * 0.1)
+    st = st_ref.copy()
+    for Tc in (T, 1):
+        x = f32(rng.standard_normal((Tc, hidden)))
+        want = ko.kda_layer(ko.orc(), x, W, cfg, Tc, st_ref)
+        out = np.zeros((Tc, hidden), np.float32)
+        gpu.kda_layer_host(out, x, W.w, cfg, Tc, st)
+        assert_close(out, want, 1e-4 * rms(want), 1e-4, f"int8 random case {case} T={Tc} out")
+        assert_close(st, st_ref, 1e-4 * rms(st_ref), 1e-4, f"int8 random case {case} T={Tc} state")
