@@ -99,9 +99,12 @@ __global__ __launch_bounds__(4 * D) void kda_layer_step_kernel(const StepArgs a)
     const int cg = tid % CPR, rs = tid / CPR;
     const size_t P = (size_t)H * D;
 
-    // Every global operand is requested up front, so the step waits for memory once: this
-    // thread's K1 inputs (task hw + i HWS: 0..2 = q, k, v conv, 3 = the decay gate), the
-    // state, the beta logit and, for the K4 lanes, the gate logits and o_norm.
+    // Core form: every global operand is requested up front, so the step waits for memory
+    // once: this thread's K1 inputs (task hw + i HWS: 0..2 = q, k, v conv, 3 = the decay
+    // gate), the state, the beta logit and, for the K4 lanes, the gate logits and o_norm. The
+    // layer form loads its K1 and K4 operands where it uses them: holding them across the
+    // z product would take its registers from 90 to 152 and halve the workgroups per CU
+    // (batch-16 step 16 -> 20 us).
     const int hw = tid >> 5, l32 = tid & 31;
     const bool active = l32 * CPL < D;
     const int cl = active ? l32 * CPL : 0;   // channel within the head
@@ -109,8 +112,7 @@ __global__ __launch_bounds__(4 * D) void kda_layer_step_kernel(const StepArgs a)
     float *hist = a.hist + (size_t)b * a.h_stride;   // [3][P][K-1]
     float pcur[TPT][CPL], pw[TPT][CPL][K], ph[TPT][CPL][NH > 0 ? NH : 1], pz[CPL], pdt[CPL];
     float pA = 0.0f;
-#pragma unroll
-    for (int i = 0; i < TPT; i++) {
+    auto k1_operands = [&](int i) {
         const int task = hw + i * HWS;
         if (task < 3) {
             const float *cw = task == 0 ? a.q_conv : (task == 1 ? a.k_conv : a.v_conv);
@@ -134,12 +136,11 @@ __global__ __launch_bounds__(4 * D) void kda_layer_step_kernel(const StepArgs a)
                 if constexpr (ZIN) pz[e] = a.z[(size_t)b * a.ldz + c0 + e];
             }
         }
-    }
-    float pbl = 0.0f;
-    if (tid == 0) pbl = a.bl[(size_t)b * a.ldb + h];
+    };
     const size_t at4 = (size_t)b * P + (size_t)h * D + 4 * (tid % CPR);
     f4 gt = 0.0f, wn = 0.0f;
-    if (tid < CPR) {
+    auto k4_operands = [&]() {
+        if (tid >= CPR) return;
         if (a.g_dt == K3HIP_BF16) {
             const uint2 v = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(a.gl) + at4);
             gt = f4{__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u), __uint_as_float(v.y << 16),
@@ -151,7 +152,14 @@ __global__ __launch_bounds__(4 * D) void kda_layer_step_kernel(const StepArgs a)
                 gt = gt + *reinterpret_cast<const f4 *>(g32 + (size_t)sp * a.gplane + at4);
         }
         wn = reinterpret_cast<const f4 *>(a.o_norm)[tid];
+    };
+    if constexpr (ZIN) {
+#pragma unroll
+        for (int i = 0; i < TPT; i++) k1_operands(i);
+        k4_operands();
     }
+    float pbl = 0.0f;
+    if (tid == 0) pbl = a.bl[(size_t)b * a.ldb + h];
 
     // layer form, z: wave wv takes the head's 16-channel group wv of W_fb (D / 16 groups =
     // NT / 64 waves); A-operand row 0 is this sequence's f_a, rows 1..15 zero.
@@ -207,10 +215,11 @@ __global__ __launch_bounds__(4 * D) void kda_layer_step_kernel(const StepArgs a)
         for (int e = 0; e < CPL; e++) pz[e] = s_z[cl + e];
     }
 
-    // K1 on the preloaded operands
+    // K1
 #pragma unroll
     for (int i = 0; i < TPT; i++) {
         const int task = hw + i * HWS;
+        if constexpr (!ZIN) k1_operands(i);
         if (task < 3) {
             float yv[CPL];
 #pragma unroll
@@ -274,6 +283,7 @@ __global__ __launch_bounds__(4 * D) void kda_layer_step_kernel(const StepArgs a)
         else Sp[(rs + m * RPP) * CPR + cg] = s[m];
     }
     s_red[rs][cg] = acc;   // every read of s_red above finished before the last barrier
+    if constexpr (!ZIN) k4_operands();
     __syncthreads();
     if (tid >= CPR) return;
 
