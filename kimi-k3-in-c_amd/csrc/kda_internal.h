@@ -111,14 +111,19 @@ int gemm_rows_with_part(int B, int K, const float *x, long ldx, int N1, const ui
 // the query rows qcat[b][h] = [A2[b][h] + A2[B+b][h] | q_rope(b, h)] are formed in the kernel
 // from the absorb GEMM's hi/lo halves A2 [2B][H CW] (first KL of each head's CW columns) and
 // q [B][H][QN + CW - KL] (rope at column QN); cache [B][cap][CW] fp32 (latent = channels
-// 0..KL-1), positions 0..Tn-1; writes chat = softmax(scale qcat . cache^T) . latent as bf16
-// hi (rows 0..B-1) and lo (rows B..2B-1) of ch2 [2B][H KL]. Shapes: mla_attention_supported
-// (H <= 64, KL a multiple of 16 up to 512, CW a multiple of 4 up to 576) and QN % 4 == 0.
-// ws: mla_attention_ws_bytes bytes, 256-byte aligned; A2, q and cache 16-byte aligned.
+// 0..KL-1), positions 0..Tn-1; chat = softmax(scale qcat . cache^T) . latent (its position
+// ranges merged into the bf16 hi / lo rows of ch2 [2B][H KL], 16-byte aligned), then
+// o [B][H VH] = (chat_h . W_UV_h^T) * sigmoid(g) with W_UV_h the rows
+// h (QN + VH) + QN .. + VH of kvb [H (QN + VH)][KL] (bf16) and g (may be nullptr) the gate
+// logits at row stride ldg; zout[0 .. zn) = 0 on the way (may be nullptr). Shapes:
+// mla_attention_supported (H <= 64, KL a multiple of 16 up to 512, CW a multiple of 4 up to
+// 576), QN % 4 == 0, KL % 8 == 0, VH <= 128. ws: mla_attention_ws_bytes bytes, 256-byte aligned; A2, q,
+// cache and kvb 16-byte aligned.
 bool mla_attention_supported(int H, int KL, int CW);
 size_t mla_attention_ws_bytes(int B, int H, int KL, int Tn);
 int mla_attention(int B, int H, int KL, int CW, int Tn, int cap, float scale, const float *A2, const float *q,
-                  int QN, const float *cache, uint16_t *ch2, void *ws, size_t ws_bytes, hipStream_t st);
+                  int QN, const float *cache, const uint16_t *kvb, int VH, const float *g, long ldg, float *o,
+                  float *zout, size_t zn, uint16_t *ch2, void *ws, size_t ws_bytes, hipStream_t st);
 
 // One decode token of a KDA layer between its projections (kda_step.hip): K1 + K3 + K4 per
 // (head, sequence). Cin rows (stride ldc) hold q | k | v at columns 0, P, 2P and the beta

@@ -301,10 +301,10 @@ extern "C" int k3hip_mla_decode(const k3hip_mla_weights *w, int B, int pos, int 
         K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_mla_decode: q_lora=%d, heads*v_head=%d not multiples of 8", QL, HV);
     // attention in one pass over the cache (kda_mla_attn.hip) where the shape fits it, else
     // as two strided-batched fp32 GEMMs around the softmax
-    const bool fused = mla_attention_supported(H, KL, CW) && !((uintptr_t)cache & 15) && !(QN & 3);
+    const bool fused = mla_attention_supported(H, KL, CW) && !((uintptr_t)cache & 15) && !(QN & 3) && VH <= 128;
     // scratch: q_a kv_a g projections [B][ld1] | q_a normed | q | q hi/lo | absorb halves | qcat |
-    //          scores or the fused attention's workspace | chat | chat hi/lo | W_UV halves | o |
-    //          split-K partials
+    //          scores or the fused attention's workspace | chat | chat hi/lo | W_UV halves (chat
+    //          and the W_UV halves only without the fused attention) | o | split-K partials
     const int N1 = QL + CW + (w->gate ? HV : 0);
     const long ld1 = (N1 + 3) & ~3;
     const size_t wsf = std::max({gemm_rows_ws_floats(B, N1, E), gemm_rows_ws_floats(B, H * QH, QL),
@@ -313,7 +313,7 @@ extern "C" int k3hip_mla_decode(const k3hip_mla_weights *w, int B, int pos, int 
                       (size_t)2 * B * H * QH * 2, (size_t)2 * B * H * CW * 4, (size_t)B * H * CW * 4,
                       fused ? mla_attention_ws_bytes(B, H, KL, Tn) : (size_t)B * H * Tn * 4,
                       fused ? 0 : (size_t)B * H * KL * 4, (size_t)2 * B * H * KL * 2,
-                      (size_t)2 * B * HV * 4, (size_t)B * HV * 4, wsf * 4};
+                      fused ? 0 : (size_t)2 * B * HV * 4, (size_t)B * HV * 4, wsf * 4};
     constexpr int NB = sizeof sizes / sizeof sizes[0];
     size_t off[NB], total = 0;
     for (int i = 0; i < NB; i++) {
@@ -349,13 +349,20 @@ extern "C" int k3hip_mla_decode(const k3hip_mla_weights *w, int B, int pos, int 
     ga.lda = (long)H * QH; ga.ldb = KL; ga.ldc = (long)H * CW; ga.batch = H;
     ga.sa = QH; ga.sb = (long)(QN + VH) * KL; ga.sc = CW;
     if ((rc = gemm(ga, qs2, kvb, A2, st))) return rc;
+    // o_proj as two K-ranges adds into `out`, zeroed by the kernel before it (no reduction
+    // launch); atomics on ordinary device memory only
+    const bool oz = gemm_rows_splits(E, HV) == 2 && coarse_device_mem(out);
+    const float *gl = w->gate ? C1 + QL + CW : nullptr;
     if (fused) {
-        // the query rows formed inside the attention from A2 and q; chat as the bf16 hi/lo
-        // rows of the W_UV GEMM, straight from the attention
-        if ((rc = mla_attention(B, H, KL, CW, Tn, cap, 1.0f / sqrtf((float)QH), A2, q, QN, cache, ch2, S,
+        // the query rows formed inside the attention from A2 and q; the ranges merged, W_UV and
+        // the output gate applied in the launch after it (kda_mla_attn.hip)
+        if ((rc = mla_attention(B, H, KL, CW, Tn, cap, 1.0f / sqrtf((float)QH), A2, q, QN, cache, kvb, VH, gl, ld1,
+                                o, oz ? out : nullptr, oz ? (size_t)B * E : (size_t)0, ch2, S,
                                 mla_attention_ws_bytes(B, H, KL, Tn), st)))
             return rc;
-    } else {
+        return gemm_rows(B, E, HV, o, HV, (const uint16_t *)w->o, out, E, st, ws, wsf, oz);
+    }
+    {
         hipLaunchKernelGGL(mla_qcat_kernel, dim3(mla_grid((size_t)B * H * CW)), dim3(256), 0, st, A2, q, B, H,
                            QN, QR, KL, qcat);
         K3_LAUNCHED();
@@ -391,11 +398,8 @@ extern "C" int k3hip_mla_decode(const k3hip_mla_weights *w, int B, int pos, int 
     gu.lda = (long)H * KL; gu.ldb = KL; gu.ldc = HV; gu.batch = H;
     gu.sa = KL; gu.sb = (long)(QN + VH) * KL; gu.sc = VH;
     if ((rc = gemm(gu, ch2, kvb + (size_t)QN * KL, O2, st))) return rc;
-    // o_proj as two K-ranges adds into `out`, which the gate kernel zeroes (no reduction launch)
-    const bool oz = gemm_rows_splits(E, HV) == 2 && coarse_device_mem(out);   // atomics: ordinary device memory only
-    hipLaunchKernelGGL(mla_gate_kernel, dim3(mla_grid((size_t)B * HV)), dim3(256), 0, st, O2,
-                       w->gate ? C1 + QL + CW : nullptr, ld1, B, (size_t)HV, o, oz ? out : nullptr,
-                       oz ? (size_t)B * E : (size_t)0);
+    hipLaunchKernelGGL(mla_gate_kernel, dim3(mla_grid((size_t)B * HV)), dim3(256), 0, st, O2, gl, ld1, B,
+                       (size_t)HV, o, oz ? out : nullptr, oz ? (size_t)B * E : (size_t)0);
     K3_LAUNCHED();
     return gemm_rows(B, E, HV, o, HV, (const uint16_t *)w->o, out, E, st, ws, wsf, oz);
 }

@@ -381,6 +381,87 @@ __global__ __launch_bounds__(128) void mla_attn_merge_kernel(int B, int H, int K
     }
 }
 
+// o = (chat . W_UV_h^T) * sigmoid(g) per (head h, block of up to 16 sequences) from the merged
+// chat's bf16 hi / lo rows (ch2 [2B][H KL]): both halves against the bf16 weight into one fp32
+// accumulator on 16x16x32 MFMA (the products exact, the sums fp32), then the output gate
+// sigmoid(g) (the reference's 1 / (1 + expf(-g)), src/core/k3_ops.c:105), written as fp32
+// rows of o [B][H VH] for o_proj. Replaces a head-batched W_UV GEMM and a gate kernel (two
+// launches and the GEMM's two fp32 output planes). W_UV_h = rows h (QN + VH) + QN .. + VH of
+// kvb [H (QN + VH)][KL]. zout[0 .. zn) = 0 on the way (may be nullptr) for an o_proj that
+// adds its two K-range partials there.
+constexpr int AO_NT = 512;                 // 8 waves, one 16-column tile of o each (VH <= 128)
+constexpr int AO_KP = 32 * 16 + 8;         // LDS row pitch (bf16): 16 bytes of skew per row
+__global__ __launch_bounds__(AO_NT) void mla_attn_out_kernel(int B, int H, int KL, int QN, int VH,
+                                                            const uint16_t *__restrict__ ch2,
+                                                            const uint16_t *__restrict__ kvb,
+                                                            const float *__restrict__ g, long ldg,
+                                                            float *__restrict__ o, float *__restrict__ zout, size_t zn)
+{
+    __shared__ __attribute__((aligned(16))) uint16_t chh[16 * AO_KP], chl[16 * AO_KP];
+    const int h = blockIdx.x, b0 = blockIdx.y * 16, nb = min(16, B - b0), tid = threadIdx.x;
+    const int lane = tid & 63, wv = tid >> 6;
+    const int r16 = lane & 15, kq = lane >> 4;
+    const int KLr = (KL + 31) & ~31;
+    // this wave's weight fragments (column tile wv of o, every K-step) and gate logits are
+    // requested first, with the chat rows, so the step waits for memory once
+    const uint16_t *Wuv = kvb + ((size_t)h * (QN + VH) + QN) * KL;   // [VH][KL]
+    const int n = wv * 16 + r16;
+    const bool nok = n < VH;
+    const uint16_t *wrow = Wuv + (size_t)(nok ? n : 0) * KL;
+    bf16x8 wf[AT_MAXCT / 2];
+#pragma unroll
+    for (int ks = 0; ks < AT_MAXCT / 2; ks++) {
+        const int k = 32 * ks + 8 * kq;
+        wf[ks] = bf16x8{};
+        if (nok && k < KL) wf[ks] = *reinterpret_cast<const bf16x8 *>(wrow + k);
+    }
+    float gv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (g && nok)
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            if (4 * kq + e < nb) gv[e] = g[(size_t)(b0 + 4 * kq + e) * ldg + (size_t)h * VH + n];
+    // the block's chat rows (hi and lo) into LDS, 8 bf16 per thread and pass; rows past nb and
+    // channels past KL are zero
+    const size_t BN = (size_t)B * H * KL;
+    for (int it = tid; it < 16 * (KLr / 8); it += AO_NT) {
+        const int r = it / (KLr / 8), c = 8 * (it % (KLr / 8));
+        uint4 vh = {0, 0, 0, 0}, vl = {0, 0, 0, 0};
+        if (r < nb && c < KL) {
+            const size_t i = ((size_t)(b0 + r) * H + h) * KL + c;
+            vh = *reinterpret_cast<const uint4 *>(ch2 + i);
+            vl = *reinterpret_cast<const uint4 *>(ch2 + BN + i);
+        }
+        *reinterpret_cast<uint4 *>(chh + r * AO_KP + c) = vh;
+        *reinterpret_cast<uint4 *>(chl + r * AO_KP + c) = vl;
+    }
+    if (zout) {
+        const size_t nwg = (size_t)gridDim.x * gridDim.y, id = (size_t)blockIdx.y * gridDim.x + h;
+        const size_t per = (zn + nwg - 1) / nwg, z0 = id * per, z1 = min(zn, z0 + per);
+        for (size_t i = z0 + tid; i < z1; i += AO_NT) zout[i] = 0.0f;
+    }
+    __syncthreads();
+    if (wv * 16 >= VH) return;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int ks = 0; ks < AT_MAXCT / 2; ks++) {
+        if (32 * ks >= KLr) break;
+        const int k = 32 * ks + 8 * kq;
+        const bf16x8 ah = *reinterpret_cast<const bf16x8 *>(chh + r16 * AO_KP + k);
+        const bf16x8 al = *reinterpret_cast<const bf16x8 *>(chl + r16 * AO_KP + k);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, wf[ks], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, wf[ks], acc, 0, 0, 0);
+    }
+    // C layout: lane holds rows 4 kq + e (sequences), column r16 (value channel n)
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int r = 4 * kq + e;
+        if (r >= nb || !nok) continue;
+        float v = acc[e];
+        if (g) v *= 1.0f / (1.0f + expf(-gv[e]));
+        o[(size_t)(b0 + r) * H * VH + (size_t)h * VH + n] = v;
+    }
+}
+
 int at_cus()
 {
     static int n = 0;
@@ -427,7 +508,8 @@ bool mla_attention_supported(int H, int KL, int CW)
 }
 
 int mla_attention(int B, int H, int KL, int CW, int Tn, int cap, float scale, const float *A2, const float *q,
-                  int QN, const float *cache, uint16_t *ch2, void *ws, size_t ws_bytes, hipStream_t st)
+                  int QN, const float *cache, const uint16_t *kvb, int VH, const float *gate, long ldg, float *o,
+                  float *zout, size_t zn, uint16_t *ch2, void *ws, size_t ws_bytes, hipStream_t st)
 {
     AtGeom g;
     if (!at_geom(H, KL, CW, g))
@@ -437,7 +519,8 @@ int mla_attention(int B, int H, int KL, int CW, int Tn, int cap, float scale, co
     const size_t need = mla_attention_ws_bytes(B, H, KL, Tn);
     const int QH = QN + (CW - KL);
     if (!ws || ws_bytes < need || ((uintptr_t)ws & 255) || ((uintptr_t)cache & 15) || ((uintptr_t)A2 & 15) ||
-        ((uintptr_t)q & 15) || (QN & 3))
+        ((uintptr_t)q & 15) || (QN & 3) || (KL & 7) || ((uintptr_t)kvb & 15) || ((uintptr_t)ch2 & 15) ||
+        VH < 1 || VH > 16 * (AO_NT / 64))
         K3_FAIL(K3HIP_EINVAL, "mla attention: workspace %zu < %zu bytes, or a misaligned buffer", ws_bytes, need);
     const AtQ qs{A2, q, B, QN, QH};
     const size_t r = (size_t)B * nsplit * H;
@@ -460,6 +543,9 @@ int mla_attention(int B, int H, int KL, int CW, int Tn, int cap, float scale, co
                            scale * AT_LOG2E, qs, cache, pctx, pm, pl);
     K3_LAUNCHED();
     hipLaunchKernelGGL(mla_attn_merge_kernel, dim3(H, B), dim3(128), 0, st, B, H, KL, nsplit, pctx, pm, pl, ch2);
+    K3_LAUNCHED();
+    hipLaunchKernelGGL(mla_attn_out_kernel, dim3(H, (B + 15) / 16), dim3(AO_NT), 0, st, B, H, KL, QN, VH, ch2, kvb,
+                       gate, ldg, o, zout, zn);
     K3_LAUNCHED();
     return K3HIP_OK;
 }
