@@ -21,8 +21,10 @@
 // Arithmetic: K1 is that of kda_prep_math.h with one half-wave per row (the wide prep
 // kernel's layout: CPL = max(1, D/32) adjacent channels per lane, fp32 L2 sums), K3 that of
 // kda_decode_kernel (same thread tile, same reduction order), K4 that of
-// kda_epilogue2_kernel (fp32 per-lane squares, double across the row's lanes, hardware
-// sigmoid). The output-gate logits may arrive as split-K partial planes of the gate
+// kda_epilogue2_kernel except for the row's sum of squares: fp32 per-lane squares added
+// across the half-wave by DPP in fp32 (the epilogue kernel adds the lanes in double; for a
+// 128-channel head the two differ by a few 1e-7 relative) and the hardware reciprocal
+// square root; hardware sigmoid. The output-gate logits may arrive as split-K partial planes of the gate
 // projection; they are added in plane order, which is what the split-K reduction does.
 //
 // The core form (k3hip_kda_decode_step) takes the decay logits z and the conv inputs as
@@ -279,34 +281,40 @@ __global__ __launch_bounds__(4 * D) void kda_layer_step_kernel(const StepArgs a)
         const float kr = s_k[r], qr = s_q[r];
         if (kr != 0.0f) s[m] = s[m] + (kr * bt) * d;
         if (qr != 0.0f) acc = acc + qr * s[m];
-        if (a.stream_state) __builtin_nontemporal_store(s[m], &Sp[(rs + m * RPP) * CPR + cg]);
-        else Sp[(rs + m * RPP) * CPR + cg] = s[m];
     }
     s_red[rs][cg] = acc;   // every read of s_red above finished before the last barrier
     if constexpr (!ZIN) k4_operands();
     __syncthreads();
-    if (tid >= CPR) return;
 
-    // K4 (kda_epilogue2_kernel) on o = the CPR lanes' float4s: RMSNorm, then the gate
-    f4 x = s_red[0][tid];
+    // K4 (kda_epilogue2_kernel's RMSNorm and gate) on o = the first CPR lanes' float4s, in the
+    // first half-wave; the other waves store their part of the new state meanwhile (the
+    // state stores, 4 D^2 bytes through one CU, take longer than K4)
+    if (tid < 32) {
+        f4 x = s_red[0][tid < CPR ? tid : 0];
 #pragma unroll
-    for (int r = 1; r < RPP; r++) x = x + s_red[r][tid];
-    double ss = (double)(((x.x * x.x) + (x.y * x.y)) + ((x.z * x.z) + (x.w * x.w)));
+        for (int r = 1; r < RPP; r++) x = x + s_red[r][tid < CPR ? tid : 0];
+        const float part = tid < CPR ? ((x.x * x.x) + (x.y * x.y)) + ((x.z * x.z) + (x.w * x.w)) : 0.0f;
+        const float inv = __builtin_amdgcn_rsqf(half_wave_sum(part) / (float)D + a.eps);
+        if (tid < CPR) {
+            f4 out;
 #pragma unroll
-    for (int m = CPR / 2; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
-    const float inv = (float)(1.0 / sqrt(ss / (double)D + (double)a.eps));
-    f4 out;
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-        const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-gt[e] * 1.4426950408889634f));
-        out[e] = ((wn[e] * x[e]) * inv) * sg;
+            for (int e = 0; e < 4; e++) {
+                const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-gt[e] * 1.4426950408889634f));
+                out[e] = ((wn[e] * x[e]) * inv) * sg;
+            }
+            if (a.y_dt == K3HIP_BF16) {
+                const uint2 v = {(uint32_t)f2bf(out[0]) | ((uint32_t)f2bf(out[1]) << 16),
+                                 (uint32_t)f2bf(out[2]) | ((uint32_t)f2bf(out[3]) << 16)};
+                *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(a.y) + at4) = v;
+            } else {
+                *reinterpret_cast<f4 *>(reinterpret_cast<float *>(a.y) + at4) = out;
+            }
+        }
     }
-    if (a.y_dt == K3HIP_BF16) {
-        const uint2 v = {(uint32_t)f2bf(out[0]) | ((uint32_t)f2bf(out[1]) << 16),
-                         (uint32_t)f2bf(out[2]) | ((uint32_t)f2bf(out[3]) << 16)};
-        *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(a.y) + at4) = v;
-    } else {
-        *reinterpret_cast<f4 *>(reinterpret_cast<float *>(a.y) + at4) = out;
+#pragma unroll
+    for (int m = 0; m < NPASS; m++) {
+        if (a.stream_state) __builtin_nontemporal_store(s[m], &Sp[(rs + m * RPP) * CPR + cg]);
+        else Sp[(rs + m * RPP) * CPR + cg] = s[m];
     }
 }
 
