@@ -12,26 +12,26 @@
 //
 //  * A workgroup (8 waves, two per SIMD) owns one sequence and a contiguous range of
 //    positions (~CUs/B ranges per sequence) and walks it in tiles of 16 positions (16
-//    contiguous cache rows). Every thread loads its 16-byte units of a tile two tiles
+//    contiguous cache rows). Every thread loads its 16-byte units of a tile one iteration
 //    ahead into registers, splits them into bf16 hi/lo and stages them row-major in LDS
-//    (four tile buffers).
-//  * The two waves of a SIMD take different roles on consecutive tiles, so one score
-//    product and one weighted sum share the SIMD's MFMA pipe instead of both waves running
-//    the same phase. Lane l of wave w works for head 16 (w % 4) + (l & 15) in both roles:
-//      S waves (0-3), tile it: scores^T (positions x heads) = cache tile (16 x CW) . qcat^T
-//        on split-bf16 MFMA (16x16x32, cache rows read from LDS, the q fragments of all 18
-//        K-steps held in registers for the whole range; the channel halves summed
-//        separately and then added), then the online softmax in base 2: running max M
-//        (exchanged between the 4 lanes of a head), per-lane partial sums; P (bf16 hi/lo)
-//        and the rescale factor 2^(M_old - M_new) go to LDS;
-//      U waves (4-7), tile it - 1: the weighted sums, all 32 latent channel tiles, rescaled
-//        only when some max of the wave grew, then chat^T (latent channels x heads) +=
-//        latent tile^T . P on split-bf16 MFMA (16x16x16); the transposed latent fragments
-//        come straight from the row-major tile through ds_read_b64_tr_b16, and P is read in
-//        the score product's output layout (the lanes that hold a head's scores are the
-//        lanes that need its weights).
-//    One barrier per tile: P of tile it and the staging of tile it + 2 are published, tiles
-//    it and it - 1 consumed.
+//    (four tile buffers: the tile being scored, the two being summed, the next one).
+//  * The two waves of a SIMD take different roles, so score products and weighted sums
+//    share the SIMD's MFMA pipe instead of both waves running the same phase:
+//      S waves (0-3), tile it, heads 16 w + (l & 15): scores^T (positions x heads) = cache
+//        tile (16 x CW) . qcat^T on split-bf16 MFMA (16x16x32, cache rows read from LDS, the
+//        q fragments of all 18 K-steps held in registers for the whole range; K-steps in
+//        groups of three on three accumulators, so dependent MFMAs do not wait on each
+//        other), then the online softmax in base 2: a reference max M per head (exchanged
+//        between the 4 lanes of a head) that moves only when a score passes it by AT_LAZY,
+//        per-lane partial sums; P (bf16 hi/lo) and the rescale factor 2^(M_old - M_new)
+//        go to LDS;
+//      U waves (4-7), latent channel tiles 8 (w - 4) .. + 7 for all heads, tiles it - 2 and
+//        it - 1 at even iterations: chat^T (latent channels x heads) += latent^T . P on
+//        split-bf16 MFMA with K = the pair's 32 positions (16x16x32, twice the rate of the
+//        16-deep form), rescaled only when a max moved; the transposed latent fragments come
+//        straight from the row-major tiles through ds_read_b64_tr_b16 (each fragment read by
+//        one wave), and P in the score product's output layout.
+//    One barrier per iteration: P of tile it and the staging of tile it + 1 are published.
 //  * Each workgroup writes its unnormalised sums with (M, l); a second kernel merges the
 //    ranges of a sequence (weights 2^(M_s - M*), the sums in a fixed order), divides by the
 //    merged sum and writes chat directly as the bf16 hi/lo rows of the W_UV GEMM.
@@ -54,14 +54,14 @@ typedef s16x4 __attribute__((address_space(3))) *lds_s16x4_ptr;
 constexpr int AT_T = 16;             // positions per tile
 constexpr int AT_NT = 512;           // threads per workgroup: 8 waves, two per SIMD
 constexpr int AT_MAXKS = 18;         // 32-channel K-steps of the scores (kv_lora + rope <= 576)
-constexpr int AT_KSW = AT_MAXKS / 2; // K-steps per channel half of the score product
 constexpr int AT_MAXCT = 32;         // 16-channel tiles of the latent (kv_lora <= 512)
 constexpr int AT_MAXU = 5;           // 16-byte cache loads per thread per tile (kv_lora + rope <= 576)
 constexpr int AT_NB = 4;             // staged tile buffers
-constexpr int AT_UPF = 8;            // channel tiles of transposed reads in flight (U waves)
-constexpr int AT_SPF = 4;            // K-steps of cache fragment reads in flight (S waves)
+constexpr int AT_UCT = AT_MAXCT / 4; // latent channel tiles per U wave
+constexpr int AT_UPF = 2;            // channel tiles of transposed reads in flight (U waves)
 constexpr int AT_MAXSPLIT = 64;      // position ranges per sequence
 constexpr float AT_LOG2E = 1.4426950408889634f;
+constexpr float AT_LAZY = 8.0f;      // log2 of the largest softmax weight before a rescale
 
 // LDS: AT_NB buffers x {hi, lo} x [AT_T][AT_PR] bf16 (152 KB), then P and the rescale
 // factors of two tiles (10 KB). Rows hold the 576 channels of the largest shape (smaller
@@ -98,30 +98,11 @@ __device__ __forceinline__ void split2(float a, float b, bf16x2 &hi, bf16x2 &lo)
     lo = __builtin_convertvector(f2{a - __uint_as_float(u << 16), b - __uint_as_float(u & 0xffff0000u)}, bf16x2);
 }
 
-// acc + ah.bh + ah.bl + al.bh, 16x16x32 bf16 MFMA (A rows x K, B K x columns)
-__device__ __forceinline__ f32x4 mma3_32(f32x4 acc, const bf16x8 &ah, const bf16x8 &al, const bf16x8 &bh,
-                                         const bf16x8 &bl)
-{
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
-}
-
-// the same on 16x16x16 bf16 MFMA (4 K values per lane)
-__device__ __forceinline__ f32x4 mma3_16(f32x4 acc, const s16x4 &ah, const s16x4 &al, const s16x4 &bh,
-                                         const s16x4 &bl)
-{
-    acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(al, bh, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bl, acc, 0, 0, 0);
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bh, acc, 0, 0, 0);
-}
-
 // Workgroup (sp, b): positions [Tn sp / nsplit, Tn (sp + 1) / nsplit) of sequence b.
-// Wave w: head tile ht = w % 4 (heads 16 ht .. 16 ht + 15), S role for w < 4, U role
-// otherwise. Lane l works for head h = 16 ht + (l & 15); kg = l >> 4 picks its K slice in
-// the score product and its 4 positions of each tile (4 kg .. 4 kg + 3). The S wave sums
-// the score product as K-steps 0-8 and 9-17, each into two alternating accumulators, then
-// the two halves. FULL: kv_lora + rope = 576, every staging unit of a row exists.
+// Wave w: S role for w < 4 (head tile ht = w: heads 16 ht .. 16 ht + 15; lane l works for
+// head h = 16 ht + (l & 15), kg = l >> 4 picks its K slice in the score product and its 4
+// positions of each tile, 4 kg .. 4 kg + 3), U role otherwise (latent channel quarter
+// w - 4, all head tiles). FULL: kv_lora + rope = 576, every staging unit of a row exists.
 template <bool FULL>
 __global__ __launch_bounds__(AT_NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void mla_attn_kernel(
     AtGeom g, int Tn, int cap, int nsplit, float scale2, AtQ qs,
@@ -175,9 +156,10 @@ __global__ __launch_bounds__(AT_NT) __attribute__((amdgpu_waves_per_eu(2, 2))) v
     load_tile(0);
     stage(0);
     load_tile(1);
-    stage(1);
-    load_tile(2);
     __syncthreads();
+    // the U waves take the tiles in pairs (one K = 32 product per channel tile): an even
+    // iteration closes the pair before it, so the loop runs to the even count at or past ntile
+    const int itend = ntile + (ntile & 1);
     // iteration it: S scores tile it, U sums tile it - 1, every thread stages tile it + 2
     // (loaded one iteration earlier) and loads tile it + 3; both roles pass one barrier per
     // iteration
@@ -217,33 +199,49 @@ __global__ __launch_bounds__(AT_NT) __attribute__((amdgpu_waves_per_eu(2, 2))) v
             const int buf = it % AT_NB;
             const uint16_t *hi = at_smem + (size_t)(2 * buf) * AT_PLANE + m * AT_PR + at_col(m, 8 * kg);
             const uint16_t *lo = hi + AT_PLANE;
-            // the cache fragments are read AT_SPF K-steps ahead of the MFMAs that use them
-            bf16x8 rah[AT_SPF], ral[AT_SPF];
+            // K-steps in groups of three, one accumulator each: each of the three split products
+            // runs over the group's accumulators in turn (three independent chains hide the
+            // ~40-cycle latency of a dependent MFMA); the next group's lo fragments are read once
+            // this group's second product is issued, its hi fragments after the third
+            constexpr int SG = 3;
+            static_assert(AT_MAXKS % SG == 0, "K-step groups");
+            bf16x8 rah[SG], ral[SG];
 #pragma unroll
-            for (int ks = 0; ks < AT_SPF; ks++) {
-                rah[ks] = *reinterpret_cast<const bf16x8 *>(hi + 32 * ks);
-                ral[ks] = *reinterpret_cast<const bf16x8 *>(lo + 32 * ks);
+            for (int t = 0; t < SG; t++) {
+                ral[t] = *reinterpret_cast<const bf16x8 *>(lo + 32 * t);
+                rah[t] = *reinterpret_cast<const bf16x8 *>(hi + 32 * t);
             }
             __builtin_amdgcn_sched_barrier(0);
-            f32x4 half[2], s0 = 0.0f, s1 = 0.0f;
+            f32x4 sa[SG];
 #pragma unroll
-            for (int ks = 0; ks < AT_MAXKS; ks++) {
-                const int i = ks % AT_KSW;
-                const bf16x8 ah = rah[ks % AT_SPF], al = ral[ks % AT_SPF];
-                if (ks + AT_SPF < AT_MAXKS) {
-                    rah[ks % AT_SPF] = *reinterpret_cast<const bf16x8 *>(hi + 32 * (ks + AT_SPF));
-                    ral[ks % AT_SPF] = *reinterpret_cast<const bf16x8 *>(lo + 32 * (ks + AT_SPF));
+            for (int t = 0; t < SG; t++) sa[t] = 0.0f;
+#pragma unroll
+            for (int k0 = 0; k0 < AT_MAXKS; k0 += SG) {
+                const bool nxt = k0 + SG < AT_MAXKS;
+#pragma unroll
+                for (int t = 0; t < SG; t++)
+                    sa[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ral[t], qh[k0 + t], sa[t], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int t = 0; t < SG; t++)
+                    sa[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(rah[t], ql[k0 + t], sa[t], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                if (nxt) {
+#pragma unroll
+                    for (int t = 0; t < SG; t++) ral[t] = *reinterpret_cast<const bf16x8 *>(lo + 32 * (k0 + SG + t));
                 }
-                if (i & 1) s1 = mma3_32(s1, ah, al, qh[ks], ql[ks]);
-                else s0 = mma3_32(s0, ah, al, qh[ks], ql[ks]);
-                if (i == AT_KSW - 1) {   // a channel half done: K-steps 0-8, then 9-17
-                    half[ks / AT_KSW] = s0 + s1;
-                    s0 = 0.0f;
-                    s1 = 0.0f;
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int t = 0; t < SG; t++)
+                    sa[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(rah[t], qh[k0 + t], sa[t], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                if (nxt) {
+#pragma unroll
+                    for (int t = 0; t < SG; t++) rah[t] = *reinterpret_cast<const bf16x8 *>(hi + 32 * (k0 + SG + t));
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
-            const f32x4 s = half[0] + half[1];
+            const f32x4 s = (sa[0] + sa[1]) + sa[2];
             const int t0 = p0 + AT_T * it + 4 * kg;
             float x[4], mt = -INFINITY;
 #pragma unroll
@@ -253,7 +251,10 @@ __global__ __launch_bounds__(AT_NT) __attribute__((amdgpu_waves_per_eu(2, 2))) v
             }
             mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
             mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-            const float mn = fmaxf(M, mt);
+            // the reference max moves only when a score passes it by AT_LAZY (base 2): the
+            // weights stay below 2^AT_LAZY and the sums are rescaled rarely; the ranges' merge
+            // takes each range's reference max with its sums, so the result is the same
+            const float mn = mt > M + AT_LAZY ? mt : M;
             const float alpha = __builtin_amdgcn_exp2f(M - mn);
             float p[4];
 #pragma unroll
@@ -268,10 +269,10 @@ __global__ __launch_bounds__(AT_NT) __attribute__((amdgpu_waves_per_eu(2, 2))) v
                                                    __builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23)};
             reinterpret_cast<float *>(sbase + AT_A)[((it & 1) * 4 + ht) * 64 + lane] = alpha;
         };
-        for (int it = 0; it <= ntile; it++) {
+        for (int it = 0; it <= itend; it++) {
             if (act && it < ntile) s_tile(it);
-            stage((it + 2) % AT_NB);   // past the last tile: a copy nothing reads
-            load_tile(it + 3);
+            stage((it + 1) % AT_NB);   // past the last tile: a copy nothing reads
+            load_tile(it + 2);
             __syncthreads();
         }
         lsum += __shfl_xor(lsum, 16, 64);
@@ -281,53 +282,157 @@ __global__ __launch_bounds__(AT_NT) __attribute__((amdgpu_waves_per_eu(2, 2))) v
             pl[((size_t)b * nsplit + sp) * H + h] = lsum;
         }
     } else {
-        // chat^T[channel 16 j + 4 kg + e][head m] for all 32 channel tiles
-        f32x4 acc[AT_MAXCT];
+        // U wave u = w - 4 owns latent channel tiles 8 u .. 8 u + 7 for all four head tiles:
+        // acc[jj][g] = chat^T[channel 16 (8 u + jj) + 4 kg + e][head 16 g + m], so each latent
+        // fragment is read from LDS by one wave only (a wave per head tile would read every
+        // fragment four times and make the LDS the bound)
+        const int u = w - 4;
+        f32x4 acc[AT_UCT][4];
 #pragma unroll
-        for (int j = 0; j < AT_MAXCT; j++) acc[j] = 0.0f;
-        auto u_tile = [&](int it) {
-            const int buf = it % AT_NB;
-            const uint16_t *hi = at_smem + (size_t)(2 * buf) * AT_PLANE, *lo = hi + AT_PLANE;
-            const uint4 pv = *reinterpret_cast<const uint4 *>(sbase + AT_P + ((size_t)((it & 1) * 4 + ht) * 64 + lane) * 16);
-            const float alpha = reinterpret_cast<const float *>(sbase + AT_A)[((it & 1) * 4 + ht) * 64 + lane];
-            if (__ballot(alpha != 1.0f)) {
+        for (int jj = 0; jj < AT_UCT; jj++)
 #pragma unroll
-                for (int j = 0; j < AT_MAXCT; j++) acc[j] *= alpha;
+            for (int g2 = 0; g2 < 4; g2++) acc[jj][g2] = 0.0f;
+        // P operands per head tile g2. Lane (head 16 g2 + m, K slice kg) supplies positions
+        // 4 (kg & 1) .. + 3 and 8 + 4 (kg & 1) .. + 3 of the pair's tile kg >> 1 (so that each
+        // 32-lane half of a transposed read covers 8 rows of one half of the tile, on distinct
+        // banks): the entries (hi01, hi23, lo01, lo23) of the head's S lanes kg & 1 and
+        // 2 + (kg & 1). The lanes of the pair's first tile (kg < 2) read theirs one iteration
+        // early: the S waves overwrite that P buffer in the pair's iteration.
+        uint4 pa[4], pb[4];
+        float al0[4];
+        const int src0 = m + 16 * (kg & 1), src1 = src0 + 32;
+        auto p_entry = [&](int t, int g2, int src) {
+            return *reinterpret_cast<const uint4 *>(sbase + AT_P + ((size_t)((t & 1) * 4 + g2) * 64 + src) * 16);
+        };
+        auto alpha_of = [&](int t, int g2) {
+            return reinterpret_cast<const float *>(sbase + AT_A)[((t & 1) * 4 + g2) * 64 + lane];
+        };
+        auto u_grab = [&](int t0) {
+            // every read first, one wait
+            float a[4];
+            uint4 xa[4], xb[4];
+#pragma unroll
+            for (int g2 = 0; g2 < 4; g2++) {
+                a[g2] = alpha_of(t0, g2);
+                xa[g2] = p_entry(t0, g2, src0);
+                xb[g2] = p_entry(t0, g2, src1);
             }
-            const s16x4 ph = __builtin_bit_cast(s16x4, uint2{pv.x, pv.y});
-            const s16x4 pq = __builtin_bit_cast(s16x4, uint2{pv.z, pv.w});
-            const int tr = 4 * kg + ((lane >> 2) & 3);
-            const int to = tr * AT_PR + at_col(tr, 4 * (lane & 3));
-            // the transposed reads run AT_UPF channel tiles ahead of the MFMAs that use them
-            s16x4 rh[AT_UPF], rl[AT_UPF];
 #pragma unroll
-            for (int j = 0; j < AT_UPF; j++) {
-                rh[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(hi + to + 16 * j));
-                rl[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(lo + to + 16 * j));
+            for (int g2 = 0; g2 < 4; g2++) {
+                const bool hg = 16 * g2 < H;   // head tiles without heads: weight zero
+                al0[g2] = hg ? a[g2] : 1.0f;
+                if (!(kg >> 1)) {
+                    pa[g2] = hg ? xa[g2] : uint4{0, 0, 0, 0};
+                    pb[g2] = hg ? xb[g2] : uint4{0, 0, 0, 0};
+                }
+            }
+        };
+        // tiles t0, t0 + 1 (the second may lie past the last tile: weight zero)
+        auto u_pair = [&](int t0) {
+            const int t1 = t0 + 1;
+            const bool has1 = t1 < ntile;
+            float a[4];
+            uint4 xa[4], xb[4];
+#pragma unroll
+            for (int g2 = 0; g2 < 4; g2++) {
+                a[g2] = alpha_of(t1, g2);
+                xa[g2] = p_entry(t1, g2, src0);
+                xb[g2] = p_entry(t1, g2, src1);
+            }
+            bf16x8 ph[4], pq[4];
+#pragma unroll
+            for (int g2 = 0; g2 < 4; g2++) {
+                const bool hg = 16 * g2 < H, use1 = has1 && hg;
+                const float al1 = use1 ? a[g2] : 1.0f;
+                if (kg >> 1) {
+                    pa[g2] = use1 ? xa[g2] : uint4{0, 0, 0, 0};
+                    pb[g2] = use1 ? xb[g2] : uint4{0, 0, 0, 0};
+                } else if (__ballot(al1 != 1.0f)) {
+                    // acc a0 a1 + X0 (P0 a1) + X1 P1 = ((acc a0 + X0 P0) a1 + X1 P1)
+                    float pv[8];
+                    const uint32_t wh[4] = {pa[g2].x, pa[g2].y, pb[g2].x, pb[g2].y};
+                    const uint32_t wl[4] = {pa[g2].z, pa[g2].w, pb[g2].z, pb[g2].w};
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        pv[2 * e] = (__uint_as_float(wh[e] << 16) + __uint_as_float(wl[e] << 16)) * al1;
+                        pv[2 * e + 1] = (__uint_as_float(wh[e] & 0xffff0000u) + __uint_as_float(wl[e] & 0xffff0000u)) * al1;
+                    }
+                    bf16x2 hh[4], ll[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) split2(pv[2 * e], pv[2 * e + 1], hh[e], ll[e]);
+                    pa[g2] = uint4{__builtin_bit_cast(uint32_t, hh[0]), __builtin_bit_cast(uint32_t, hh[1]),
+                                   __builtin_bit_cast(uint32_t, ll[0]), __builtin_bit_cast(uint32_t, ll[1])};
+                    pb[g2] = uint4{__builtin_bit_cast(uint32_t, hh[2]), __builtin_bit_cast(uint32_t, hh[3]),
+                                   __builtin_bit_cast(uint32_t, ll[2]), __builtin_bit_cast(uint32_t, ll[3])};
+                }
+                const float sc = al0[g2] * al1;
+                if (__ballot(sc != 1.0f)) {
+#pragma unroll
+                    for (int jj = 0; jj < AT_UCT; jj++) acc[jj][g2] *= sc;
+                }
+                ph[g2] = __builtin_bit_cast(bf16x8, uint4{pa[g2].x, pa[g2].y, pb[g2].x, pb[g2].y});
+                pq[g2] = __builtin_bit_cast(bf16x8, uint4{pa[g2].z, pa[g2].w, pb[g2].z, pb[g2].w});
+            }
+            const int buf = (t0 + (kg >> 1)) % AT_NB;
+            const uint16_t *hi = at_smem + (size_t)(2 * buf) * AT_PLANE + 16 * AT_UCT * u, *lo = hi + AT_PLANE;
+            const int tr0 = 4 * (kg & 1) + ((lane >> 2) & 3), tr1 = tr0 + 8;
+            const int to0 = tr0 * AT_PR + at_col(tr0, 4 * (lane & 3)), to1 = tr1 * AT_PR + at_col(tr1, 4 * (lane & 3));
+            auto rd = [&](const uint16_t *pl, int jj) {
+                const s16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(pl + to0 + 16 * jj));
+                const s16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(pl + to1 + 16 * jj));
+                return __builtin_bit_cast(bf16x8, uint4{__builtin_bit_cast(uint2, x0).x, __builtin_bit_cast(uint2, x0).y,
+                                                        __builtin_bit_cast(uint2, x1).x, __builtin_bit_cast(uint2, x1).y});
+            };
+            // per channel tile: each of the three split products over the four head tiles (four
+            // independent chains hide the ~40-cycle latency of a dependent MFMA); the latent
+            // fragments are read AT_UPF channel tiles ahead
+            bf16x8 rh[AT_UPF], rl[AT_UPF];
+#pragma unroll
+            for (int jj = 0; jj < AT_UPF; jj++) {
+                rl[jj] = rd(lo, jj);
+                rh[jj] = rd(hi, jj);
             }
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int j = 0; j < AT_MAXCT; j++) {
-                const s16x4 ah = rh[j % AT_UPF], al = rl[j % AT_UPF];
-                if (j + AT_UPF < AT_MAXCT) {
-                    rh[j % AT_UPF] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(hi + to + 16 * (j + AT_UPF)));
-                    rl[j % AT_UPF] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(lo + to + 16 * (j + AT_UPF)));
+            for (int jj = 0; jj < AT_UCT; jj++) {
+                const bf16x8 ah = rh[jj % AT_UPF], al = rl[jj % AT_UPF];
+#pragma unroll
+                for (int g2 = 0; g2 < 4; g2++)
+                    acc[jj][g2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, ph[g2], acc[jj][g2], 0, 0, 0);
+#pragma unroll
+                for (int g2 = 0; g2 < 4; g2++)
+                    acc[jj][g2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, pq[g2], acc[jj][g2], 0, 0, 0);
+#pragma unroll
+                for (int g2 = 0; g2 < 4; g2++)
+                    acc[jj][g2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, ph[g2], acc[jj][g2], 0, 0, 0);
+                if (jj + AT_UPF < AT_UCT) {
+                    rl[jj % AT_UPF] = rd(lo, jj + AT_UPF);
+                    rh[jj % AT_UPF] = rd(hi, jj + AT_UPF);
                 }
-                acc[j] = mma3_16(acc[j], ah, al, ph, pq);
                 __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead (the scheduler sinks them)
             }
         };
-        for (int it = 0; it <= ntile; it++) {
-            if (act && it > 0) u_tile(it - 1);
-            stage((it + 2) % AT_NB);
-            load_tile(it + 3);
+        const bool uact = 16 * AT_UCT * u < KL;   // wave-uniform: this wave has latent channels
+        for (int it = 0; it <= itend; it++) {
+            if (uact && (it & 1)) u_grab(it - 1);
+            if (uact && it >= 2 && !(it & 1)) u_pair(it - 2);
+            stage((it + 1) % AT_NB);
+            load_tile(it + 2);
             __syncthreads();
         }
-        if (act && h < H) {
-            float *outp = pctx + (((size_t)b * nsplit + sp) * H + h) * KL + 4 * kg;
+        if (uact) {
 #pragma unroll
-            for (int j = 0; j < AT_MAXCT; j++)
-                if (16 * j < KL) *reinterpret_cast<f4 *>(outp + 16 * j) = f4{acc[j][0], acc[j][1], acc[j][2], acc[j][3]};
+            for (int g2 = 0; g2 < 4; g2++) {
+                const int hh = 16 * g2 + m;
+                if (hh >= H) continue;
+                float *outp = pctx + (((size_t)b * nsplit + sp) * H + hh) * KL + 4 * kg;
+#pragma unroll
+                for (int jj = 0; jj < AT_UCT; jj++) {
+                    const int j = AT_UCT * u + jj;
+                    if (16 * j < KL)
+                        *reinterpret_cast<f4 *>(outp + 16 * j) = f4{acc[jj][g2][0], acc[jj][g2][1], acc[jj][g2][2], acc[jj][g2][3]};
+                }
+            }
         }
     }
 }
