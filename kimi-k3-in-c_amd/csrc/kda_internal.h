@@ -94,6 +94,11 @@ int rows_frag_pack(const uint16_t *W, int N, int K, uint16_t *Wf, hipStream_t st
 size_t gemm_rows_ws_floats(int B, int N, int K);
 int gemm_rows(int B, int N, int K, const float *x, long ldx, const uint16_t *Wf, float *C, long ldc,
               hipStream_t st, float *ws = nullptr, size_t ws_floats = 0, bool c_zeroed = false);
+// gemm_rows with C also written as bf16 hi (rows 0 .. B-1) and lo (rows B .. 2B-1) rows of
+// hl (row stride ldhl; hi = bf16(c), lo = bf16(c - hi), the bits of split_rows2 on C), in the
+// same launch when the product runs unsplit (otherwise split_rows2 after it, ldc = ldhl = N).
+int gemm_rows_hl(int B, int N, int K, const float *x, long ldx, const uint16_t *Wf, float *C, long ldc,
+                 uint16_t *hl, long ldhl, hipStream_t st, float *ws = nullptr, size_t ws_floats = 0);
 // The same product left as its S = gemm_rows_splits(N, K) K-range partials: planes
 // P[s][B][N], whose sum in increasing s is C bit for bit, for a consumer that adds them
 // itself instead of a reduction launch.

@@ -340,10 +340,11 @@ extern "C" int k3hip_mla_decode(const k3hip_mla_weights *w, int B, int pos, int 
                        NormJob{C1, QL, QL, w->q_a_norm, qn, nullptr},
                        NormJob{C1 + QL, CW, KL, w->kv_a_norm, nullptr, cache}, (long)cap, pos);
     K3_LAUNCHED();
-    if ((rc = gemm_rows(B, H * QH, QL, qn, QL, (const uint16_t *)w->q_b, q, (long)H * QH, st, ws, wsf)))
+    // q, and q as bf16 hi / lo rows for the absorb GEMM, from one launch
+    if ((rc = gemm_rows_hl(B, H * QH, QL, qn, QL, (const uint16_t *)w->q_b, q, (long)H * QH, qs2, (long)H * QH, st,
+                           ws, wsf)))
         return rc;
     // absorb: per head h, [q hi; lo] (2B x QN) . W_UK_h (QN x KL), batched over heads
-    if ((rc = split_rows2(q, qs2, B, H * QH, st))) return rc;
     GemmDesc ga;
     ga.M = 2 * B; ga.N = KL; ga.K = QN; ga.ab_dtype = K3HIP_BF16; ga.c_dtype = K3HIP_F32; ga.b_trans = false;
     ga.lda = (long)H * QH; ga.ldb = KL; ga.ldc = (long)H * CW; ga.batch = H;

@@ -69,6 +69,10 @@ struct RowsJob {
     const uint16_t *Wf;
     float *P;
     long ldp, split_stride;
+    // unsplit products only: C also as bf16 hi (row m) and lo (plane hlplane on) rows of
+    // stride ldhl, x = hi + lo, for a following GEMM on split rows (nullptr: none)
+    uint16_t *hl = nullptr;
+    long ldhl = 0, hlplane = 0;
 };
 
 // Block (nb, s) of a job: column groups 4 nb .. 4 nb + 3, K-steps [s tchunk, min(KT, (s + 1)
@@ -158,8 +162,16 @@ __global__ __launch_bounds__(64 * RT_WAVES) void rows_gemm_kernel(int B, int K, 
         for (int e = 0; e < 4; e++) {
             const int m = 16 * mt + 4 * kg + e;   // MFMA C layout: lane n + 16 j holds rows 4j..4j+3
             if (m < B && n < N) {
-                if constexpr (ATOM) unsafeAtomicAdd(&out[(size_t)m * ldp + n], t[e]);
-                else out[(size_t)m * ldp + n] = t[e];
+                if constexpr (ATOM) {
+                    unsafeAtomicAdd(&out[(size_t)m * ldp + n], t[e]);
+                } else {
+                    out[(size_t)m * ldp + n] = t[e];
+                    if (jb.hl) {
+                        const uint16_t hi = f2bf(t[e]);
+                        jb.hl[(size_t)m * jb.ldhl + n] = hi;
+                        jb.hl[(size_t)jb.hlplane + (size_t)m * jb.ldhl + n] = f2bf(t[e] - __uint_as_float((uint32_t)hi << 16));
+                    }
+                }
             }
         }
     }
@@ -340,6 +352,32 @@ int gemm_rows_with_part(int B, int K, const float *x, long ldx, int N1, const ui
         const RowsJob j0 = rows_job(N1, p1.tchunk, 1, Wf1, C1 + (size_t)b0 * ldc1, ldc1, 0);
         const RowsJob j1 = rows_job(N2, p2.tchunk, p2.S, Wf2, P2 + (size_t)b0 * N2, N2, plane);
         int rc = launch_jobs_b(bb, K, x + (size_t)b0 * ldx, ldx, j0, j1, st);
+        if (rc) return rc;
+    }
+    return K3HIP_OK;
+}
+
+int gemm_rows_hl(int B, int N, int K, const float *x, long ldx, const uint16_t *Wf, float *C, long ldc,
+                 uint16_t *hl, long ldhl, hipStream_t st, float *ws, size_t ws_floats)
+{
+    if (B <= 0 || N <= 0 || K <= 0) return K3HIP_OK;
+    const RowsPlan pl = rows_plan(N, K);
+    if (pl.S != 1) {   // the split rows from the reduced product
+        int rc = gemm_rows(B, N, K, x, ldx, Wf, C, ldc, st, ws, ws_floats);
+        if (rc) return rc;
+        if (ldhl != N || ldc != N) K3_FAIL(K3HIP_EINVAL, "gemm_rows_hl: a split-K product needs ldc = ldhl = N");
+        return split_rows2(C, hl, B, N, st);
+    }
+    if ((K & 7) || (ldx & 3) || (((uintptr_t)x | (uintptr_t)Wf) & 15))
+        K3_FAIL(K3HIP_EINVAL, "gemm_rows_hl: K=%d ldx=%ld need multiples of 8 / 4 and 16-byte aligned x, W", K, ldx);
+    const RowsJob none{1, 1, 0, 1, Wf, C, 0, 0};   // no blocks
+    for (int b0 = 0; b0 < B; b0 += 64) {
+        const int bb = std::min(64, B - b0);
+        RowsJob j = rows_job(N, pl.tchunk, 1, Wf, C + (size_t)b0 * ldc, ldc, 0);
+        j.hl = hl + (size_t)b0 * ldhl;
+        j.ldhl = ldhl;
+        j.hlplane = (long)B * ldhl;
+        int rc = launch_jobs_b(bb, K, x + (size_t)b0 * ldx, ldx, j, none, st);
         if (rc) return rc;
     }
     return K3HIP_OK;
