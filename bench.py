@@ -988,7 +988,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build measures one GPU only; run with --gpus 1", file=sys.stderr)
+        print("bench.py: the benchmark runs on one GPU (the path is measured per GPU); run with --gpus 1", file=sys.stderr)
         return 2
     import torch
     import k3kda as k3

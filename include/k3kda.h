@@ -129,7 +129,7 @@ enum { K3HIP_F32 = 0, K3HIP_BF16 = 1 };
 /* Message for the last non-zero return on the calling thread ("" when none). */
 const char *k3hip_last_error(void);
 
-/* Version string of this build (kernel set and target). */
+/* Version string of the library (kernel set and target). */
 const char *k3hip_version(void);
 
 /* Number of HIP devices visible (0 on a machine without one); never aborts. */

@@ -1,8 +1,8 @@
 /* SPDX-License-Identifier: Apache-2.0 */
 /*
  * k3_oracle.c - CPU restatement of the reference KDA path. TEST INFRASTRUCTURE ONLY:
- * the checker for the HIP kernels and the CPU baseline of bench.py. The shipped library
- * never links it.
+ * the oracle the HIP kernels are tested against, and the CPU baseline of bench.py. The
+ * shipped library never links it.
  *
  * Build contract (same as the reference, src/core/k3_ops.c:8-10, Makefile:133-140):
  * -ffp-contract=off, no -ffast-math. Double accumulators exactly where the reference

@@ -2,7 +2,7 @@
 /*
  * k3_oracle.h - CPU restatement of the reference KDA path. TEST INFRASTRUCTURE ONLY.
  *
- * This library is the checker the GPU kernels are compared against, and the CPU
+ * This library is the oracle the GPU kernels are compared against, and the CPU
  * baseline that bench.py times beside them. Nothing in the shipped library links or
  * calls it. Every function names the reference lines (kimi-k3-in-c, src/core/k3_ops.c
  * unless stated) whose arithmetic it restates, including accumulation width and
