@@ -97,8 +97,11 @@ int gemm_rows(int B, int N, int K, const float *x, long ldx, const uint16_t *Wf,
 // gemm_rows with C also written as bf16 hi (rows 0 .. B-1) and lo (rows B .. 2B-1) rows of
 // hl (row stride ldhl; hi = bf16(c), lo = bf16(c - hi), the bits of split_rows2 on C), in the
 // same launch when the product runs unsplit (otherwise split_rows2 after it, ldc = ldhl = N).
+// xw != nullptr (unsplit products only, gemm_rows_splits(N, K) == 1): the x rows are
+// RMS-normalised with weight xw and eps xeps on the way in (the rmsnorm of k3_ops.c:94-102).
 int gemm_rows_hl(int B, int N, int K, const float *x, long ldx, const uint16_t *Wf, float *C, long ldc,
-                 uint16_t *hl, long ldhl, hipStream_t st, float *ws = nullptr, size_t ws_floats = 0);
+                 uint16_t *hl, long ldhl, hipStream_t st, float *ws = nullptr, size_t ws_floats = 0,
+                 const float *xw = nullptr, float xeps = 0.0f);
 // The same product left as its S = gemm_rows_splits(N, K) K-range partials: planes
 // P[s][B][N], whose sum in increasing s is C bit for bit, for a consumer that adds them
 // itself instead of a reduction launch.
@@ -126,9 +129,13 @@ int gemm_rows_with_part(int B, int K, const float *x, long ldx, int N1, const ui
 // cache and kvb 16-byte aligned.
 bool mla_attention_supported(int H, int KL, int CW);
 size_t mla_attention_ws_bytes(int B, int H, int KL, int Tn);
+// lat != nullptr: position Tn - 1's cache row is written first from row b of lat (stride
+// ldlat): the first KL floats rmsnorm'd with weight lat_w and eps lat_eps, the rope slot
+// copied (the norm launch before the attention otherwise writes it).
 int mla_attention(int B, int H, int KL, int CW, int Tn, int cap, float scale, const float *A2, const float *q,
-                  int QN, const float *cache, const uint16_t *kvb, int VH, const float *g, long ldg, float *o,
-                  float *zout, size_t zn, uint16_t *ch2, void *ws, size_t ws_bytes, hipStream_t st);
+                  int QN, float *cache, const float *lat, long ldlat, const float *lat_w, float lat_eps,
+                  const uint16_t *kvb, int VH, const float *g, long ldg, float *o, float *zout, size_t zn,
+                  uint16_t *ch2, void *ws, size_t ws_bytes, hipStream_t st);
 
 // One decode token of a KDA layer between its projections (kda_step.hip): K1 + K3 + K4 per
 // (head, sequence). Cin rows (stride ldc) hold q | k | v at columns 0, P, 2P and the beta

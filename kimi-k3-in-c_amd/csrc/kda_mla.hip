@@ -335,15 +335,24 @@ extern "C" int k3hip_mla_decode(const k3hip_mla_weights *w, int B, int pos, int 
     // q_a, kv_a and g in one pass over their weights (fp32 x split hi/lo in registers);
     // q = q_b(rmsnorm(q_a x)); latent + rope = kv_a x, the latent rmsnorm'd into the cache
     if ((rc = gemm_rows(B, N1, E, x, E, (const uint16_t *)w->xin, C1, ld1, st, ws, wsf))) return rc;
-    // the q_a rmsnorm into qn and the latent rmsnorm into the cache, one launch
-    hipLaunchKernelGGL(mla_norm_kernel, dim3(B, 2), dim3(256), 0, st, ld1, w->eps,
-                       NormJob{C1, QL, QL, w->q_a_norm, qn, nullptr},
-                       NormJob{C1 + QL, CW, KL, w->kv_a_norm, nullptr, cache}, (long)cap, pos);
-    K3_LAUNCHED();
+    // the two rmsnorms: with the fused attention and an unsplit q_b product, the q_b GEMV
+    // normalises q_a as it reads it and the attention writes the new latent row itself;
+    // otherwise one launch writes qn and the cache row
+    const bool fold_norms = fused && gemm_rows_splits(H * QH, QL) == 1 && !((uintptr_t)w->q_a_norm & 15);
+    if (!fold_norms) {
+        hipLaunchKernelGGL(mla_norm_kernel, dim3(B, 2), dim3(256), 0, st, ld1, w->eps,
+                           NormJob{C1, QL, QL, w->q_a_norm, qn, nullptr},
+                           NormJob{C1 + QL, CW, KL, w->kv_a_norm, nullptr, cache}, (long)cap, pos);
+        K3_LAUNCHED();
+    }
     // q, and q as bf16 hi / lo rows for the absorb GEMM, from one launch
-    if ((rc = gemm_rows_hl(B, H * QH, QL, qn, QL, (const uint16_t *)w->q_b, q, (long)H * QH, qs2, (long)H * QH, st,
-                           ws, wsf)))
-        return rc;
+    if (fold_norms)
+        rc = gemm_rows_hl(B, H * QH, QL, C1, ld1, (const uint16_t *)w->q_b, q, (long)H * QH, qs2, (long)H * QH, st, ws,
+                          wsf, w->q_a_norm, w->eps);
+    else
+        rc = gemm_rows_hl(B, H * QH, QL, qn, QL, (const uint16_t *)w->q_b, q, (long)H * QH, qs2, (long)H * QH, st, ws,
+                          wsf);
+    if (rc) return rc;
     // absorb: per head h, [q hi; lo] (2B x QN) . W_UK_h (QN x KL), batched over heads
     GemmDesc ga;
     ga.M = 2 * B; ga.N = KL; ga.K = QN; ga.ab_dtype = K3HIP_BF16; ga.c_dtype = K3HIP_F32; ga.b_trans = false;
@@ -357,7 +366,8 @@ extern "C" int k3hip_mla_decode(const k3hip_mla_weights *w, int B, int pos, int 
     if (fused) {
         // the query rows formed inside the attention from A2 and q; the ranges merged, W_UV and
         // the output gate applied in the launch after it (kda_mla_attn.hip)
-        if ((rc = mla_attention(B, H, KL, CW, Tn, cap, 1.0f / sqrtf((float)QH), A2, q, QN, cache, kvb, VH, gl, ld1,
+        if ((rc = mla_attention(B, H, KL, CW, Tn, cap, 1.0f / sqrtf((float)QH), A2, q, QN, cache,
+                                fold_norms ? C1 + QL : nullptr, ld1, w->kv_a_norm, w->eps, kvb, VH, gl, ld1,
                                 o, oz ? out : nullptr, oz ? (size_t)B * E : (size_t)0, ch2, S,
                                 mla_attention_ws_bytes(B, H, KL, Tn), st)))
             return rc;

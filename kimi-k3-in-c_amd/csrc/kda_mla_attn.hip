@@ -91,6 +91,18 @@ struct AtQ {
     int B, QN, QH;
 };
 
+// The new position's cache row, written by the workgroup that owns the last range before it
+// reads any cache row: the rmsnorm'd latent (weight w, double mean of squares,
+// src/core/k3_ops.c:94-102) and the rope slot copied, from row b of src (stride ld). src ==
+// nullptr: the row is already in the cache.
+struct AtRow {
+    const float *src;
+    long ld;
+    const float *w;
+    float eps;
+    int pos;
+};
+
 __device__ __forceinline__ void split2(float a, float b, bf16x2 &hi, bf16x2 &lo)
 {
     hi = __builtin_convertvector(f2{a, b}, bf16x2);
@@ -105,8 +117,8 @@ __device__ __forceinline__ void split2(float a, float b, bf16x2 &hi, bf16x2 &lo)
 // w - 4, all head tiles). FULL: kv_lora + rope = 576, every staging unit of a row exists.
 template <bool FULL>
 __global__ __launch_bounds__(AT_NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void mla_attn_kernel(
-    AtGeom g, int Tn, int cap, int nsplit, float scale2, AtQ qs,
-    const float *__restrict__ cache, float *__restrict__ pctx, float *__restrict__ pm, float *__restrict__ pl)
+    AtGeom g, int Tn, int cap, int nsplit, float scale2, AtQ qs, AtRow nr,
+    float *__restrict__ cache, float *__restrict__ pctx, float *__restrict__ pm, float *__restrict__ pl)
 {
     extern __shared__ __attribute__((aligned(16))) uint16_t at_smem[];
     char *sbase = reinterpret_cast<char *>(at_smem);
@@ -120,6 +132,32 @@ __global__ __launch_bounds__(AT_NT) __attribute__((amdgpu_waves_per_eu(2, 2))) v
     const int h = 16 * ht + m;
     const bool act = 16 * ht < H;   // wave-uniform: this wave has heads
 
+    if (nr.src && sp == nsplit - 1) {   // the new position (Tn - 1 = pos) lies in this range
+        const float *src = nr.src + (size_t)b * nr.ld;
+        double ss = 0.0;
+        for (int n = tid; n < KL; n += AT_NT) {
+            const double v = (double)src[n];
+            ss += v * v;
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        double *red = reinterpret_cast<double *>(at_smem);
+        if (lane == 0) red[w] = ss;
+        __syncthreads();
+        ss = 0.0;
+#pragma unroll
+        for (int i = 0; i < AT_NT / 64; i++) ss += red[i];
+        const float inv = (float)(1.0 / sqrt(ss / (double)KL + (double)nr.eps));
+        float *dst = cache + ((size_t)b * cap + nr.pos) * CW;
+        for (int n = tid; n < CW; n += AT_NT) {
+            const float v = src[n];
+            dst[n] = n < KL ? (nr.w[n] * v) * inv : v;
+        }
+        // the row is read back only by this workgroup's own cache loads (which go to L2: no
+        // line of it was loaded here before): its stores complete, then every wave goes on
+        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+        __syncthreads();
+    }
     if (!FULL) {
         const int padw = 32 * AT_MAXKS - CW;
         for (int i = tid; i < 2 * AT_NB * AT_T * padw; i += AT_NT) {
@@ -613,8 +651,9 @@ bool mla_attention_supported(int H, int KL, int CW)
 }
 
 int mla_attention(int B, int H, int KL, int CW, int Tn, int cap, float scale, const float *A2, const float *q,
-                  int QN, const float *cache, const uint16_t *kvb, int VH, const float *gate, long ldg, float *o,
-                  float *zout, size_t zn, uint16_t *ch2, void *ws, size_t ws_bytes, hipStream_t st)
+                  int QN, float *cache, const float *lat, long ldlat, const float *lat_w, float lat_eps,
+                  const uint16_t *kvb, int VH, const float *gate, long ldg, float *o, float *zout, size_t zn,
+                  uint16_t *ch2, void *ws, size_t ws_bytes, hipStream_t st)
 {
     AtGeom g;
     if (!at_geom(H, KL, CW, g))
@@ -628,6 +667,7 @@ int mla_attention(int B, int H, int KL, int CW, int Tn, int cap, float scale, co
         VH < 1 || VH > 16 * (AO_NT / 64))
         K3_FAIL(K3HIP_EINVAL, "mla attention: workspace %zu < %zu bytes, or a misaligned buffer", ws_bytes, need);
     const AtQ qs{A2, q, B, QN, QH};
+    const AtRow nr{lat, ldlat, lat_w, lat_eps, Tn - 1};
     const size_t r = (size_t)B * nsplit * H;
     float *pctx = (float *)ws;
     float *pm = (float *)((char *)ws + ((r * KL * 4 + 255) & ~(size_t)255));
@@ -642,10 +682,10 @@ int mla_attention(int B, int H, int KL, int CW, int Tn, int cap, float scale, co
     }
     if (CW == 32 * AT_MAXKS)
         hipLaunchKernelGGL(mla_attn_kernel<true>, dim3(nsplit, B), dim3(AT_NT), AT_LDS, st, g, Tn, cap, nsplit,
-                           scale * AT_LOG2E, qs, cache, pctx, pm, pl);
+                           scale * AT_LOG2E, qs, nr, cache, pctx, pm, pl);
     else
         hipLaunchKernelGGL(mla_attn_kernel<false>, dim3(nsplit, B), dim3(AT_NT), AT_LDS, st, g, Tn, cap, nsplit,
-                           scale * AT_LOG2E, qs, cache, pctx, pm, pl);
+                           scale * AT_LOG2E, qs, nr, cache, pctx, pm, pl);
     K3_LAUNCHED();
     hipLaunchKernelGGL(mla_attn_merge_kernel, dim3(H, B), dim3(128), 0, st, B, H, KL, nsplit, pctx, pm, pl, ch2);
     K3_LAUNCHED();

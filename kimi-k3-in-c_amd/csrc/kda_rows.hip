@@ -81,10 +81,15 @@ struct RowsJob {
 // 8, ...; each step loads the 4 groups' fragments (4 x 1 KB) and the x slice, then runs the
 // hi and lo MFMAs.
 template <int MT, bool ATOM>
+// xw != nullptr: each x row is RMS-normalised on the way in, x'[k] = (xw[k] x[k]) inv with
+// inv = 1 / sqrt(mean_k x^2 + xeps) (mean in double; src/core/k3_ops.c:94-102), so a
+// normalised input needs no launch of its own.
 __global__ __launch_bounds__(64 * RT_WAVES) void rows_gemm_kernel(int B, int K, const float *__restrict__ x,
-                                                                  long ldx, RowsJob j0, RowsJob j1)
+                                                                  long ldx, RowsJob j0, RowsJob j1,
+                                                                  const float *__restrict__ xw, float xeps)
 {
     __shared__ f32x4 red[RT_WAVES][RT_NT][MT][64];
+    __shared__ float xinv[16 * MT];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int r16 = lane & 15, kg = lane >> 4;
     const int n0 = j0.nb * j0.S;
@@ -113,6 +118,33 @@ __global__ __launch_bounds__(64 * RT_WAVES) void rows_gemm_kernel(int B, int K, 
         xrow[mt] = x + (size_t)min(16 * mt + r16, B - 1) * ldx;
     }
 
+    if (xw) {   // the rows' inverse RMS: 32 lanes per row, 16 rows per pass
+        for (int rr0 = 0; rr0 < 16 * MT; rr0 += 16) {
+            const int rr = rr0 + ((int)threadIdx.x >> 5), ln = threadIdx.x & 31;
+            double ss = 0.0;
+            if (rr < B) {
+                // eight loads in flight per step
+                const float *xr = x + (size_t)rr * ldx;
+                int k = ln;
+                for (; k + 7 * 32 < K; k += 8 * 32) {
+                    float v[8];
+#pragma unroll
+                    for (int u = 0; u < 8; u++) v[u] = xr[k + 32 * u];
+#pragma unroll
+                    for (int u = 0; u < 8; u++) ss += (double)v[u] * (double)v[u];
+                }
+                for (; k < K; k += 32) ss += (double)xr[k] * (double)xr[k];
+            }
+#pragma unroll
+            for (int o = 16; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 32);
+            if (ln == 0) xinv[rr] = rr < B ? (float)(1.0 / sqrt(ss / (double)K + (double)xeps)) : 0.0f;
+        }
+        __syncthreads();
+    }
+    float xiv[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) xiv[mt] = xw ? xinv[16 * mt + r16] : 1.0f;
+
     f32x4 acc[RT_NT][MT];
 #pragma unroll
     for (int j = 0; j < RT_NT; j++)
@@ -130,6 +162,15 @@ __global__ __launch_bounds__(64 * RT_WAVES) void rows_gemm_kernel(int B, int K, 
         for (int mt = 0; mt < MT; mt++) {
             xa[mt] = *reinterpret_cast<const f4 *>(xrow[mt] + (kin ? k : 0));
             xb[mt] = *reinterpret_cast<const f4 *>(xrow[mt] + (kin ? k : 0) + 4);
+        }
+        if (xw) {
+            const f4 wa = *reinterpret_cast<const f4 *>(xw + (kin ? k : 0));
+            const f4 wb = *reinterpret_cast<const f4 *>(xw + (kin ? k : 0) + 4);
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                xa[mt] = (wa * xa[mt]) * xiv[mt];
+                xb[mt] = (wb * xb[mt]) * xiv[mt];
+            }
         }
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
@@ -219,11 +260,12 @@ RowsJob rows_job(int N, int tchunk, int S, const uint16_t *Wf, float *P, long ld
 }
 
 template <int MT, bool ATOM = false>
-int launch_jobs(int B, int K, const float *x, long ldx, const RowsJob &j0, const RowsJob &j1, hipStream_t st)
+int launch_jobs(int B, int K, const float *x, long ldx, const RowsJob &j0, const RowsJob &j1, hipStream_t st,
+                const float *xw = nullptr, float xeps = 0.0f)
 {
     const long nblk = (long)j0.nb * j0.S + (long)j1.nb * j1.S;
     hipLaunchKernelGGL((rows_gemm_kernel<MT, ATOM>), dim3((unsigned)nblk), dim3(64 * RT_WAVES), 0, st, B, K, x,
-                       ldx, j0, j1);
+                       ldx, j0, j1, xw, xeps);
     K3_LAUNCHED();
     return K3HIP_OK;
 }
@@ -237,11 +279,12 @@ int launch_rows(int B, int N, int K, int tchunk, int S, const float *x, long ldx
 }
 
 // rows for one launch of up to 64 rows (MT = 1, 2 or 4 16-row tiles)
-int launch_jobs_b(int bb, int K, const float *x, long ldx, const RowsJob &j0, const RowsJob &j1, hipStream_t st)
+int launch_jobs_b(int bb, int K, const float *x, long ldx, const RowsJob &j0, const RowsJob &j1, hipStream_t st,
+                  const float *xw = nullptr, float xeps = 0.0f)
 {
-    if (bb <= 16) return launch_jobs<1>(bb, K, x, ldx, j0, j1, st);
-    if (bb <= 32) return launch_jobs<2>(bb, K, x, ldx, j0, j1, st);
-    return launch_jobs<4>(bb, K, x, ldx, j0, j1, st);
+    if (bb <= 16) return launch_jobs<1>(bb, K, x, ldx, j0, j1, st, xw, xeps);
+    if (bb <= 32) return launch_jobs<2>(bb, K, x, ldx, j0, j1, st, xw, xeps);
+    return launch_jobs<4>(bb, K, x, ldx, j0, j1, st, xw, xeps);
 }
 
 int cu_total()
@@ -358,10 +401,12 @@ int gemm_rows_with_part(int B, int K, const float *x, long ldx, int N1, const ui
 }
 
 int gemm_rows_hl(int B, int N, int K, const float *x, long ldx, const uint16_t *Wf, float *C, long ldc,
-                 uint16_t *hl, long ldhl, hipStream_t st, float *ws, size_t ws_floats)
+                 uint16_t *hl, long ldhl, hipStream_t st, float *ws, size_t ws_floats, const float *xw, float xeps)
 {
     if (B <= 0 || N <= 0 || K <= 0) return K3HIP_OK;
     const RowsPlan pl = rows_plan(N, K);
+    if (xw && (pl.S != 1 || (((uintptr_t)xw) & 15)))
+        K3_FAIL(K3HIP_EUNSUPPORTED, "gemm_rows_hl: the normalised input needs an unsplit product and 16-byte aligned weights");
     if (pl.S != 1) {   // the split rows from the reduced product
         int rc = gemm_rows(B, N, K, x, ldx, Wf, C, ldc, st, ws, ws_floats);
         if (rc) return rc;
@@ -377,7 +422,7 @@ int gemm_rows_hl(int B, int N, int K, const float *x, long ldx, const uint16_t *
         j.hl = hl + (size_t)b0 * ldhl;
         j.ldhl = ldhl;
         j.hlplane = (long)B * ldhl;
-        int rc = launch_jobs_b(bb, K, x + (size_t)b0 * ldx, ldx, j, none, st);
+        int rc = launch_jobs_b(bb, K, x + (size_t)b0 * ldx, ldx, j, none, st, xw, xeps);
         if (rc) return rc;
     }
     return K3HIP_OK;
