@@ -132,32 +132,6 @@ __global__ __launch_bounds__(AT_NT) __attribute__((amdgpu_waves_per_eu(2, 2))) v
     const int h = 16 * ht + m;
     const bool act = 16 * ht < H;   // wave-uniform: this wave has heads
 
-    if (nr.src && sp == nsplit - 1) {   // the new position (Tn - 1 = pos) lies in this range
-        const float *src = nr.src + (size_t)b * nr.ld;
-        double ss = 0.0;
-        for (int n = tid; n < KL; n += AT_NT) {
-            const double v = (double)src[n];
-            ss += v * v;
-        }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
-        double *red = reinterpret_cast<double *>(at_smem);
-        if (lane == 0) red[w] = ss;
-        __syncthreads();
-        ss = 0.0;
-#pragma unroll
-        for (int i = 0; i < AT_NT / 64; i++) ss += red[i];
-        const float inv = (float)(1.0 / sqrt(ss / (double)KL + (double)nr.eps));
-        float *dst = cache + ((size_t)b * cap + nr.pos) * CW;
-        for (int n = tid; n < CW; n += AT_NT) {
-            const float v = src[n];
-            dst[n] = n < KL ? (nr.w[n] * v) * inv : v;
-        }
-        // the row is read back only by this workgroup's own cache loads (which go to L2: no
-        // line of it was loaded here before): its stores complete, then every wave goes on
-        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
-        __syncthreads();
-    }
     if (!FULL) {
         const int padw = 32 * AT_MAXKS - CW;
         for (int i = tid; i < 2 * AT_NB * AT_T * padw; i += AT_NT) {
@@ -191,16 +165,46 @@ __global__ __launch_bounds__(AT_NT) __attribute__((amdgpu_waves_per_eu(2, 2))) v
             }
     };
 
-    load_tile(0);
+    // the workgroup of the last range writes the new position's row (Tn - 1 = pos) first;
+    // tile 0 goes out before that unless it is the tile that holds the row
+    const bool own_row = nr.src && sp == nsplit - 1;
+    if (!own_row || ntile > 1) load_tile(0);
+    if (own_row) {
+        const float *src = nr.src + (size_t)b * nr.ld;
+        double ss = 0.0;
+        for (int n = tid; n < KL; n += AT_NT) {
+            const double v = (double)src[n];
+            ss += v * v;
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        double *red = reinterpret_cast<double *>(at_smem);
+        if (lane == 0) red[w] = ss;
+        __syncthreads();
+        ss = 0.0;
+#pragma unroll
+        for (int i = 0; i < AT_NT / 64; i++) ss += red[i];
+        const float inv = (float)(1.0 / sqrt(ss / (double)KL + (double)nr.eps));
+        float *dst = cache + ((size_t)b * cap + nr.pos) * CW;
+        for (int n = tid; n < CW; n += AT_NT) {
+            const float v = src[n];
+            dst[n] = n < KL ? (nr.w[n] * v) * inv : v;
+        }
+        // the row is read back only by this workgroup's own cache loads (which go to L2: no
+        // line of it was loaded here before): its stores complete, then every wave goes on
+        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+        __syncthreads();
+    }
+    if (own_row && ntile <= 1) load_tile(0);
     stage(0);
     load_tile(1);
     __syncthreads();
     // the U waves take the tiles in pairs (one K = 32 product per channel tile): an even
     // iteration closes the pair before it, so the loop runs to the even count at or past ntile
     const int itend = ntile + (ntile & 1);
-    // iteration it: S scores tile it, U sums tile it - 1, every thread stages tile it + 2
-    // (loaded one iteration earlier) and loads tile it + 3; both roles pass one barrier per
-    // iteration
+    // iteration it: S scores tile it; at even it the U waves sum tiles it - 2 and it - 1;
+    // every thread stages tile it + 1 (loaded one iteration earlier) and loads tile it + 2;
+    // both roles pass one barrier per iteration
     if (isS) {
         // S: q B-fragments of all K-steps (channels 32 ks + 8 kg .. +7, column = head h), hi/lo
         bf16x8 qh[AT_MAXKS], ql[AT_MAXKS];
