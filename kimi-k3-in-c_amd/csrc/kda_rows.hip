@@ -80,8 +80,8 @@ struct RowsJob {
 // are j0's). MT = 16-row tiles of x (B <= 16 MT). Wave w takes K-steps tbeg + w, tbeg + w +
 // 8, ...; each step loads the 4 groups' fragments (4 x 1 KB) and the x slice, then runs the
 // hi and lo MFMAs.
-template <int MT, bool ATOM>
-// xw != nullptr: each x row is RMS-normalised on the way in, x'[k] = (xw[k] x[k]) inv with
+template <int MT, bool ATOM, bool NORM>
+// NORM (xw != nullptr): each x row is RMS-normalised on the way in, x'[k] = (xw[k] x[k]) inv with
 // inv = 1 / sqrt(mean_k x^2 + xeps) (mean in double; src/core/k3_ops.c:94-102), so a
 // normalised input needs no launch of its own.
 __global__ __launch_bounds__(64 * RT_WAVES) void rows_gemm_kernel(int B, int K, const float *__restrict__ x,
@@ -118,7 +118,15 @@ __global__ __launch_bounds__(64 * RT_WAVES) void rows_gemm_kernel(int B, int K, 
         xrow[mt] = x + (size_t)min(16 * mt + r16, B - 1) * ldx;
     }
 
-    if (xw) {   // the rows' inverse RMS: 32 lanes per row, 16 rows per pass
+    // with a normalised input, this wave's first weight fragments are requested before the
+    // rows' inverse RMS is formed, so that their latency hides behind it
+    bf16x8 wv0[RT_NT];
+    const int t0 = tbeg + w;
+    if (NORM && t0 < tend) {
+#pragma unroll
+        for (int j = 0; j < RT_NT; j++) wv0[j] = __builtin_nontemporal_load(&wg[j][(size_t)t0 * 64]);
+    }
+    if constexpr (NORM) {   // the rows' inverse RMS: 32 lanes per row, 16 rows per pass
         for (int rr0 = 0; rr0 < 16 * MT; rr0 += 16) {
             const int rr = rr0 + ((int)threadIdx.x >> 5), ln = threadIdx.x & 31;
             double ss = 0.0;
@@ -143,7 +151,7 @@ __global__ __launch_bounds__(64 * RT_WAVES) void rows_gemm_kernel(int B, int K, 
     }
     float xiv[MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; mt++) xiv[mt] = xw ? xinv[16 * mt + r16] : 1.0f;
+    for (int mt = 0; mt < MT; mt++) xiv[mt] = NORM ? xinv[16 * mt + r16] : 1.0f;
 
     f32x4 acc[RT_NT][MT];
 #pragma unroll
@@ -151,10 +159,15 @@ __global__ __launch_bounds__(64 * RT_WAVES) void rows_gemm_kernel(int B, int K, 
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) acc[j][mt] = 0.0f;
 
-    for (int t = tbeg + w; t < tend; t += RT_WAVES) {
+    for (int t = t0; t < tend; t += RT_WAVES) {
         bf16x8 wv[RT_NT];
+        if (NORM && t == t0) {
 #pragma unroll
-        for (int j = 0; j < RT_NT; j++) wv[j] = __builtin_nontemporal_load(&wg[j][(size_t)t * 64]);
+            for (int j = 0; j < RT_NT; j++) wv[j] = wv0[j];
+        } else {
+#pragma unroll
+            for (int j = 0; j < RT_NT; j++) wv[j] = __builtin_nontemporal_load(&wg[j][(size_t)t * 64]);
+        }
         const int k = 32 * t + 8 * kg;   // K % 8 == 0: the 8-slice is wholly inside or outside
         const bool kin = k < K;
         f4 xa[MT], xb[MT];
@@ -163,7 +176,7 @@ __global__ __launch_bounds__(64 * RT_WAVES) void rows_gemm_kernel(int B, int K, 
             xa[mt] = *reinterpret_cast<const f4 *>(xrow[mt] + (kin ? k : 0));
             xb[mt] = *reinterpret_cast<const f4 *>(xrow[mt] + (kin ? k : 0) + 4);
         }
-        if (xw) {
+        if constexpr (NORM) {
             const f4 wa = *reinterpret_cast<const f4 *>(xw + (kin ? k : 0));
             const f4 wb = *reinterpret_cast<const f4 *>(xw + (kin ? k : 0) + 4);
 #pragma unroll
@@ -264,8 +277,12 @@ int launch_jobs(int B, int K, const float *x, long ldx, const RowsJob &j0, const
                 const float *xw = nullptr, float xeps = 0.0f)
 {
     const long nblk = (long)j0.nb * j0.S + (long)j1.nb * j1.S;
-    hipLaunchKernelGGL((rows_gemm_kernel<MT, ATOM>), dim3((unsigned)nblk), dim3(64 * RT_WAVES), 0, st, B, K, x,
-                       ldx, j0, j1, xw, xeps);
+    if (xw)
+        hipLaunchKernelGGL((rows_gemm_kernel<MT, ATOM, true>), dim3((unsigned)nblk), dim3(64 * RT_WAVES), 0, st, B, K,
+                           x, ldx, j0, j1, xw, xeps);
+    else
+        hipLaunchKernelGGL((rows_gemm_kernel<MT, ATOM, false>), dim3((unsigned)nblk), dim3(64 * RT_WAVES), 0, st, B,
+                           K, x, ldx, j0, j1, xw, xeps);
     K3_LAUNCHED();
     return K3HIP_OK;
 }
