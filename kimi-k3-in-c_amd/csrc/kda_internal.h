@@ -102,6 +102,12 @@ int gemm_rows(int B, int N, int K, const float *x, long ldx, const uint16_t *Wf,
 int gemm_rows_hl(int B, int N, int K, const float *x, long ldx, const uint16_t *Wf, float *C, long ldc,
                  uint16_t *hl, long ldhl, hipStream_t st, float *ws = nullptr, size_t ws_floats = 0,
                  const float *xw = nullptr, float xeps = 0.0f);
+// gemm_rows on S = gemm_rows_plane_count(N, K) K-ranges, the count that spreads the
+// workgroups most evenly over the CUs when N has fewer column blocks than there are CUs (1:
+// unsplit), summed in range order into C by a second launch; ws holds S B N floats.
+int gemm_rows_plane_count(int N, int K);
+int gemm_rows_even(int B, int N, int K, const float *x, long ldx, const uint16_t *Wf, float *C, long ldc,
+                   hipStream_t st, float *ws, size_t ws_floats);
 // The same product left as its S = gemm_rows_splits(N, K) K-range partials: planes
 // P[s][B][N], whose sum in increasing s is C bit for bit, for a consumer that adds them
 // itself instead of a reduction launch.

@@ -307,8 +307,11 @@ extern "C" int k3hip_mla_decode(const k3hip_mla_weights *w, int B, int pos, int 
     //          and the W_UV halves only without the fused attention) | o | split-K partials
     const int N1 = QL + CW + (w->gate ? HV : 0);
     const long ld1 = (N1 + 3) & ~3;
-    const size_t wsf = std::max({gemm_rows_ws_floats(B, N1, E), gemm_rows_ws_floats(B, H * QH, QL),
-                                 gemm_rows_ws_floats(B, E, HV)});
+    // the q_a / kv_a / g product on K-ranges that spread it over every CU, summed by a second
+    // launch (161 column blocks at hidden 7168: 3 ranges, 483 workgroups)
+    const int np1 = gemm_rows_plane_count(N1, E);
+    const size_t wsf = std::max({gemm_rows_ws_floats(B, N1, E), np1 > 1 ? (size_t)np1 * std::min(64, B) * N1 : 0,
+                                 gemm_rows_ws_floats(B, H * QH, QL), gemm_rows_ws_floats(B, E, HV)});
     size_t sizes[] = {(size_t)B * ld1 * 4, (size_t)B * QL * 4, (size_t)B * H * QH * 4,
                       (size_t)2 * B * H * QH * 2, (size_t)2 * B * H * CW * 4, (size_t)B * H * CW * 4,
                       fused ? mla_attention_ws_bytes(B, H, KL, Tn) : (size_t)B * H * Tn * 4,
@@ -334,7 +337,7 @@ extern "C" int k3hip_mla_decode(const k3hip_mla_weights *w, int B, int pos, int 
 
     // q_a, kv_a and g in one pass over their weights (fp32 x split hi/lo in registers);
     // q = q_b(rmsnorm(q_a x)); latent + rope = kv_a x, the latent rmsnorm'd into the cache
-    if ((rc = gemm_rows(B, N1, E, x, E, (const uint16_t *)w->xin, C1, ld1, st, ws, wsf))) return rc;
+    if ((rc = gemm_rows_even(B, N1, E, x, E, (const uint16_t *)w->xin, C1, ld1, st, ws, wsf))) return rc;
     // the two rmsnorms: with the fused attention and an unsplit q_b product, the q_b GEMV
     // normalises q_a as it reads it and the attention writes the new latent row itself;
     // otherwise one launch writes qn and the cache row

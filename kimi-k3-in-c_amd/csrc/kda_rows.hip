@@ -445,13 +445,35 @@ int gemm_rows_hl(int B, int N, int K, const float *x, long ldx, const uint16_t *
     return K3HIP_OK;
 }
 
-int gemm_rows(int B, int N, int K, const float *x, long ldx, const uint16_t *Wf, float *C, long ldc,
-              hipStream_t st, float *ws, size_t ws_floats, bool c_zeroed)
+namespace {
+
+// K-ranges that spread the workgroups most evenly: the most workgroups one CU gets over the
+// share of K each reads, least wins, the fewer ranges on a tie (161 column blocks on 256 CUs:
+// 3 ranges, at most 2 workgroups per CU, against 1 range on 161 CUs)
+RowsPlan rows_plan_even(int N, int K)
+{
+    const long nblk = (N + 16 * RT_NT - 1) / (16 * RT_NT), ncu = cu_total();
+    const int KT = (K + 31) / 32;
+    RowsPlan p{1, KT};
+    double cost = (double)((nblk + ncu - 1) / ncu);
+    for (int s = 2; s <= std::min(8, KT); s++) {
+        const int tchunk = (KT + s - 1) / s;
+        if ((KT + tchunk - 1) / tchunk != s) continue;   // s ranges of whole K-steps, none empty
+        const double c = (double)((nblk * s + ncu - 1) / ncu) / s;
+        if (c < cost - 1e-9) {
+            cost = c;
+            p = RowsPlan{s, tchunk};
+        }
+    }
+    return p;
+}
+
+int rows_run(int B, int N, int K, const float *x, long ldx, const uint16_t *Wf, float *C, long ldc,
+             hipStream_t st, float *ws, size_t ws_floats, bool c_zeroed, const RowsPlan &pl)
 {
     if (B <= 0 || N <= 0 || K <= 0) return K3HIP_OK;
     if ((K & 7) || (ldx & 3) || (((uintptr_t)x | (uintptr_t)Wf) & 15))
         K3_FAIL(K3HIP_EINVAL, "gemm_rows: K=%d ldx=%ld need multiples of 8 / 4 and 16-byte aligned x, W", K, ldx);
-    const RowsPlan pl = rows_plan(N, K);
     const int S = pl.S, tchunk = pl.tchunk;
     if (c_zeroed && S == 2) {   // the two K-range partials are added into C in place
         for (int b0 = 0; b0 < B; b0 += 64) {
@@ -466,7 +488,7 @@ int gemm_rows(int B, int N, int K, const float *x, long ldx, const uint16_t *Wf,
         }
         return K3HIP_OK;
     }
-    const size_t need = gemm_rows_ws_floats(B, N, K);
+    const size_t need = S > 1 ? (size_t)S * std::min(64, B) * N : 0;
     StreamBuf own;
     if (need && (!ws || ws_floats < need || ((uintptr_t)ws & 15))) {
         int rc = stream_alloc(own, need * sizeof(float), st);
@@ -502,6 +524,28 @@ int gemm_rows(int B, int N, int K, const float *x, long ldx, const uint16_t *Wf,
         }
     }
     return K3HIP_OK;
+}
+
+}  // namespace
+
+int gemm_rows(int B, int N, int K, const float *x, long ldx, const uint16_t *Wf, float *C, long ldc,
+              hipStream_t st, float *ws, size_t ws_floats, bool c_zeroed)
+{
+    if (B <= 0 || N <= 0 || K <= 0) return K3HIP_OK;
+    return rows_run(B, N, K, x, ldx, Wf, C, ldc, st, ws, ws_floats, c_zeroed, rows_plan(N, K));
+}
+
+int gemm_rows_plane_count(int N, int K)
+{
+    if (N <= 0 || K <= 0) return 1;
+    return rows_plan_even(N, K).S;
+}
+
+int gemm_rows_even(int B, int N, int K, const float *x, long ldx, const uint16_t *Wf, float *C, long ldc,
+                   hipStream_t st, float *ws, size_t ws_floats)
+{
+    if (B <= 0 || N <= 0 || K <= 0) return K3HIP_OK;
+    return rows_run(B, N, K, x, ldx, Wf, C, ldc, st, ws, ws_floats, false, rows_plan_even(N, K));
 }
 
 }  // namespace k3kda
