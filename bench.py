@@ -375,40 +375,49 @@ def bench_layer(torch, k3, steps: int, warmup: int, cpu: bool) -> dict:
         state.zero_()
         dw.layer_prefill(out, x, state, T)
 
+    # the default projections (hipBLASLt) and the same step with every projection on the
+    # hand-written MFMA GEMM, timed step by step in alternating order: the part's clock falls
+    # under seconds of dense MFMA work, so paths timed one after the other would not see the
+    # same clock
+    paths = (k3.GEMM_HIPBLASLT, k3.GEMM_HANDWRITTEN)
     step()
     torch.cuda.synchronize()
     ramp(torch, step)
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
-    e0, e1 = ev_pair(torch)
-    t0 = time.perf_counter()
-    e0.record()
-    for _ in range(steps):
-        step()
-    e1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    step_s = e0.elapsed_time(e1) * 1e-3 / steps
-    flops = layer_flops_per_token(E, H, D, 64) * T
-    # the same step with every projection on the hand-written MFMA GEMM (reported beside it)
-    k3.set_projection_gemm(k3.GEMM_HANDWRITTEN)
     try:
-        for _ in range(warmup + 1):
-            step()
-        e0.record()
-        for _ in range(steps):
-            step()
-        e1.record()
+        for p in paths:
+            k3.set_projection_gemm(p)
+            for _ in range(warmup + 1):
+                step()
         torch.cuda.synchronize()
-        hw_s = e0.elapsed_time(e1) * 1e-3 / steps
+        # one event between consecutive steps, read after the last one (no host wait between
+        # steps, which would idle the part and let the clock drop)
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(2 * steps + 1)]
+        order = []
+        t0 = time.perf_counter()
+        evs[0].record()
+        for i in range(steps):
+            for p in (paths if i % 2 == 0 else paths[::-1]):
+                k3.set_projection_gemm(p)
+                step()
+                evs[len(order) + 1].record()
+                order.append(p)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        times = {p: [] for p in paths}
+        for n, p in enumerate(order):
+            times[p].append(evs[n].elapsed_time(evs[n + 1]) * 1e-3)
     finally:
         k3.set_projection_gemm(k3.GEMM_HIPBLASLT)
+    step_s = sum(times[paths[0]]) / steps
+    hw_s = sum(times[paths[1]]) / steps
+    flops = layer_flops_per_token(E, H, D, 64) * T
     dw.close()
     dropin = bench_dropin(torch, k3, w, cfg, x_host)
     out_d = {
         "value": T / step_s, "unit": "tokens/s", "ms_per_step": step_s * 1e3,
-        "wall_ms_per_step": wall / steps * 1e3,
+        "wall_ms_per_step": wall / (2 * steps) * 1e3,
+        "timing": "both projection paths timed step by step in alternating order (HIP events per step); "
+                  "wall_ms_per_step is the wall clock over both paths' steps",
         "config": {"workload": "kda_layer_prefill", "hidden": E, "heads": H, "head_dim": D, "T": T,
                    "chunk": 64, "batch": 1, "conv_k": K, "weights": "bf16", "activations": "bf16 in",
                    "intermediates": "fp32; f_a as a bf16 hi/lo pair into f_b; y in fp16 into o_proj (fp16 copy of W_o)"},

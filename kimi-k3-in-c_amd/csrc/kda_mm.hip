@@ -298,6 +298,239 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     }
 }
 
+// ---- whole tiles on v_mfma_f32_16x16x32 with direct-to-LDS loads ----------------------
+//
+// The same 256 x 256 workgroup tile and 2 x 2 waves, each wave's 128 x 128 block as 8 x 8
+// tiles of 16 x 16 on the 16x16x32 MFMA (64 accumulators of 4 registers, kept in AGPRs by
+// tying them to the instruction). K advances in stages of 32: each stage's A and B rows
+// (32 KiB) are brought into LDS by buffer loads that write LDS directly (no VGPR staging and
+// no LDS write instructions); four stages rotate, so a stage's loads are issued three stages
+// before it is read. The load stream runs on across the tiles a workgroup of the persistent
+// grid walks, so the next tile's first stages arrive while the current one finishes.
+// Rows are 64 bytes (4 chunks of 16); chunk c of row r sits at c ^ ((r >> 2) & 3), which
+// keeps every 16-lane fragment read on 64 distinct banks.
+constexpr int QBK = 32, QNST = 4;
+constexpr int QROW = QBK * 2;                     // bytes per staged row
+constexpr int QSTAGE = (BM + BN) * QROW;          // 32 KiB
+constexpr int QLDS = QNST * QSTAGE;               // 128 KiB
+constexpr int QDMA = QSTAGE / 1024 / 4;           // 1 KiB loads per wave per stage (8)
+constexpr int QT = WM / 16;                       // 16-row tiles per wave side (8)
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+// acc += a . b on the 16x16x32 MFMA with the accumulator tied to its AGPRs (the builtin lets
+// the compiler move 64 accumulators between register files inside the loop)
+template <int AB>
+__device__ __forceinline__ void mfma16(const u32x4 &a, const u32x4 &b, f32x4 &c)
+{
+    if constexpr (AB == K3_DT_F16)
+        asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+    else
+        asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
+
+// Wait states between the accumulators' MFMA writes and their reads (or between their
+// writes and the next MFMAs), pinned in order: each statement takes eight accumulators as
+// operands, so no read moves above the first and no MFMA above the last.
+#define K3_TIE8(nops, r)                                                                                       \
+    asm volatile(nops : "+a"(r[0]), "+a"(r[1]), "+a"(r[2]), "+a"(r[3]), "+a"(r[4]), "+a"(r[5]), "+a"(r[6]), \
+                 "+a"(r[7]))
+#define K3_TIE_ACC(nops, acc)                                                                                  \
+    do {                                                                                                       \
+        K3_TIE8(nops, acc[0]); K3_TIE8("", acc[1]); K3_TIE8("", acc[2]); K3_TIE8("", acc[3]);                  \
+        K3_TIE8("", acc[4]); K3_TIE8("", acc[5]); K3_TIE8("", acc[6]); K3_TIE8("", acc[7]);                    \
+    } while (0)
+
+// s_waitcnt vmcnt(n) lgkmcnt(0)
+template <int n>
+__device__ __forceinline__ void q_wait()
+{
+    static_assert(n >= 0 && n < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4));
+}
+
+template <int AB, int OUT, bool PERS>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void mm16_kernel(
+    int M, int N, int K, const uint16_t *__restrict__ A, long lda, const uint16_t *__restrict__ B, long ldb,
+    void *__restrict__ Cv, long ldc, int gcols, long gstride, int tiles_m, int tiles_n)
+{
+    extern __shared__ __attribute__((aligned(1024))) char smem[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int nks = K / QBK;   // >= QNST (checked by the launcher)
+
+    auto tile_at = [&](int r, int &m0, int &n0) -> bool {
+        int tm, tn, sp;
+        if constexpr (PERS) {
+            if (!ptile_of(blockIdx.x, gridDim.x, r, tiles_m * tiles_n, tiles_m, tiles_n, tm, tn)) return false;
+        } else {
+            if (r > 0) return false;
+            tile_of(blockIdx.x, gridDim.x, tiles_m, tiles_n, 1, tm, tn, sp);
+        }
+        m0 = min(tm * BM, M - BM);
+        n0 = min(tn * BN, N - BN);
+        return true;
+    };
+    auto rsrc = [&](const uint16_t *base) {
+        return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, 0x7fffffff, 0x00020000);
+    };
+
+    // loads: instruction j (0 .. QDMA - 1) of wave w fills staged rows 16 (w + 4 j) .. + 15 (1 KiB
+    // at stage + 1024 (w + 4 j); A rows for j < QDMA / 2, B rows after); lane l lands at row
+    // + l / 4, physical chunk l & 3, so it loads logical chunk (l & 3) ^ ((l >> 4) & 3), the
+    // chunk whose swizzled place that is (the row's (r >> 2) & 3 is (l >> 4) & 3 for every j)
+    const int lch = (lane & 3) ^ ((lane >> 4) & 3);
+    const int voA = ((lane >> 2) * (int)lda + lch * 8) * 2, voB = ((lane >> 2) * (int)ldb + lch * 8) * 2;
+    int ir = 0, iks = 0, im0 = 0, in0 = 0;
+    if (!tile_at(0, im0, in0)) return;
+    __amdgpu_buffer_rsrc_t iA = rsrc(A + (long)im0 * lda), iB = rsrc(B + (long)in0 * ldb);
+    // load j of a stage at stream position (rA, rB, ks)
+    auto load = [&](int j, uint32_t stage_off, __amdgpu_buffer_rsrc_t rA, __amdgpu_buffer_rsrc_t rB, int ks) {
+        const int R = 16 * (wave + 4 * j);
+        char *dst = smem + stage_off + 1024 * (wave + 4 * j);
+        if (j < QDMA / 2)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lds_void *)dst, 16, voA, R * (int)lda * 2 + ks * QROW, 0, 0);
+        else
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, (lds_void *)dst, 16, voB, (R - BM) * (int)ldb * 2 + ks * QROW,
+                                                     0, 0);
+    };
+    // the stream position moves on one stage (past the last stage it stays: the last stage is
+    // loaded again into a buffer nothing reads)
+    auto advance = [&]() {
+        if (iks + 1 < nks) {
+            iks++;
+            return;
+        }
+        int m, n;
+        if (!tile_at(ir + 1, m, n)) return;
+        ir++;
+        iks = 0;
+        iA = rsrc(A + (long)m * lda);
+        iB = rsrc(B + (long)n * ldb);
+    };
+
+    // fragments: lane (row r16 of a 16-row tile, K chunk kq) at its swizzled chunk
+    const int r16 = lane & 15, kq = lane >> 4;
+    const uint32_t fo = r16 * QROW + ((kq ^ ((r16 >> 2) & 3)) << 4);
+    const uint32_t ra = fo + wm * WM * QROW, rb = fo + BM * QROW + wn * WN * QROW;
+    auto lds16 = [&](uint32_t off) { return *reinterpret_cast<const u32x4 *>(smem + off); };
+
+    // prologue: stages 0 .. 3 requested, stage 0 landed and published, its fragments read
+#pragma unroll
+    for (int p = 0; p < QNST; p++) {
+#pragma unroll
+        for (int j = 0; j < QDMA; j++) load(j, p * QSTAGE, iA, iB, iks);
+        advance();
+    }
+    q_wait<(QNST - 1) * QDMA>();
+    __builtin_amdgcn_s_barrier();
+    u32x4 a[2][QT], b[QT];
+#pragma unroll
+    for (int i = 0; i < QT; i++) a[0][i] = lds16(ra + 1024 * i);
+#pragma unroll
+    for (int j = 0; j < QT; j++) b[j] = lds16(rb + 1024 * j);
+
+    f32x4 acc[QT][QT];
+#pragma unroll
+    for (int i = 0; i < QT; i++)
+#pragma unroll
+        for (int j = 0; j < QT; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    K3_TIE_ACC("s_nop 4", acc);   // the zeroed AGPRs before the first MFMA reads them
+
+    // stage G from buffer G % 4, its fragments in a[CUR] and b. 64 MFMA slots in column-group
+    // order; slot 16 opens with the wait for stage G + 1 (this wave's loads, with G + 2 and
+    // G + 3 still in flight) and the barrier after which every wave has read stage G's buffer
+    // (it takes stage G + 4, one load every 4 slots from slot 26) and may read stage G + 1's:
+    // b[0], b[1] (dead since slots 7, 15) at slots 16, 17, a[1 - CUR] at 18-25, b[j] right
+    // after its last use from slot 23 on
+    auto stage = [&](auto curc, uint32_t G) {
+        constexpr int cur = decltype(curc)::value, nx = cur ^ 1;
+        const uint32_t s1 = ((G + 1) % QNST) * QSTAGE, s0 = (G % QNST) * QSTAGE;
+        const __amdgpu_buffer_rsrc_t dA = iA, dB = iB;
+        const int dks = iks;
+        advance();
+#pragma unroll
+        for (int q = 0; q < QT * QT; q++) {
+            const int j = q / QT, i = q % QT;
+            if (q == 16) {
+                q_wait<(QNST - 2) * QDMA>();
+                __builtin_amdgcn_s_barrier();
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            mfma16<AB>(a[cur][i], b[j], acc[i][j]);
+            if (q == 16) b[0] = lds16(rb + s1);
+            if (q == 17) b[1] = lds16(rb + s1 + 1024);
+            if (q >= 18 && q < 18 + QT) a[nx][q - 18] = lds16(ra + s1 + 1024 * (q - 18));
+            if (i == QT - 1 && j >= 2) b[j] = lds16(rb + s1 + 1024 * j);
+            if (q >= 26 && (q - 26) % 4 == 0 && (q - 26) / 4 < QDMA) load((q - 26) / 4, s0, dA, dB, dks);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    uint32_t G = 0;   // stage being computed, counted over this workgroup's tiles
+    int m0, n0;
+    for (int r = 0; tile_at(r, m0, n0); r++) {
+        // nks is even: stages in pairs, so that the fragment register set is known statically
+        for (int ks = 0; ks < nks; ks += 2, G += 2) {
+            stage(std::integral_constant<int, 0>{}, G);
+            stage(std::integral_constant<int, 1>{}, G + 1);
+        }
+
+        // the last MFMAs' results, then the tile out of the accumulators: lane holds rows
+        // 4 kq .. 4 kq + 3, column r16 of each 16 x 16 tile
+        K3_TIE_ACC("s_nop 15\n s_nop 15\n s_nop 15", acc);
+#pragma unroll
+        for (int i = 0; i < QT; i++)
+#pragma unroll
+            for (int j = 0; j < QT; j++) {
+                const int col = n0 + wn * WN + j * 16 + r16;
+                const int g = col / gcols;
+                const long cbase = g * gstride + (col - g * gcols);
+                const f32x4 v = acc[i][j];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int row = m0 + wm * WM + i * 16 + 4 * kq + e;
+                    if constexpr (OUT == OUT_F32) {
+                        reinterpret_cast<float *>(Cv)[(long)row * ldc + cbase] = v[e];
+                    } else if constexpr (OUT == OUT_F16) {
+                        reinterpret_cast<_Float16 *>(Cv)[(long)row * ldc + cbase] = (_Float16)v[e];
+                    } else {
+                        reinterpret_cast<uint16_t *>(Cv)[(long)row * ldc + cbase] = f2bf(v[e]);
+                    }
+                }
+                acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        // the stores count with the loads: let them drain so that the stage waits stay exact
+        q_wait<0>();
+        K3_TIE_ACC("s_nop 4", acc);
+    }
+    // no load may still be writing this workgroup's LDS when it ends
+    q_wait<0>();
+}
+
+template <int AB, int OUT, bool PERS>
+int launch_mm16(int M, int N, int K, const void *A, long lda, const void *B, long ldb, void *C, long ldc, int gcols,
+                long gstride, long grid, hipStream_t st)
+{
+    static bool lds_ok[64];
+    int dev = 0;
+    K3_HIP(hipGetDevice(&dev));
+    if (dev >= 0 && dev < 64 && !lds_ok[dev]) {
+        K3_HIP(hipFuncSetAttribute((const void *)mm16_kernel<AB, OUT, PERS>,
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, QLDS));
+        lds_ok[dev] = true;
+    }
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    if (grid > 0x7fffffffL) K3_FAIL(K3HIP_EUNSUPPORTED, "mm: %dx%d output needs too many workgroups", M, N);
+    hipLaunchKernelGGL((mm16_kernel<AB, OUT, PERS>), dim3((unsigned)grid), dim3(NT), QLDS, st, M, N, K,
+                       (const uint16_t *)A, lda, (const uint16_t *)B, ldb, C, ldc, gcols, gstride, tiles_m, tiles_n);
+    K3_LAUNCHED();
+    return K3HIP_OK;
+}
+
 template <int AB, int OUT, bool EDGE, bool PERS>
 int launch_mm_e(int M, int N, int K, const void *A, long lda, const void *B, long ldb, void *C, long ldc, int gcols,
                 long gstride, int splits, long grid, hipStream_t st)
@@ -333,6 +566,14 @@ int launch_mm(int M, int N, int K, const void *A, long lda, const void *B, long 
     int ncu = 0, rc;
     if ((rc = cu_count(ncu))) return rc;
     const int pgrid = ncu / 8 * 8;
+    if constexpr (OUT != OUT_PART) {
+        // whole tiles in one K-range: the 16x16x32 form with direct-to-LDS stages
+        if (splits == 1 && K % (2 * QBK) == 0 && K / QBK >= QNST) {
+            if (pgrid >= 8 && tiles > pgrid)
+                return launch_mm16<AB, OUT, true>(M, N, K, A, lda, B, ldb, C, ldc, gcols, gstride, pgrid, st);
+            return launch_mm16<AB, OUT, false>(M, N, K, A, lda, B, ldb, C, ldc, gcols, gstride, tiles, st);
+        }
+    }
     if (splits == 1 && pgrid >= 8 && tiles > pgrid)
         return launch_mm_e<AB, OUT, false, true>(M, N, K, A, lda, B, ldb, C, ldc, gcols, gstride, 1, pgrid, st);
     return launch_mm_e<AB, OUT, false, false>(M, N, K, A, lda, B, ldb, C, ldc, gcols, gstride, splits,

@@ -31,7 +31,9 @@ def check(got, a, b, out_rel):
 @pytest.mark.parametrize("M,N,K,ab,out", [
     (1, 1, 64, "bf16", "f32"), (255, 257, 64, "bf16", "f32"), (1000, 520, 256, "bf16", "f32"),
     (300, 160, 4096, "bf16", "f32"), (513, 384, 128, "f16", "f32"), (777, 1000, 192, "bf16", "bf16"),
-    (256, 768, 512, "bf16", "f16"), (1024, 4096, 4096, "bf16", "f32"), (640, 2048, 4096, "f16", "bf16")])
+    (256, 768, 512, "bf16", "f16"), (1024, 4096, 4096, "bf16", "f32"), (640, 2048, 4096, "f16", "bf16"),
+    # more tiles than CUs: the persistent grid, its load stream running across tiles
+    (4352, 4352, 256, "bf16", "f32"), (4608, 4352, 128, "f16", "f16")])
 def test_proj_gemm_vs_float64(gpu, M, N, K, ab, out):
     import torch
     g = torch.Generator(device="cuda").manual_seed(M * 7 + N * 3 + K)
