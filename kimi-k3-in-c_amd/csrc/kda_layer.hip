@@ -528,8 +528,10 @@ extern "C" int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *
     hipStream_t st = as_stream(stream);
     const size_t P = (size_t)H * D, TP = (size_t)T * P;
     const size_t wsb = k3hip_kda_chunk_workspace(T, H, D, 64);
-    // The projections are plain GEMMs and run on hipBLASLt by default: the hand-written MFMA
-    // GEMM (kda_mm.hip, k3hip_proj_gemm) measures 0.90-0.93x of its speed on these shapes.
+    // The 4096-deep projections are plain GEMMs and run on hipBLASLt by default: the
+    // hand-written MFMA GEMM (kda_mm.hip, k3hip_proj_gemm) matches it within 1-2% on the
+    // 4096-wide ones but not on q/k/v, whose fp32 output stores keep it at ~0.93x; the 256-deep
+    // z product runs on the hand-written kernel either way (faster there).
     // k3hip_set_projection_gemm(K3HIP_GEMM_HANDWRITTEN) selects the hand-written kernels for
     // every projection (`own`).
     // The hand-written kernel needs hidden % 64 == 0 and a 16-byte aligned bf16 x (an fp32 x is
@@ -603,7 +605,11 @@ extern "C" int k3hip_kda_layer_prefill(const k3hip_kda_weights *w, int T, void *
         hipLaunchKernelGGL(split_fa_b_kernel, dim3(grid_for((size_t)T * (D + H))), dim3(256), 0, st, fa,
                            fa2, bl, D, H, (size_t)T * (D + H));
         K3_LAUNCHED();
-        if ((rc = gemm_bf16(T, (int)P, 2 * D, fa2, w->f_b2, z, K3HIP_F32, st))) return rc;
+        if (mm_supported(2 * D, 2 * D, 2 * D))
+            rc = mm(T, (int)P, 2 * D, K3HIP_BF16, fa2, 2 * D, w->f_b2, 2 * D, z, K3HIP_F32, (long)P, st);
+        else
+            rc = gemm_bf16(T, (int)P, 2 * D, fa2, w->f_b2, z, K3HIP_F32, st);
+        if (rc) return rc;
     }
     // 2-5 K1 fused into 6 K2 (chunked): the prepared q, k, v, g never reach HBM
     if ((rc = k3hip_kda_prefill(T, H, D, K, w->gate_lb, K3HIP_F32, qp, kp, vp, z, bl, w->q_conv,
