@@ -8,21 +8,28 @@
 //                                      the reference's [out][in] matrix), both K-contiguous
 // with bf16 or fp16 operands and fp32 accumulation.
 //
-// Workgroup tile 256 x 256, K in steps of 64, four waves in a 2 x 2 grid; each wave owns a
-// 128 x 128 block = 4 x 4 v_mfma_f32_32x32x16 tiles (256 accumulator registers, one wave per
-// SIMD). Per K-step the workgroup stages A[256][64] and B[256][64] (64 KiB) in LDS, double
-// buffered (128 KiB): each thread loads its 16-byte pieces of step ks+2 into registers while
-// step ks computes and writes them to the other LDS buffer during step ks+1. One barrier per
-// step, placed before the step's last 16-wide substep so the first fragments of the next
-// step load under that substep's MFMAs. Fragment reads are 16 bytes per lane; rows are 128
-// bytes and the 16-byte chunk index is XORed with (row & 7) ^ ((row >> 3) & 1), which keeps
-// every 16-lane group of a fragment read on distinct banks (no LDS bank conflicts, counter-
-// verified). Global loads are buffer loads: a thread's 16 pieces differ only by wave-uniform
-// offsets, so one per-lane offset register per operand addresses all of them, and every LDS
-// offset is one per-lane base plus an immediate; the loop body stays at ~150 VGPRs. Each
-// substep is 16 MFMA slots in a fixed order (sched_barrier between slots), each slot also
-// carrying one fragment read or one LDS write + global load, and the same branch-free body
-// runs every K-step (the last steps reload clamped copies that nothing reads).
+// Two kernels share the workgroup tile (256 x 256, four waves in a 2 x 2 grid, a 128 x 128
+// block per wave, one wave per SIMD), the tile order and the persistent grid:
+//  * mm16_kernel (whole tiles, one K-range, fp32 or fp16 output: every layer projection but
+//    the split-K f_a / b): v_mfma_f32_16x16x32 with the accumulators tied to their AGPRs;
+//    K in stages of 32 brought into LDS by direct-to-LDS buffer loads, four stages rotating,
+//    each loaded three stages before it is read (its own description below);
+//  * mm_kernel (the general form: partial tiles, split-K partial planes, bf16 outputs): each
+//    wave's block is 4 x 4 v_mfma_f32_32x32x16 tiles (256 accumulator registers). Per K-step
+//    of 64 the workgroup stages A[256][64] and B[256][64] (64 KiB) in LDS, double buffered
+//    (128 KiB): each thread loads its 16-byte pieces of step ks+2 into registers while step
+//    ks computes and writes them to the other LDS buffer during step ks+1. One barrier per
+//    step, placed before the step's last 16-wide substep so the first fragments of the next
+//    step load under that substep's MFMAs. Fragment reads are 16 bytes per lane; rows are 128
+//    bytes and the 16-byte chunk index is XORed with (row & 7) ^ ((row >> 3) & 1), which keeps
+//    every 16-lane group of a fragment read on distinct banks (no LDS bank conflicts,
+//    counter-verified). Global loads are buffer loads: a thread's 16 pieces differ only by
+//    wave-uniform offsets, so one per-lane offset register per operand addresses all of them,
+//    and every LDS offset is one per-lane base plus an immediate; the loop body stays at ~150
+//    VGPRs. Each substep is 16 MFMA slots in a fixed order (sched_barrier between slots), each
+//    slot also carrying one fragment read or one LDS write + global load, and the same
+//    branch-free body runs every K-step (the last steps reload clamped copies that nothing
+//    reads).
 //
 // Tile order is XCD-aware: workgroup b runs on XCD b % 8, and consecutive tile ids (groups
 // of 8 M-tiles walked along N) are given to the same XCD, so the tiles running together on
