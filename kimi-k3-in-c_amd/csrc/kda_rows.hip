@@ -80,10 +80,10 @@ struct RowsJob {
 // are j0's). MT = 16-row tiles of x (B <= 16 MT). Wave w takes K-steps tbeg + w, tbeg + w +
 // 8, ...; each step loads the 4 groups' fragments (4 x 1 KB) and the x slice, then runs the
 // hi and lo MFMAs.
-template <int MT, bool ATOM, bool NORM>
 // NORM (xw != nullptr): each x row is RMS-normalised on the way in, x'[k] = (xw[k] x[k]) inv with
 // inv = 1 / sqrt(mean_k x^2 + xeps) (mean in double; src/core/k3_ops.c:94-102), so a
 // normalised input needs no launch of its own.
+template <int MT, bool ATOM, bool NORM>
 __global__ __launch_bounds__(64 * RT_WAVES) void rows_gemm_kernel(int B, int K, const float *__restrict__ x,
                                                                   long ldx, RowsJob j0, RowsJob j1,
                                                                   const float *__restrict__ xw, float xeps)
