@@ -14,10 +14,12 @@
 // NPASS float4s at rows rs, rs+RPP, ... of column group cg. A pass over the rows is one
 // contiguous D*RPP*4-byte span of S per instruction, so every wave issues full 64-byte
 // segments. The two reductions over rows (u, then o) go through LDS. The state is read
-// with nontemporal loads and written back with nontemporal stores: it streams through
-// without being kept in the caches. The stores measured 54.5 -> 45.5 us per B=64, H=32,
-// D=128 step (5.0 -> 6.0 TB/s) on MI355X; the loads a further ~0.6 us (48.6 -> 48.0 us
-// in the current build, alternating runs).
+// with nontemporal loads and written back with system-scope non-temporal stores (the
+// `sc0 sc1 nt` cache policy: through to memory, not kept in any cache): it streams through.
+// Nontemporal stores measured 54.5 -> 45.5 us per B=64, H=32, D=128 step (5.0 -> 6.0 TB/s)
+// on MI355X, the loads a further ~0.6 us; the system-scope form of the stores 49.6 -> 48.0
+// us against the compiler's nontemporal store on one box (48.5 for a plain `nt` store,
+// 48.5 with the loads in that form too).
 // D = 128 uses 512 threads (8 float4s each, 60 VGPRs, 8 waves per SIMD): the 2,048 states
 // of a B=64 step then run as two full rounds of 1,024 workgroups; with 256 threads
 // (16 float4s, 90 VGPRs, 5 waves per SIMD) they ran as 1,280 + 768, about 1.5% slower.
@@ -28,6 +30,12 @@
 #include "kda_internal.h"
 
 namespace k3kda {
+
+// One 16-byte state store with the system-scope non-temporal policy (through to memory).
+__device__ __forceinline__ void store_stream(f4 *p, const f4 &v)
+{
+    asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1 nt" ::"v"(p), "v"(v) : "memory");
+}
 
 template <int D, int NT>
 __global__ __launch_bounds__(NT) void kda_decode_kernel(
@@ -93,7 +101,7 @@ __global__ __launch_bounds__(NT) void kda_decode_kernel(
         const float kr = s_k[r], qr = s_q[r];
         if (kr != 0.0f) s[m] = s[m] + (kr * b) * d;
         if (qr != 0.0f) acc = acc + qr * s[m];
-        __builtin_nontemporal_store(s[m], &Sp[(rs + m * RPP) * CPR + cg]);
+        store_stream(&Sp[(rs + m * RPP) * CPR + cg], s[m]);
     }
     s_red[rs][cg] = acc;   // every read of s_red above finished before the last barrier
     __syncthreads();
