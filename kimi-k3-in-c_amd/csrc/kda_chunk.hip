@@ -130,15 +130,34 @@ __device__ __forceinline__ void store_cpl(float *p, const float (&v)[CPL])
     else *reinterpret_cast<f2 *>(p) = f2{v[0], v[1]};
 }
 
-// Split x and store it as lane `lane` of the fragment block at `blk`. Workspace stores are
-// nontemporal: the block is read back by the next kernel from HBM (its L2 warm-up touches),
-// so keeping it in this kernel's L2 only displaces the inputs (phase 1 at T=8192, H=32, D=128: -5 us).
-__device__ __forceinline__ void store_frag(char *blk, int lane, const float (&x)[8])
+// Workspace stores: 16-byte buffer stores with the system-scope non-temporal policy
+// (aux 19 = sc0 | nt | sc1: through to memory, kept in no cache), addressed from the item's
+// block. The workspace is read back by the next kernel from HBM (its L2 warm-up touches) and
+// is larger than the memory-side cache, so keeping any of it only displaces the inputs: phase
+// 1 at T=8192, H=32, D=128 -5 us with the compiler's nontemporal stores, and the core step
+// 0.5355 -> 0.5333 ms with this policy. They are compiler-visible stores, so the wait states
+// a store needs (an MFMA result as data, a VALU overwrite of its data registers) are inserted
+// as for any other.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t ws_rsrc(char *blk, size_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(blk, (short)0, (int)bytes, 0x00020000);
+}
+
+template <typename V>
+__device__ __forceinline__ void store_ws(__amdgpu_buffer_rsrc_t r, int off, const V &v)
+{
+    static_assert(sizeof(V) == 16, "16-byte stores");
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, 19);
+}
+
+// Split x and store it as lane `lane` of the fragment block `off` bytes into the item's block.
+__device__ __forceinline__ void store_frag(__amdgpu_buffer_rsrc_t r, int off, int lane, const float (&x)[8])
 {
     bf16x8 hi, lo;
     split8(x, hi, lo);
-    __builtin_nontemporal_store(hi, reinterpret_cast<bf16x8 *>(blk + lane * 16));
-    __builtin_nontemporal_store(lo, reinterpret_cast<bf16x8 *>(blk + 1024 + lane * 16));
+    store_ws(r, off + lane * 16, hi);
+    store_ws(r, off + 1024 + lane * 16, lo);
 }
 
 struct Frag {
@@ -215,6 +234,8 @@ __device__ __forceinline__ void p1_item(float *lds, const float (&vreg)[2][8], c
     asm volatile("" : "+v"(tid_o));
     const int tid = tid_o, lane = tid & 63, w = threadIdx.x >> 6;
     const int m = lane & 15, kg = lane >> 4;
+    const __amdgpu_buffer_rsrc_t wr = ws_rsrc(blk, WL::SIZE);
+    static_assert(WL::SIZE < (1u << 31), "workspace offsets are 32-bit");
 
 
     // (2) G = cumulative sum of g down the chunk (padded rows add 0), kept as G*log2(e):
@@ -260,7 +281,7 @@ __device__ __forceinline__ void p1_item(float *lds, const float (&vreg)[2][8], c
                 const int s = 32 * ks + 8 * kg + e;
                 x[e] = sK[s * PD + i] * exp2_fast(gl - sG[s * PD + i]);
             }
-            store_frag(blk + WL::KF + (size_t)fb * 2048, lane, x);
+            store_frag(wr, (int)WL::KF + fb * 2048, lane, x);
         }
     } else {
         // wave -> (row block a, first column block b0, column blocks nb)
@@ -322,7 +343,7 @@ __device__ __forceinline__ void p1_item(float *lds, const float (&vreg)[2][8], c
         const int fb = tid >> 6, rt = fb >> 1, ks = fb & 1;
         float x[8];
         lds8(x, &sT[(SB * rt + m) * PA + 32 * ks + 8 * kg]);
-        store_frag(blk + WL::AF + (size_t)fb * 2048, lane, x);
+        store_frag(wr, (int)WL::AF + fb * 2048, lane, x);
     }
     __syncthreads();   // the inverse below overwrites every block of sT at or below the diagonal
 
@@ -398,7 +419,7 @@ __device__ __forceinline__ void p1_item(float *lds, const float (&vreg)[2][8], c
             lds8(gx, &sG[t * PD + i0]);
 #pragma unroll
             for (int e = 0; e < 8; e++) x[e] = x[e] * exp2_fast(gx[e]);
-            store_frag(blk + WL::QF + (size_t)fb * 2048, lane, x);
+            store_frag(wr, (int)WL::QF + fb * 2048, lane, x);
         }
     }
     __syncthreads();
@@ -472,7 +493,7 @@ __device__ __forceinline__ void p1_item(float *lds, const float (&vreg)[2][8], c
         }
 #pragma unroll
         for (int a = 0; a < 4; a++) {
-            __builtin_nontemporal_store(au[a], reinterpret_cast<f32x4 *>(blk + WL::UC + ((size_t)(a * NCT + nt) * 64 + lane) * 16));
+            store_ws(wr, (int)WL::UC + ((a * NCT + nt) * 64 + lane) * 16, au[a]);
 #pragma unroll
             for (int e = 0; e < 4; e++) sX[(SB * a + 4 * kg + e) * PD + n0 + m] = aw[a][e];
         }
@@ -485,7 +506,7 @@ __device__ __forceinline__ void p1_item(float *lds, const float (&vreg)[2][8], c
         const int fb = f >> 6, rt = fb / KSI, ks = fb % KSI;
         float x[8];
         lds8(x, &sX[(SB * rt + m) * PD + 32 * ks + 8 * kg]);
-        store_frag(blk + WL::WF + (size_t)fb * 2048, lane, x);
+        store_frag(wr, (int)WL::WF + fb * 2048, lane, x);
     }
 
     hook(6);

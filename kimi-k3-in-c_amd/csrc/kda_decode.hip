@@ -31,10 +31,13 @@
 
 namespace k3kda {
 
-// One 16-byte state store with the system-scope non-temporal policy (through to memory).
-__device__ __forceinline__ void store_stream(f4 *p, const f4 &v)
+// One 16-byte state store, `off` bytes into the state, with the system-scope non-temporal
+// policy (aux 19 = sc0 | nt | sc1: through to memory): a buffer store the compiler sees as
+// one, so the wait states before a VALU overwrite of its data registers are its own.
+__device__ __forceinline__ void store_stream(__amdgpu_buffer_rsrc_t r, int off, const f4 &v)
 {
-    asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1 nt" ::"v"(p), "v"(v) : "memory");
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, 19);
 }
 
 template <int D, int NT>
@@ -66,6 +69,7 @@ __global__ __launch_bounds__(NT) void kda_decode_kernel(
     }
     // sequence pair / H's state starts s_stride floats after the previous one's
     f4 *Sp = reinterpret_cast<f4 *>(S + (size_t)(pair / H) * s_stride + (size_t)(pair % H) * D * D);
+    const __amdgpu_buffer_rsrc_t Sr = __builtin_amdgcn_make_buffer_rsrc(Sp, (short)0, D * D * 4, 0x00020000);
     f4 s[NPASS];
 #pragma unroll
     for (int m = 0; m < NPASS; m++) s[m] = __builtin_nontemporal_load(&Sp[(rs + m * RPP) * CPR + cg]);
@@ -101,7 +105,7 @@ __global__ __launch_bounds__(NT) void kda_decode_kernel(
         const float kr = s_k[r], qr = s_q[r];
         if (kr != 0.0f) s[m] = s[m] + (kr * b) * d;
         if (qr != 0.0f) acc = acc + qr * s[m];
-        store_stream(&Sp[(rs + m * RPP) * CPR + cg], s[m]);
+        store_stream(Sr, ((rs + m * RPP) * CPR + cg) * 16, s[m]);
     }
     s_red[rs][cg] = acc;   // every read of s_red above finished before the last barrier
     __syncthreads();

@@ -76,9 +76,10 @@ __global__ __launch_bounds__(256) void kda_epilogue2_kernel(long rows, int H, fl
     constexpr int LPR = D / 4, RPW = 64 / LPR;
     const int lane = threadIdx.x & 63, sub = lane / LPR, cl = lane % LPR;
     const f4 w = reinterpret_cast<const f4 *>(wn)[cl];
-    const long nw = (long)gridDim.x * (blockDim.x >> 6) * RPW;
-    for (long r0 = ((long)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * RPW; r0 < rows; r0 += nw) {
-        const long r = r0 + sub;
+    const long rpb = (long)(blockDim.x >> 6) * RPW, nw = (long)gridDim.x * rpb;
+    // rb, the block's first row, is uniform (the base of the bf16 y stores' buffer resource)
+    for (long rb = (long)blockIdx.x * rpb; rb < rows; rb += nw) {
+        const long r = rb + (long)(threadIdx.x >> 6) * RPW + sub;
         const bool live = r < rows;
         const size_t base = (size_t)(live ? r : rows - 1) * D + 4 * cl;
         const f4 x = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(o + base));   // read once: streamed
@@ -130,9 +131,15 @@ __global__ __launch_bounds__(256) void kda_epilogue2_kernel(long rows, int H, fl
             } else if constexpr (YDT == K3HIP_BF16) {
                 const uint2 u = {(uint32_t)f2bf(v.x) | ((uint32_t)f2bf(v.y) << 16),
                                  (uint32_t)f2bf(v.z) | ((uint32_t)f2bf(v.w) << 16)};
-                // y is not read again by this step: streamed out past the caches (T=8192, H=32 prefill core: -1%)
+                // y is not read again by this step: streamed out past the caches with the
+                // system-scope non-temporal policy (aux 19 = sc0 | nt | sc1: through to memory,
+                // kept in no cache; T=8192, H=32 prefill core: -1% with the compiler's
+                // nontemporal store, then 0.5340 -> 0.5325 ms per core step with this one),
+                // as a buffer store from the block's first row
                 typedef unsigned int u32x2s __attribute__((ext_vector_type(2)));
-                __builtin_nontemporal_store(u32x2s{u.x, u.y}, reinterpret_cast<u32x2s *>(reinterpret_cast<uint16_t *>(y) + base));
+                const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(
+                    reinterpret_cast<uint16_t *>(y) + (size_t)rb * D, (short)0, (int)(rpb * D * 2), 0x00020000);
+                __builtin_amdgcn_raw_buffer_store_b64(u32x2s{u.x, u.y}, yr, (int)((size_t)(r - rb) * D + 4 * cl) * 2, 0, 19);
             } else {
                 *reinterpret_cast<f4 *>(reinterpret_cast<float *>(y) + base) = v;
             }
