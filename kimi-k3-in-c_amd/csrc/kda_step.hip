@@ -92,8 +92,8 @@ __global__ __launch_bounds__(4 * D) void kda_layer_step_kernel(const StepArgs a)
     constexpr int TPT = (4 + HWS - 1) / HWS;    // K1 tasks per half-wave
 
     __shared__ float s_q[D], s_k[D], s_v[D], s_a[D], s_z[D];
-    __shared__ f4 s_red[RPP][CPR];
-    __shared__ f4 s_u[CPR];
+    __shared__ f4 s_upart[RPP][CPR];   // per row slot: partial u = S^T k, then partial o = S^T q
+    __shared__ f4 s_opart[RPP][CPR];
     __shared__ float s_beta;
 
     const int H = a.H;
@@ -264,16 +264,16 @@ __global__ __launch_bounds__(4 * D) void kda_layer_step_kernel(const StepArgs a)
         s[m] = s[m] * s_a[r];
         if (kr != 0.0f) u = u + kr * s[m];
     }
-    s_red[rs][cg] = u;
+    // every thread adds its column group's RPP partials itself, in row-slot order (the same
+    // bits as one reducing thread per group; no second barrier and no LDS round trip of u:
+    // B=1, H=32 decode tail 5.59 -> 5.42 us per token); o's partials go to their own array,
+    // so no barrier separates these reads from its writes
+    s_upart[rs][cg] = u;
     __syncthreads();
-    if (tid < CPR) {
-        f4 t = s_red[0][tid];
+    f4 ut = s_upart[0][cg];
 #pragma unroll
-        for (int r = 1; r < RPP; r++) t = t + s_red[r][tid];
-        s_u[tid] = t;
-    }
-    __syncthreads();
-    const f4 d = vv - s_u[cg];
+    for (int r = 1; r < RPP; r++) ut = ut + s_upart[r][cg];
+    const f4 d = vv - ut;
     f4 acc = 0.0f;
 #pragma unroll
     for (int m = 0; m < NPASS; m++) {
@@ -282,7 +282,7 @@ __global__ __launch_bounds__(4 * D) void kda_layer_step_kernel(const StepArgs a)
         if (kr != 0.0f) s[m] = s[m] + (kr * bt) * d;
         if (qr != 0.0f) acc = acc + qr * s[m];
     }
-    s_red[rs][cg] = acc;   // every read of s_red above finished before the last barrier
+    s_opart[rs][cg] = acc;
     if constexpr (!ZIN) k4_operands();
     __syncthreads();
 
@@ -290,9 +290,9 @@ __global__ __launch_bounds__(4 * D) void kda_layer_step_kernel(const StepArgs a)
     // first half-wave; the other waves store their part of the new state meanwhile (the
     // state stores, 4 D^2 bytes through one CU, take longer than K4)
     if (tid < 32) {
-        f4 x = s_red[0][tid < CPR ? tid : 0];
+        f4 x = s_opart[0][tid < CPR ? tid : 0];
 #pragma unroll
-        for (int r = 1; r < RPP; r++) x = x + s_red[r][tid < CPR ? tid : 0];
+        for (int r = 1; r < RPP; r++) x = x + s_opart[r][tid < CPR ? tid : 0];
         const float part = tid < CPR ? ((x.x * x.x) + (x.y * x.y)) + ((x.z * x.z) + (x.w * x.w)) : 0.0f;
         const float inv = __builtin_amdgcn_rsqf(half_wave_sum(part) / (float)D + a.eps);
         if (tid < CPR) {
