@@ -92,8 +92,8 @@ __global__ __launch_bounds__(4 * D) void kda_layer_step_kernel(const StepArgs a)
     constexpr int TPT = (4 + HWS - 1) / HWS;    // K1 tasks per half-wave
 
     __shared__ float s_q[D], s_k[D], s_v[D], s_a[D], s_z[D];
-    __shared__ f4 s_upart[RPP][CPR];   // per row slot: partial u = S^T k, then partial o = S^T q
-    __shared__ f4 s_opart[RPP][CPR];
+    __shared__ f4 s_upart[RPP][CPR];   // per row slot and column group: partial u = S^T k
+    __shared__ f4 s_opart[RPP][CPR];   // the same for o = S^T q
     __shared__ float s_beta;
 
     const int H = a.H;
