@@ -15,8 +15,11 @@
 // latent goes to position pos and attends over 0..pos. The dense projections run on the
 // few-rows bf16 GEMM of kda_rows.hip (fp32 activations split into bf16 hi + lo in registers,
 // each weight read once for all B; q_a, kv_a and g in one pass over their concatenated
-// weights), so activations keep fp32 accuracy. The absorption (W_UK_h^T q) and the final
-// W_UV_h are bf16 GEMMs batched over heads on hi/lo row pairs (2B rows). The attention reads
+// weights), so activations keep fp32 accuracy. The absorption (W_UK_h^T q) is a bf16 MFMA
+// product per head on q's hi/lo row pairs (2B rows) against a transposed copy of W_UK made at
+// upload (mla_absorb_kernel, 5.5 us at 64 heads, B = 16, against 6.2 us for the library's
+// batched GEMM: 8.4 MB of W_UK read cold each step); the final W_UV_h is applied after the
+// attention the same way. The attention reads
 // the cache once where the shape fits the fused kernel (kda_mla_attn.hip: split-bf16 MFMA
 // scores, online softmax with the reference's scale (nope+rope)^-0.5, split-bf16 weighted
 // sum of the latents; heads <= 64, kv_lora <= 512, kv_lora + rope <= 576); other shapes take
@@ -38,6 +41,10 @@ struct k3hip_mla_weights {
     // stays row-major (bf16) for the head-batched absorb GEMMs.
     void *xin, *q_b, *kv_b, *o;
     float *q_a_norm, *kv_a_norm;
+    // W_UK_h^T per head, [H][KL][QNP] bf16 with QNP = QN rounded up to 32 (zeros past QN): the
+    // B operand of the absorb product, each lane's 8 consecutive K values one 16-byte load
+    void *ukt;
+    int QNP;
 };
 
 namespace k3kda {
@@ -64,6 +71,112 @@ struct NormJob {
     const float *w;
     float *y, *cache;
 };
+// ukt[h][n][k] = W_UK_h[k][n] for k < QN, 0 for QN <= k < QNP; W_UK_h is rows 0..QN-1 of
+// head h's (QN + VH) x KL block of kv_b.
+__global__ void mla_ukt_kernel(const uint16_t *__restrict__ kvb, uint16_t *__restrict__ ukt, int H, int QN,
+                               int VH, int KL, int QNP)
+{
+    const size_t n = (size_t)H * KL * QNP;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const int k = (int)(i % QNP);
+        const size_t hn = i / QNP;
+        const int c = (int)(hn % KL), h = (int)(hn / KL);
+        ukt[i] = k < QN ? kvb[((size_t)h * (QN + VH) + k) * KL + c] : (uint16_t)0;
+    }
+}
+
+// The absorb product A2[r][h][c] = sum_k x[r][h QH + k] W_UK_h[k][c] for the M = 2B rows of
+// x (q's bf16 hi rows, then its lo rows; row stride ldx) and every head h: one 16 x 16 x 32
+// bf16 MFMA tile chain per wave (16 latent columns of one head, the M rows in tiles of 16,
+// K-steps of 32 in order), fp32 results at A2 + r ldc + h CW + c. Workgroup (x, h) takes
+// columns 64 x .. 64 x + 63 of head h. VEC: x's rows and head offsets are 16-byte aligned
+// and QN is a multiple of 8 (QH, QN and ldx multiples of 8), so each lane's 8 K values are
+// one load or none. KS = QNP / 32 K-steps, a template constant so that a tile's loads are
+// issued together and waited for once (with a run-time count each load waited alone: 5.9 us).
+typedef __bf16 mla_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float mla_f32x4 __attribute__((ext_vector_type(4)));
+template <bool VEC, int KS>
+__global__ __launch_bounds__(256) void mla_absorb_kernel(int M, int QH, int QN, int KL, int CW,
+                                                         const uint16_t *__restrict__ x, long ldx,
+                                                         const uint16_t *__restrict__ ukt, float *__restrict__ A2,
+                                                         long ldc)
+{
+    constexpr int QNP = 32 * KS;
+    const int h = blockIdx.y, lane = threadIdx.x & 63;
+    const int n0 = 64 * blockIdx.x + 16 * (threadIdx.x >> 6);
+    if (n0 >= KL) return;   // wave-uniform; no barrier in this kernel
+    const int col = n0 + (lane & 15), kq = 8 * (lane >> 4);
+    const bool cok = col < KL;
+    const uint16_t *brow = ukt + ((size_t)h * KL + (cok ? col : 0)) * QNP + kq;
+    mla_bf16x8 bf[KS];
+#pragma unroll
+    for (int t = 0; t < KS; t++) bf[t] = *reinterpret_cast<const mla_bf16x8 *>(brow + 32 * t);
+    for (int m0 = 0; m0 < M; m0 += 16) {
+        const int r = m0 + (lane & 15);
+        const uint16_t *xr = x + (size_t)(r < M ? r : 0) * ldx + (size_t)h * QH + kq;
+        mla_bf16x8 af[KS];
+#pragma unroll
+        for (int t = 0; t < KS; t++) {
+            mla_bf16x8 a;
+            if constexpr (VEC) {
+                // QN % 8 == 0: an 8-value group is wholly inside or past QN; a group past it (or
+                // a row past M) loads the head's first group instead and is zeroed, so every
+                // load is issued unconditionally from an address inside the row
+                const bool ok = r < M && 32 * t + kq < QN;
+                const mla_bf16x8 v = *reinterpret_cast<const mla_bf16x8 *>(xr + (ok ? 32 * t : -kq));
+                a = ok ? v : mla_bf16x8{};
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const int k = 32 * t + kq + e;
+                    a[e] = __builtin_bit_cast(__bf16, r < M && k < QN ? xr[32 * t + e] : (uint16_t)0);
+                }
+            }
+            af[t] = a;
+        }
+        mla_f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int t = 0; t < KS; t++) c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t], bf[t], c, 0, 0, 0);
+        // C layout: lane l holds rows 4 (l / 16) + i of the tile, column l % 16
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int rr = m0 + 4 * (lane >> 4) + i;
+            if (rr < M && cok) A2[(size_t)rr * ldc + (size_t)h * CW + col] = c[i];
+        }
+    }
+}
+
+template <bool VEC>
+static int mla_absorb_v(int M, int H, int QH, int QN, int QNP, int KL, int CW, const uint16_t *x, long ldx,
+                        const uint16_t *ukt, float *A2, long ldc, hipStream_t st)
+{
+    const dim3 grid((unsigned)((KL + 63) / 64), (unsigned)H);
+#define K3_ABS(KS) hipLaunchKernelGGL((mla_absorb_kernel<VEC, KS>), grid, dim3(256), 0, st, M, QH, QN, KL, CW, x, ldx, ukt, A2, ldc)
+    switch (QNP / 32) {
+    case 1: K3_ABS(1); break;
+    case 2: K3_ABS(2); break;
+    case 3: K3_ABS(3); break;
+    case 4: K3_ABS(4); break;
+    case 5: K3_ABS(5); break;
+    case 6: K3_ABS(6); break;
+    case 7: K3_ABS(7); break;
+    case 8: K3_ABS(8); break;
+    default: K3_FAIL(K3HIP_EUNSUPPORTED, "mla absorb: qk_nope padded to %d above 256", QNP);
+    }
+#undef K3_ABS
+    K3_LAUNCHED();
+    return K3HIP_OK;
+}
+
+// A2 = per head h, x (M rows, columns h QH .. h QH + QN - 1) . W_UK_h, via mla_absorb_kernel.
+static int mla_absorb(int M, int H, int QH, int QN, int QNP, int KL, int CW, const uint16_t *x, long ldx,
+                      const uint16_t *ukt, float *A2, long ldc, hipStream_t st)
+{
+    if (QH % 8 == 0 && QN % 8 == 0 && ldx % 8 == 0 && ((uintptr_t)x & 15) == 0)
+        return mla_absorb_v<true>(M, H, QH, QN, QNP, KL, CW, x, ldx, ukt, A2, ldc, st);
+    return mla_absorb_v<false>(M, H, QH, QN, QNP, KL, CW, x, ldx, ukt, A2, ldc, st);
+}
+
 __global__ void mla_norm_kernel(long ldc, float eps, NormJob j0, NormJob j1, long cap, int pos)
 {
     __shared__ double red[16];
@@ -196,7 +309,7 @@ extern "C" int k3hip_mla_release(k3hip_mla_weights *w)
 {
     clear_error();
     if (!w) return K3HIP_OK;
-    void *ptrs[] = {w->xin, w->q_b, w->kv_b, w->o, w->q_a_norm, w->kv_a_norm};
+    void *ptrs[] = {w->xin, w->q_b, w->kv_b, w->o, w->q_a_norm, w->kv_a_norm, w->ukt};
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
     free(w);
@@ -258,6 +371,28 @@ extern "C" int k3hip_mla_upload(const K3MlaW *w, const K3Cfg *c, k3hip_mla_weigh
             (void)hipGetLastError();
             k3hip_mla_release(d);
             K3_FAIL(K3HIP_ENOMEM, "k3hip_mla_upload: device copy of %zu bytes", u.bytes);
+        }
+    }
+    // W_UK^T per head for the absorb product
+    d->QNP = (d->QN + 31) / 32 * 32;
+    if (d->QNP > 256) {
+        k3hip_mla_release(d);
+        K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_mla_upload: qk_nope=%d above 256", c->qk_nope);
+    }
+    {
+        const size_t n = H * d->KL * d->QNP;
+        if (hipMalloc(&d->ukt, n * 2) != hipSuccess) {
+            (void)hipGetLastError();
+            d->ukt = nullptr;
+            k3hip_mla_release(d);
+            K3_FAIL(K3HIP_ENOMEM, "k3hip_mla_upload: device allocation");
+        }
+        hipLaunchKernelGGL(mla_ukt_kernel, dim3((unsigned)std::min<size_t>((n + 255) / 256, 65536)), dim3(256), 0,
+                           nullptr, (const uint16_t *)d->kv_b, (uint16_t *)d->ukt, (int)H, d->QN, d->VH, d->KL, d->QNP);
+        if (hipGetLastError() != hipSuccess || hipStreamSynchronize(nullptr) != hipSuccess) {
+            (void)hipGetLastError();
+            k3hip_mla_release(d);
+            K3_FAIL(K3HIP_EHIP, "k3hip_mla_upload: W_UK transpose failed");
         }
     }
     // xin, q_b and o into MFMA fragment order (the row-major uploads are only the source)
@@ -356,12 +491,10 @@ extern "C" int k3hip_mla_decode(const k3hip_mla_weights *w, int B, int pos, int 
         rc = gemm_rows_hl(B, H * QH, QL, qn, QL, (const uint16_t *)w->q_b, q, (long)H * QH, qs2, (long)H * QH, st, ws,
                           wsf);
     if (rc) return rc;
-    // absorb: per head h, [q hi; lo] (2B x QN) . W_UK_h (QN x KL), batched over heads
-    GemmDesc ga;
-    ga.M = 2 * B; ga.N = KL; ga.K = QN; ga.ab_dtype = K3HIP_BF16; ga.c_dtype = K3HIP_F32; ga.b_trans = false;
-    ga.lda = (long)H * QH; ga.ldb = KL; ga.ldc = (long)H * CW; ga.batch = H;
-    ga.sa = QH; ga.sb = (long)(QN + VH) * KL; ga.sc = CW;
-    if ((rc = gemm(ga, qs2, kvb, A2, st))) return rc;
+    // absorb: per head h, [q hi; lo] (2B x QN) . W_UK_h (QN x KL)
+    if ((rc = mla_absorb(2 * B, H, QH, QN, w->QNP, KL, CW, qs2, (long)H * QH, (const uint16_t *)w->ukt, A2,
+                         (long)H * CW, st)))
+        return rc;
     // o_proj as two K-ranges adds into `out`, zeroed by the kernel before it (no reduction
     // launch); atomics on ordinary device memory only
     const bool oz = gemm_rows_splits(E, HV) == 2 && coarse_device_mem(out);
