@@ -43,7 +43,7 @@ struct k3hip_mla_weights {
     float *q_a_norm, *kv_a_norm;
     // W_UK_h^T per head, [H][KL][QNP] bf16 with QNP = QN rounded up to 32 (zeros past QN): the
     // B operand of the absorb product, each lane's 8 consecutive K values one 16-byte load
-    void *ukt;
+    void *ukt;   // nullptr when qk_nope > 256
     int QNP;
 };
 
@@ -373,13 +373,10 @@ extern "C" int k3hip_mla_upload(const K3MlaW *w, const K3Cfg *c, k3hip_mla_weigh
             K3_FAIL(K3HIP_ENOMEM, "k3hip_mla_upload: device copy of %zu bytes", u.bytes);
         }
     }
-    // W_UK^T per head for the absorb product
+    // W_UK^T per head for the absorb kernel (qk_nope <= 256; wider heads keep the batched
+    // library GEMM on kv_b itself)
     d->QNP = (d->QN + 31) / 32 * 32;
-    if (d->QNP > 256) {
-        k3hip_mla_release(d);
-        K3_FAIL(K3HIP_EUNSUPPORTED, "k3hip_mla_upload: qk_nope=%d above 256", c->qk_nope);
-    }
-    {
+    if (d->QNP <= 256) {
         const size_t n = H * d->KL * d->QNP;
         if (hipMalloc(&d->ukt, n * 2) != hipSuccess) {
             (void)hipGetLastError();
@@ -492,9 +489,17 @@ extern "C" int k3hip_mla_decode(const k3hip_mla_weights *w, int B, int pos, int 
                           wsf);
     if (rc) return rc;
     // absorb: per head h, [q hi; lo] (2B x QN) . W_UK_h (QN x KL)
-    if ((rc = mla_absorb(2 * B, H, QH, QN, w->QNP, KL, CW, qs2, (long)H * QH, (const uint16_t *)w->ukt, A2,
-                         (long)H * CW, st)))
-        return rc;
+    if (w->ukt) {
+        if ((rc = mla_absorb(2 * B, H, QH, QN, w->QNP, KL, CW, qs2, (long)H * QH, (const uint16_t *)w->ukt, A2,
+                             (long)H * CW, st)))
+            return rc;
+    } else {
+        GemmDesc ga;
+        ga.M = 2 * B; ga.N = KL; ga.K = QN; ga.ab_dtype = K3HIP_BF16; ga.c_dtype = K3HIP_F32; ga.b_trans = false;
+        ga.lda = (long)H * QH; ga.ldb = KL; ga.ldc = (long)H * CW; ga.batch = H;
+        ga.sa = QH; ga.sb = (long)(QN + VH) * KL; ga.sc = CW;
+        if ((rc = gemm(ga, qs2, kvb, A2, st))) return rc;
+    }
     // o_proj as two K-ranges adds into `out`, zeroed by the kernel before it (no reduction
     // launch); atomics on ordinary device memory only
     const bool oz = gemm_rows_splits(E, HV) == 2 && coarse_device_mem(out);

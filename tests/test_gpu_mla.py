@@ -41,6 +41,7 @@ def mla_case(rng, hidden, H, ql, kvl, qn, qr, vh, gate=1):
     (128, 2, 32, 32, 16, 8, 16, 2, 40, 0),       # ungated, longer context
     (256, 64, 64, 512, 32, 64, 32, 2, 150, 1),   # the 576-channel latent + rope rows of Kimi K3
     (256, 4, 64, 64, 20, 12, 32, 3, 5, 1),       # nope not a multiple of 8: the absorb's element loads
+    (128, 2, 32, 32, 264, 8, 16, 2, 3, 1),       # nope above 256: the absorb on the batched library GEMM
 ])
 def test_mla_decode_vs_expanded_oracle(gpu, hidden, H, ql, kvl, qn, qr, vh, B, T, gate):
     _mla_decode_vs_oracle(gpu, hidden, H, ql, kvl, qn, qr, vh, B, T, gate, 0x4B334441 + 4 + hidden + B + T)
