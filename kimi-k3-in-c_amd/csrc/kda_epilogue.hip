@@ -147,11 +147,73 @@ __global__ __launch_bounds__(256) void kda_epilogue2_kernel(long rows, int H, fl
     }
 }
 
+
+// bf16 gate -> bf16 y (the prefill core's form) with 8 channels per lane: o as two float4
+// loads, the gate and y as one 16-byte access each (the general kernel above takes 4 channels
+// per lane, 8-byte gate and y accesses: T=8192, H=32 core step 0.536-0.538 -> 0.532-0.533 ms).
+// The same arithmetic, except that a lane's fp32 sum of squares covers its 8 values.
+template <int D>
+__global__ __launch_bounds__(256) void kda_epilogue8_kernel(long rows, float eps, const float *__restrict__ o,
+                                                            const uint16_t *__restrict__ gate,
+                                                            const float *__restrict__ wn, uint16_t *__restrict__ y)
+{
+#pragma clang fp contract(off)
+    constexpr int LPR = D / 8, RPW = 64 / LPR;
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    const int lane = threadIdx.x & 63, sub = lane / LPR, cl = lane % LPR;
+    const f4 w0 = reinterpret_cast<const f4 *>(wn)[2 * cl], w1 = reinterpret_cast<const f4 *>(wn)[2 * cl + 1];
+    const long rpb = (long)(blockDim.x >> 6) * RPW, nw = (long)gridDim.x * rpb;
+    for (long rb = (long)blockIdx.x * rpb; rb < rows; rb += nw) {
+        const long r = rb + (long)(threadIdx.x >> 6) * RPW + sub;
+        const bool live = r < rows;
+        const size_t base = (size_t)(live ? r : rows - 1) * D + 8 * cl;
+        const f4 x0 = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(o + base));
+        const f4 x1 = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(o + base + 4));
+        const u32x4 gu = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(gate + base));
+        float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        float g[8];
+#pragma unroll
+        for (int e = 0; e < 4; e++) { g[2 * e] = __uint_as_float(gu[e] << 16); g[2 * e + 1] = __uint_as_float(gu[e] & 0xffff0000u); }
+        double ss = (double)((((x[0] * x[0]) + (x[1] * x[1])) + ((x[2] * x[2]) + (x[3] * x[3]))) +
+                             (((x[4] * x[4]) + (x[5] * x[5])) + ((x[6] * x[6]) + (x[7] * x[7]))));
+#pragma unroll
+        for (int m = LPR / 2; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+        const float inv = (float)(1.0 / sqrt(ss / (double)D + (double)eps));
+        uint32_t pk[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            float v2[2];
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const int i = 2 * e + t;
+                const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g[i] * 1.4426950408889634f));
+                v2[t] = ((wv[i] * x[i]) * inv) * sg;
+            }
+            pk[e] = (uint32_t)f2bf(v2[0]) | ((uint32_t)f2bf(v2[1]) << 16);
+        }
+        if (live) {
+            const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(y + (size_t)rb * D, (short)0, (int)(rpb * D * 2), 0x00020000);
+            __builtin_amdgcn_raw_buffer_store_b128(u32x4{pk[0], pk[1], pk[2], pk[3]}, yr, (int)((size_t)(r - rb) * D + 8 * cl) * 2, 0, 19);
+        }
+    }
+}
+
 template <int D, int GDT, int YDT>
 static int launch_epi(long rows, int H, float eps, const float *o, const void *g,
                       const float *wn, void *y, hipStream_t st)
 {
     const bool wide = D >= 64 && ((uintptr_t)o | (uintptr_t)g | (uintptr_t)y | (uintptr_t)wn) % 16 == 0;
+    if constexpr (D >= 64 && GDT == K3HIP_BF16 && YDT == K3HIP_BF16) {
+        if (wide) {
+            long blocks = (rows + 4 * (512 / D) - 1) / (4 * (512 / D));
+            if (blocks > 16384) blocks = 16384;
+            hipLaunchKernelGGL((kda_epilogue8_kernel<D>), dim3((unsigned)blocks), dim3(256), 0, st, rows, eps, o,
+                               (const uint16_t *)g, wn, (uint16_t *)y);
+            K3_LAUNCHED();
+            return K3HIP_OK;
+        }
+    }
     if (wide) {
         long blocks = (rows + 4 * (256 / D) - 1) / (4 * (256 / D));
         if (blocks > 16384) blocks = 16384;

@@ -200,7 +200,7 @@ def test_recurrent_bitwise_vs_oracle(gpu, T, H, D):
     assert np.array_equal(host(dS).view(np.uint32), Sref.view(np.uint32))
 
 
-@pytest.mark.parametrize("T,H,D", [(1, 1, 16), (5, 3, 64), (77, 4, 128)])
+@pytest.mark.parametrize("T,H,D", [(1, 1, 16), (5, 3, 64), (77, 4, 128), (3, 5, 64), (1037, 2, 128)])
 def test_epilogue_vs_oracle(gpu, T, H, D):
     import torch
     rng = np.random.default_rng(T * 7 + D)
@@ -224,6 +224,21 @@ def test_epilogue_vs_oracle(gpu, T, H, D):
     gpu.kda_epilogue(dev(o), dev(gate), dev(wn), yb, H, D, 1e-5)
     torch.cuda.synchronize()
     assert_close(host(yb), want, 1e-6, 2 ** -8, "epilogue bf16 out")
+    # bf16 gate -> bf16 y (the prefill core's form, its own kernel for D >= 64): the oracle on
+    # the bf16-rounded gate
+    gb = torch.from_numpy(gate).to(torch.bfloat16)
+    gr = gb.float().numpy()
+    want_b = np.zeros((T, P), np.float32)
+    for t in range(T):
+        for h in range(H):
+            row = np.ascontiguousarray(o[t, h * D:(h + 1) * D])
+            yy = np.zeros(D, np.float32)
+            L.orc_rmsnorm(ko.ptr(yy), ko.ptr(row), ko.ptr(wn), D, 1e-5)
+            want_b[t, h * D:(h + 1) * D] = yy * np.array([L.orc_sigmoid(float(x)) for x in gr[t, h * D:(h + 1) * D]], np.float32)
+    ybb = torch.zeros((T, P), device="cuda", dtype=torch.bfloat16)
+    gpu.kda_epilogue(dev(o), gb.cuda(), dev(wn), ybb, H, D, 1e-5)
+    torch.cuda.synchronize()
+    assert_close(host(ybb), want_b, 1e-6, 2 ** -8, "epilogue bf16 gate, bf16 out")
 
 
 @pytest.mark.parametrize("fname", ["kda_layer1", "kda_layer8"])
